@@ -1,0 +1,278 @@
+"""Benchmark of the scaled-FP8 paged KV hot path on one MI355X.
+
+Headline (BASELINE.json metric): paged-decode achieved HBM GB/s (and % of the
+8 TB/s peak) plus us/layer on the batch-64 mixed-context workload
+(``decode_mixed``: 64 sequences, lengths U[1k, 16k], 32 of them sharing one
+4096-token prefix, 32 q / 8 kv heads, head_dim 128, 256-token scaled-FP8
+pages).  A step is one layer's decode over the batch (split-K kernel +
+combine).  Steps rotate over ``--layers`` independent KV pools so that each
+step reads its pages cold from HBM (the 256 MB MALL cannot hold a layer).
+
+``value`` = algorithmic bytes / time per step, where algorithmic bytes count
+every distinct (page, used row) once (2112 B per token per layer for K+V
+payload and scales; shared-prefix rows once) plus q, out, block tables and
+context lengths.  ``roofline.achieved`` uses the same bytes over the split-K
+kernel's own average duration, measured with HIP events on the stream it is
+launched on.  ``cpu_baseline`` times the CPU restatement of the reference's
+decode path (per-sequence page gather, bf16 dequant, GQA expand, SDPA) on a
+bounded sample of the same workload's sequences.
+
+    python bench.py [--gpus 1] [--steps 50] [--warmup 10]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO_ROOT = Path(__file__).resolve().parent
+for _p in (REPO_ROOT, REPO_ROOT / "prism-infer_amd"):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+METRIC = "paged-decode achieved HBM GB/s (% of peak) + µs/layer, batch 64 mixed ctx"
+HBM_PEAK_GBPS = 8000.0
+TRAFFIC_FILE = REPO_ROOT / "profiles" / "decode_mixed_traffic.json"
+
+
+def _log(msg: str) -> None:
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def _time_loop(fn, steps: int, torch) -> float:
+    """Seconds per call of ``fn`` over ``steps`` calls, HIP events on the current stream."""
+
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start.record()
+    for i in range(steps):
+        fn(i)
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / 1e3 / steps
+
+
+def _cpu_baseline(w, budget_s: float, torch) -> dict:
+    """Time the CPU restatement of the reference decode path on a bounded sample."""
+
+    import oracle  # noqa: PLC0415  (checker/baseline only)
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    tables = w.block_tables.cpu()
+    lens = w.context_lens.cpu()
+    done_bytes = 0
+    seqs = 0
+    elapsed = 0.0
+    per_token = 2 * 8 * 128 + 2 * 8 * 4
+    for b in range(w.batch):
+        n = int(lens[b])
+        pages = tables[b][: (n + 255) // 256].long()
+        idx = pages.to(w.k_cache.device)
+        k = w.k_cache.view(torch.uint8).index_select(0, idx).cpu().view(torch.float8_e4m3fn)
+        v = w.v_cache.view(torch.uint8).index_select(0, idx).cpu().view(torch.float8_e4m3fn)
+        ks = w.k_scale.index_select(0, idx).cpu()
+        vs = w.v_scale.index_select(0, idx).cpu()
+        local = torch.arange(pages.numel(), dtype=torch.int32).reshape(1, -1)
+        q = w.q[b:b + 1].cpu()
+        t0 = time.perf_counter()
+        oracle.decode_reference_qdtype(q, k, v, local, lens[b:b + 1], w.scale, k_scale_cache=ks, v_scale_cache=vs)
+        elapsed += time.perf_counter() - t0
+        done_bytes += n * per_token + 2 * q.numel() * 2 + local.numel() * 4 + 4
+        seqs += 1
+        if elapsed >= budget_s:
+            break
+    return {
+        "value": round(done_bytes / elapsed / 1e9, 4),
+        "unit": "GB/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"first {seqs} of {w.batch} decode_mixed sequences, reference CPU path "
+                  f"(page gather + bf16 dequant + GQA expand + SDPA), {elapsed:.1f} s",
+        "us_per_layer_equiv": round(elapsed / seqs * w.batch * 1e6, 1),
+    }
+
+
+def main() -> int:
+    parser = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=50)
+    parser.add_argument("--warmup", type=int, default=10)
+    parser.add_argument("--layers", type=int, default=4, help="independent KV pools the steps rotate over")
+    parser.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-extras", action="store_true", help="skip store/compaction/single-sequence extras")
+    args = parser.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU only: the KV hot path needs no collective and this build "
+              "runs no multi-GPU configuration (use --gpus 1).", file=sys.stderr)
+        return 2
+
+    import torch  # noqa: PLC0415
+
+    from prism_infer import _native, workloads  # noqa: PLC0415
+    from prism_infer.ops.paged_decode import (  # noqa: PLC0415
+        _launch_paged_decode_attention,
+        decode_workspace_bytes,
+    )
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        return 1
+    _native.lib()
+    dev = torch.device("cuda", 0)
+    torch.cuda.set_device(dev)
+
+    # ---- headline workload: decode_mixed, one pool per rotated layer
+    _log(f"building decode_mixed x {args.layers} layers")
+    layers = []
+    base = workloads.decode_mixed(dev)
+    layers.append(base)
+    for layer in range(1, args.layers):
+        k, v, ks, vs = (torch.empty_like(t) for t in (base.k_cache, base.v_cache, base.k_scale, base.v_scale))
+        workloads.fill_pages(k, v, ks, vs, base.used_pages, 1000 + layer)
+        layers.append(type(base)(**{**base.__dict__, "k_cache": k, "v_cache": v, "k_scale": ks, "v_scale": vs}))
+    torch.cuda.synchronize()
+    alg_bytes = base.algorithmic_bytes()
+    ws = torch.empty(max(decode_workspace_bytes(base.q, base.k_cache, base.block_tables), 1),
+                     dtype=torch.uint8, device=dev)
+    outs = [torch.empty_like(base.q) for _ in layers]
+
+    def step(i: int, stage: int = 0):
+        w = layers[i % len(layers)]
+        _launch_paged_decode_attention(
+            w.q, w.k_cache, w.v_cache, w.block_tables, w.context_lens, w.scale, w.max_context_len,
+            k_scale_cache=w.k_scale, v_scale_cache=w.v_scale, scaled_kv=True, stage=stage,
+            output=outs[i % len(layers)], workspace=ws)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    _log(f"timing {args.steps} steps")
+    sec_per_step = _time_loop(step, args.steps, torch)
+    # dominant kernel alone (split-K partial kernel), same stream, same rotation
+    for i in range(args.warmup):
+        step(i, 1)
+    kernel_s = _time_loop(lambda i: step(i, 1), args.steps, torch)
+    combine_s = _time_loop(lambda i: step(i, 2), args.steps, torch)
+
+    value = alg_bytes / sec_per_step / 1e9
+    achieved = alg_bytes / kernel_s / 1e9
+    traffic = None
+    if TRAFFIC_FILE.exists():
+        try:
+            traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
+        except (ValueError, OSError):
+            traffic = None
+    split = _native.lib().prism_paged_decode_split_tokens(64, 32, 8, 128, 256, base.block_tables.shape[1], 3)
+    result = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(sec_per_step * 1e3, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "decode_mixed: batch 64, context U[1024,16384] (seeded), 32 sequences share a "
+                        "4096-token prefix (16 pages), 32q/8kv heads, head_dim 128, 256-token scaled-FP8 "
+                        "pages in an 8192-page pool; one step = one layer's decode",
+            "batch": base.batch,
+            "context_lens_sum": int(base.context_lens.sum().item()),
+            "unique_kv_tokens": base.unique_kv_tokens(),
+            "algorithmic_bytes_per_step": alg_bytes,
+            "layers_rotated": len(layers),
+            "split_tokens": int(split),
+        },
+        "us_per_layer": round(sec_per_step * 1e6, 2),
+        "pct_of_hbm_peak": round(100.0 * value / HBM_PEAK_GBPS, 2),
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 2),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": traffic,
+            "kernel": "paged_decode_split_kernel",
+            "kernel_us": round(kernel_s * 1e6, 2),
+            "combine_us": round(combine_s * 1e6, 2),
+        },
+    }
+
+    if not args.no_extras:
+        result["extras"] = _extras(torch, dev, workloads)
+    del layers, outs, ws
+    torch.cuda.empty_cache()
+
+    if not args.no_cpu_baseline:
+        _log("cpu baseline")
+        result["cpu_baseline"] = _cpu_baseline(base, args.cpu_budget, torch)
+    else:
+        result["cpu_baseline"] = None
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+def _extras(torch, dev, workloads) -> dict:
+    """Store (prefill chunk), compaction and single-sequence decode timings."""
+
+    from prism_infer.ops.kv_cache_store import store_kvcache  # noqa: PLC0415
+    from prism_infer.ops.kv_compaction import compact_kv_slots  # noqa: PLC0415
+    from prism_infer.ops.paged_decode import paged_decode_attention  # noqa: PLC0415
+
+    out = {}
+    reps = 20
+    # store: 8192 tokens into a 512-page pool
+    sw = workloads.store_prefill(dev)
+    kc = torch.empty(sw.num_pages, 256, 8, 128, dtype=torch.float8_e4m3fn, device=dev)
+    vc = torch.empty_like(kc)
+    ks = torch.empty(sw.num_pages, 256, 8, dtype=torch.float32, device=dev)
+    vs = torch.empty_like(ks)
+    run = lambda i: store_kvcache(sw.key, sw.value, kc, vc, sw.slot_mapping, ks, vs)
+    run(0)
+    s = _time_loop(run, reps, torch)
+    out["store_prefill"] = {"us": round(s * 1e6, 2), "GBps": round(sw.algorithmic_bytes() / s / 1e9, 1),
+                            "bytes": sw.algorithmic_bytes()}
+    del kc, vc, ks, vs
+    # compaction: 64 x 8192-token prefixes, ~30% dropped, out of place, payload + scales (L=1)
+    cw = workloads.compaction_plans()
+    slots = cw.num_pages * 256
+    payload = torch.zeros(2, 1, slots, 8, 128, dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
+    scales = torch.zeros(2, 1, slots, 8, dtype=torch.float32, device=dev)
+    src = torch.tensor([x for p in cw.plans for x in p.source_slots], dtype=torch.long, device=dev)
+    dst = torch.tensor([x for p in cw.plans for x in p.destination_slots], dtype=torch.long, device=dev)
+
+    def compact(i):
+        compact_kv_slots(payload, src, dst)
+        compact_kv_slots(scales, src, dst)
+
+    compact(0)
+    s = _time_loop(compact, reps, torch)
+    out["compaction_out_of_place"] = {"us": round(s * 1e6, 2), "GBps": round(cw.algorithmic_bytes() / s / 1e9, 1),
+                                      "bytes": cw.algorithmic_bytes(), "kept_tokens": cw.kept}
+    del payload, scales
+    # single-sequence decode (latency bound): Qwen3-VL-shaped, B=1, 1800 tokens
+    qw = workloads.decode_qwen_vl(dev)
+    run = lambda i: paged_decode_attention(qw.q, qw.k_cache, qw.v_cache, qw.block_tables, qw.context_lens, qw.scale,
+                                           k_scale_cache=qw.k_scale, v_scale_cache=qw.v_scale,
+                                           max_context_len=qw.max_context_len)
+    run(0)
+    s = _time_loop(run, 50, torch)
+    out["decode_qwen_vl_b1"] = {"us_per_layer": round(s * 1e6, 2),
+                                "GBps": round(qw.algorithmic_bytes() / s / 1e9, 1)}
+    return out
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,169 @@
+/*
+ * prism_kv.h -- C ABI of libprism_mi355x.so, the MI355X (gfx950) scaled-FP8
+ * paged-KV hot path.
+ *
+ * Conventions
+ *   - Every entry point returns PRISM_OK (0) on success or a negative status;
+ *     prism_last_error() then returns a thread-local message.
+ *   - Pointers are device pointers (already including storage offsets) unless
+ *     stated otherwise.  Strides are in ELEMENTS of the pointed-to type.
+ *   - `stream` is a hipStream_t passed as void*; all work is enqueued on it and
+ *     no call synchronises the host.  Nothing here allocates or frees device
+ *     memory: scratch comes in through a caller-owned `workspace`.
+ *   - Device-side metadata (slot_mapping, block tables, context lengths,
+ *     max_context_len) is read by the kernels at run time, so a call captured
+ *     into a HIP graph follows updated contents on replay.
+ *
+ * dtype codes (PRISM_DTYPE_*) name the element type of a buffer.
+ */
+#ifndef PRISM_KV_H
+#define PRISM_KV_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define PRISM_OK 0
+#define PRISM_ERR_INVALID (-1) /* contract violation (shape, dtype, size)   */
+#define PRISM_ERR_LAYOUT (-2)  /* unsupported layout / alignment / stride   */
+#define PRISM_ERR_HIP (-3)     /* a HIP runtime call failed                 */
+
+#define PRISM_DTYPE_F32 0
+#define PRISM_DTYPE_BF16 1
+#define PRISM_DTYPE_F16 2
+#define PRISM_DTYPE_FP8_E4M3FN 3
+
+/* ABI version of this header (bumped on any signature change). */
+int prism_abi_version(void);
+
+/* Message for the most recent failing call on this thread ("" if none). */
+const char* prism_last_error(void);
+
+/* Number of compute units of the current device (used for work sizing). */
+int prism_device_cu_count(void);
+
+/*
+ * KV store.  Replaces the kernels behind
+ *   store_kvcache(key, value, k_cache, v_cache, slot_mapping,
+ *                 k_scale_cache=None, v_scale_cache=None)
+ *   (prism_infer/ops/kv_cache_store.py:419-476; scaled kernel :81-167,
+ *    dense kernel :58-78, eager semantics :170-230).
+ *
+ * key/value   : [num_tokens, num_heads, head_dim] of in_dtype (F32/BF16/F16);
+ *               strides {token, head, dim}; head and dim must be dense
+ *               (stride_dim == 1, stride_head == head_dim).
+ * k/v_cache   : contiguous [num_slots, num_heads, head_dim] of cache_dtype.
+ * k/v_scale   : contiguous [num_slots, num_heads] fp32, or both NULL.
+ *               Non-NULL requires cache_dtype == FP8_E4M3FN and selects the
+ *               per-token, per-head scaled quantiser:
+ *                 s = max(amax|x| / 448, 1e-6);  q = e4m3fn(clamp(x / s, +-448))
+ *               NULL with an FP8 cache stores a unit-scale RNE cast; NULL with
+ *               a F32/BF16/F16 cache stores a plain cast.
+ * slot_mapping: int32 [num_tokens]; slot < 0 (padding) and slot >= num_slots
+ *               are skipped.
+ */
+int prism_kv_store(const void* key, const void* value, int in_dtype, const int64_t key_strides[3],
+                   const int64_t value_strides[3], void* k_cache, void* v_cache, int cache_dtype,
+                   float* k_scale, float* v_scale, const int32_t* slot_mapping, int64_t num_tokens,
+                   int num_heads, int head_dim, int64_t num_slots, void* stream);
+
+/*
+ * Paged decode attention (one query token per sequence, GQA).  Replaces the
+ * kernel behind
+ *   paged_decode_attention(q, k_cache, v_cache, block_tables, context_lens,
+ *                          scale, *, k_scale_cache=None, v_scale_cache=None,
+ *                          max_context_len=None, block_n=32)
+ *   (prism_infer/ops/paged_decode.py:443-485; kernel :42-180).
+ *
+ * q          : [batch, num_heads, head_dim] of q_dtype (F32/BF16/F16), strides q_strides.
+ * k/v_cache  : [num_blocks, page_size, num_kv_heads, head_dim] of cache_dtype
+ *              (FP8_E4M3FN, or F32/BF16/F16 for unscaled caches), strides
+ *              k_strides / v_strides {block, token, head, dim}; dim stride 1.
+ * k/v_scale  : [num_blocks, page_size, num_kv_heads] fp32 or both NULL;
+ *              strides ks_strides / vs_strides.
+ * block_tables: int32 [>= batch, max_blocks_per_seq], strides bt_strides.
+ *              Block ids < 0 (and >= num_blocks) are skipped, not errors.
+ * context_lens: int32 [>= batch]; max_context_len: int32 [1].  A token t of
+ *              sequence b is attended iff t < min(context_lens[b],
+ *              *max_context_len, max_blocks_per_seq * page_size) and its block
+ *              id is valid.  A sequence with no attended token outputs zeros.
+ * out        : [batch, num_heads, head_dim] of q_dtype, strides out_strides.
+ * workspace  : device scratch of at least prism_paged_decode_workspace_bytes()
+ *              bytes for the same geometry (split-K partials); may be NULL
+ *              when that function returns 0.
+ */
+int64_t prism_paged_decode_workspace_bytes(int batch, int num_heads, int num_kv_heads, int head_dim,
+                                           int page_size, int max_blocks_per_seq, int cache_dtype);
+
+int prism_paged_decode(const void* q, int q_dtype, const int64_t q_strides[3], const void* k_cache,
+                       const void* v_cache, int cache_dtype, const int64_t k_strides[4],
+                       const int64_t v_strides[4], const float* k_scale, const float* v_scale,
+                       const int64_t ks_strides[3], const int64_t vs_strides[3],
+                       const int32_t* block_tables, const int64_t bt_strides[2],
+                       const int32_t* context_lens, const int32_t* max_context_len, void* out,
+                       const int64_t out_strides[3], int batch, int num_heads, int num_kv_heads,
+                       int head_dim, int page_size, int64_t num_blocks, int max_blocks_per_seq,
+                       float scale, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Stage selector for measurement: the same as prism_paged_decode but runs only
+ * the split-K partial kernel (stage 1) or only the combine kernel (stage 2).
+ * stage 0 runs both and is identical to prism_paged_decode.
+ */
+int prism_paged_decode_stage(int stage, const void* q, int q_dtype, const int64_t q_strides[3],
+                             const void* k_cache, const void* v_cache, int cache_dtype,
+                             const int64_t k_strides[4], const int64_t v_strides[4],
+                             const float* k_scale, const float* v_scale,
+                             const int64_t ks_strides[3], const int64_t vs_strides[3],
+                             const int32_t* block_tables, const int64_t bt_strides[2],
+                             const int32_t* context_lens, const int32_t* max_context_len,
+                             void* out, const int64_t out_strides[3], int batch, int num_heads,
+                             int num_kv_heads, int head_dim, int page_size, int64_t num_blocks,
+                             int max_blocks_per_seq, float scale, void* workspace,
+                             int64_t workspace_bytes, void* stream);
+
+/* Tokens per split-K work item chosen for a geometry (0 = no split-K path). */
+int prism_paged_decode_split_tokens(int batch, int num_heads, int num_kv_heads, int head_dim,
+                                    int page_size, int max_blocks_per_seq, int cache_dtype);
+
+/*
+ * Physical slot compaction.  Replaces the kernels behind
+ *   compact_kv_slots(cache, source_slots, destination_slots)
+ *   (prism_infer/ops/kv_compaction.py:93-112; gather/scatter kernels :33-86).
+ *
+ * cache      : contiguous [rows, num_slots, vec_bytes] bytes (a payload cache
+ *              [kv, layers, slots, heads, dim] or a scale cache
+ *              [kv, layers, slots, heads] viewed as bytes).
+ * src, dst   : int64 [retained] slot indices.  Semantics: every destination
+ *              slot receives the bytes its source slot held BEFORE the call
+ *              (all reads precede all writes), for every row.  Entries whose
+ *              source or destination is outside [0, num_slots) are skipped.
+ *              Duplicate destinations leave which source wins unspecified.
+ * workspace  : prism_compact_slots_workspace_bytes() bytes of device scratch.
+ *              The library detects on the device whether any destination
+ *              aliases a different entry's source; only then does it stage
+ *              the sources through the workspace (two passes), otherwise it
+ *              copies in one pass.
+ */
+int64_t prism_compact_slots_workspace_bytes(int64_t rows, int64_t num_slots, int64_t vec_bytes,
+                                            int64_t retained);
+
+int prism_compact_slots(void* cache, int64_t rows, int64_t num_slots, int64_t vec_bytes,
+                        const int64_t* src, const int64_t* dst, int64_t retained, void* workspace,
+                        int64_t workspace_bytes, void* stream);
+
+/*
+ * Test hook with no counterpart in the reference: converts n fp32 values to
+ * E4M3FN bytes with the exact device routine the scaled store uses (native
+ * gfx950 conversion plus the NaN rule), so the rounding can be checked
+ * exhaustively against the CPU oracle.
+ */
+int prism_debug_fp8_encode(const float* in, uint8_t* out, int64_t n, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* PRISM_KV_H */

@@ -1,0 +1,212 @@
+// Physical slot compaction: cache[row, dst[i], :] <- cache[row, src[i], :]
+// for every row, with all reads before any write (the semantics of
+// prism_infer/ops/kv_compaction.py:93-112: index_select(...).clone() then
+// index_copy_).
+//
+// The reference always stages through a temporary (two Triton passes,
+// :157-191).  Here the device decides per call whether staging is needed:
+//   1. clear a bitmap over all slots and a hazard flag (fill kernel; graph safe),
+//   2. mark every source slot in the bitmap,
+//   3. raise the flag if some entry writes a slot that is another entry's
+//      source (dst[i] marked and dst[i] != src[i]),
+//   4. copy: flag clear -> move bytes directly src -> dst (one pass);
+//            flag set   -> gather sources into the workspace,
+//   5. scatter (flag set only): workspace -> dst.
+// No host synchronisation; the flag lives in device memory.  Copies move 16
+// bytes per lane when the row width allows it, 4 or 1 bytes otherwise.
+#include "common.h"
+
+namespace prism {
+namespace {
+
+constexpr int kThreads = 256;
+
+struct CompactWorkspace {
+  uint32_t* bitmap;   // ceil(num_slots / 32) words
+  uint32_t* flag;     // [0] hazard flag
+  uint8_t* temp;      // rows * retained * vec_bytes
+};
+
+int64_t bitmap_words(int64_t num_slots) { return ceil_div(num_slots, 32); }
+
+int64_t workspace_layout(int64_t rows, int64_t num_slots, int64_t vec_bytes, int64_t retained,
+                         int64_t* flag_off, int64_t* temp_off) {
+  const int64_t bm = align_up(bitmap_words(num_slots) * 4, 256);
+  *flag_off = bm;
+  *temp_off = bm + 256;
+  return *temp_off + align_up(rows * retained * vec_bytes, 256);
+}
+
+__global__ void __launch_bounds__(kThreads) clear_words_kernel(uint32_t* __restrict__ words, int64_t n) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
+    words[i] = 0u;
+}
+
+__global__ void __launch_bounds__(kThreads)
+mark_sources_kernel(const int64_t* __restrict__ src, int64_t retained, int64_t num_slots,
+                    uint32_t* __restrict__ bitmap) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < retained;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t s = src[i];
+    if (s < 0 || s >= num_slots) continue;
+    atomicOr(&bitmap[s >> 5], 1u << (s & 31));
+  }
+}
+
+__global__ void __launch_bounds__(kThreads)
+detect_hazard_kernel(const int64_t* __restrict__ src, const int64_t* __restrict__ dst, int64_t retained,
+                     int64_t num_slots, const uint32_t* __restrict__ bitmap, uint32_t* __restrict__ flag) {
+  bool hazard = false;
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < retained;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t s = src[i];
+    const int64_t d = dst[i];
+    if (s < 0 || s >= num_slots || d < 0 || d >= num_slots || s == d) continue;
+    if ((bitmap[d >> 5] >> (d & 31)) & 1u) hazard = true;
+  }
+  if (__any(hazard) && lane_id() == 0) atomicOr(flag, 1u);
+}
+
+// Element type used for the byte moves.
+template <int BYTES>
+struct Chunk;
+template <>
+struct Chunk<16> { using T = u32x4; };
+template <>
+struct Chunk<4> { using T = uint32_t; };
+template <>
+struct Chunk<1> { using T = uint8_t; };
+
+// MODE 0: direct copy (skip when the hazard flag is set)
+// MODE 1: gather into temp (only when the flag is set)
+// MODE 2: scatter from temp (only when the flag is set)
+template <int BYTES, int MODE>
+__global__ void __launch_bounds__(kThreads)
+compact_move_kernel(uint8_t* __restrict__ cache, int64_t rows, int64_t num_slots, int64_t vec_bytes,
+                    const int64_t* __restrict__ src, const int64_t* __restrict__ dst, int64_t retained,
+                    uint8_t* __restrict__ temp, const uint32_t* __restrict__ flag) {
+  using T = typename Chunk<BYTES>::T;
+  const bool staged = *flag != 0u;
+  if ((MODE == 0) == staged) return;
+  const int64_t chunks_per_vec = vec_bytes / BYTES;
+  const int64_t total = rows * retained * chunks_per_vec;
+  for (int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; c < total;
+       c += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t item = c / chunks_per_vec;
+    const int64_t part = c - item * chunks_per_vec;
+    const int64_t row = item / retained;
+    const int64_t i = item - row * retained;
+    const int64_t s = src[i];
+    const int64_t d = dst[i];
+    if (s < 0 || s >= num_slots || d < 0 || d >= num_slots) continue;
+    const int64_t row_base = row * num_slots;
+    const T* from;
+    T* to;
+    if (MODE == 0) {
+      from = reinterpret_cast<const T*>(cache + (row_base + s) * vec_bytes) + part;
+      to = reinterpret_cast<T*>(cache + (row_base + d) * vec_bytes) + part;
+    } else if (MODE == 1) {
+      from = reinterpret_cast<const T*>(cache + (row_base + s) * vec_bytes) + part;
+      to = reinterpret_cast<T*>(temp + item * vec_bytes) + part;
+    } else {
+      from = reinterpret_cast<const T*>(temp + item * vec_bytes) + part;
+      to = reinterpret_cast<T*>(cache + (row_base + d) * vec_bytes) + part;
+    }
+    *to = *from;
+  }
+}
+
+int grid_for(int64_t work, int64_t cap) {
+  int64_t g = ceil_div(work, kThreads);
+  if (g < 1) g = 1;
+  if (g > cap) g = cap;
+  return static_cast<int>(g);
+}
+
+template <int BYTES>
+int launch_moves(uint8_t* cache, int64_t rows, int64_t num_slots, int64_t vec_bytes, const int64_t* src,
+                 const int64_t* dst, int64_t retained, uint8_t* temp, const uint32_t* flag,
+                 hipStream_t stream) {
+  const int64_t total = rows * retained * (vec_bytes / BYTES);
+  const int cap = device_cu_count() * 16;
+  const int grid = grid_for(total, cap);
+  hipLaunchKernelGGL((compact_move_kernel<BYTES, 0>), dim3(grid), dim3(kThreads), 0, stream, cache, rows,
+                     num_slots, vec_bytes, src, dst, retained, temp, flag);
+  int rc = check_launch("compact direct copy launch");
+  if (rc) return rc;
+  hipLaunchKernelGGL((compact_move_kernel<BYTES, 1>), dim3(grid), dim3(kThreads), 0, stream, cache, rows,
+                     num_slots, vec_bytes, src, dst, retained, temp, flag);
+  rc = check_launch("compact gather launch");
+  if (rc) return rc;
+  hipLaunchKernelGGL((compact_move_kernel<BYTES, 2>), dim3(grid), dim3(kThreads), 0, stream, cache, rows,
+                     num_slots, vec_bytes, src, dst, retained, temp, flag);
+  return check_launch("compact scatter launch");
+}
+
+}  // namespace
+}  // namespace prism
+
+extern "C" int64_t prism_compact_slots_workspace_bytes(int64_t rows, int64_t num_slots, int64_t vec_bytes,
+                                                       int64_t retained) {
+  if (rows < 0 || num_slots < 0 || vec_bytes < 0 || retained < 0) return -1;
+  int64_t f, t;
+  return prism::workspace_layout(rows, num_slots, vec_bytes, retained, &f, &t);
+}
+
+extern "C" int prism_compact_slots(void* cache, int64_t rows, int64_t num_slots, int64_t vec_bytes,
+                                   const int64_t* src, const int64_t* dst, int64_t retained,
+                                   void* workspace, int64_t workspace_bytes, void* stream_ptr) {
+  using namespace prism;
+  clear_error();
+  if (rows < 0 || num_slots < 0 || vec_bytes <= 0 || retained < 0) {
+    set_error("prism_compact_slots: invalid geometry rows=%lld slots=%lld vec_bytes=%lld retained=%lld",
+              static_cast<long long>(rows), static_cast<long long>(num_slots),
+              static_cast<long long>(vec_bytes), static_cast<long long>(retained));
+    return PRISM_ERR_INVALID;
+  }
+  if (retained == 0 || rows == 0 || num_slots == 0) return PRISM_OK;
+  if (!cache || !src || !dst || !workspace) {
+    set_error("prism_compact_slots: null pointer argument");
+    return PRISM_ERR_INVALID;
+  }
+  int64_t flag_off, temp_off;
+  const int64_t need = workspace_layout(rows, num_slots, vec_bytes, retained, &flag_off, &temp_off);
+  if (workspace_bytes < need) {
+    set_error("prism_compact_slots: workspace too small (%lld < %lld bytes)",
+              static_cast<long long>(workspace_bytes), static_cast<long long>(need));
+    return PRISM_ERR_INVALID;
+  }
+  if (!aligned(workspace, 256)) {
+    set_error("prism_compact_slots: workspace must be 256-byte aligned");
+    return PRISM_ERR_LAYOUT;
+  }
+  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  uint8_t* ws = static_cast<uint8_t*>(workspace);
+  uint32_t* bitmap = reinterpret_cast<uint32_t*>(ws);
+  uint32_t* flag = reinterpret_cast<uint32_t*>(ws + flag_off);
+  uint8_t* temp = ws + temp_off;
+  const int cap = device_cu_count() * 8;
+
+  // 1. clear bitmap and flag (the flag word sits right after the bitmap's
+  //    256-byte aligned extent, so one fill covers both).
+  const int64_t clear_words = flag_off / 4 + 1;
+  hipLaunchKernelGGL(clear_words_kernel, dim3(grid_for(clear_words, cap)), dim3(kThreads), 0, stream, bitmap,
+                     clear_words);
+  int rc = check_launch("compact clear launch");
+  if (rc) return rc;
+  // 2. mark sources, 3. detect hazards
+  hipLaunchKernelGGL(mark_sources_kernel, dim3(grid_for(retained, cap)), dim3(kThreads), 0, stream, src,
+                     retained, num_slots, bitmap);
+  if ((rc = check_launch("compact mark launch"))) return rc;
+  hipLaunchKernelGGL(detect_hazard_kernel, dim3(grid_for(retained, cap)), dim3(kThreads), 0, stream, src, dst,
+                     retained, num_slots, bitmap, flag);
+  if ((rc = check_launch("compact detect launch"))) return rc;
+  // 4./5. moves
+  uint8_t* c = static_cast<uint8_t*>(cache);
+  if (vec_bytes % 16 == 0 && aligned(cache, 16))
+    return launch_moves<16>(c, rows, num_slots, vec_bytes, src, dst, retained, temp, flag, stream);
+  if (vec_bytes % 4 == 0 && aligned(cache, 4))
+    return launch_moves<4>(c, rows, num_slots, vec_bytes, src, dst, retained, temp, flag, stream);
+  return launch_moves<1>(c, rows, num_slots, vec_bytes, src, dst, retained, temp, flag, stream);
+}

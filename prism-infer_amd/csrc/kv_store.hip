@@ -1,0 +1,287 @@
+// KV store: bf16/fp16/fp32 K and V -> paged cache slots.
+//
+// Scaled FP8 (the hot path) restates the per-(token, kv head) quantiser of
+// prism_infer/ops/kv_cache_store.py:81-167 (Triton) / :205-227 (eager):
+//     s = max(amax|x| / 448, 1e-6)      fp32, IEEE division
+//     q = e4m3fn(clamp(x / s, -448, 448))
+// bit-exactly against the eager path (correctly rounded division, native RNE
+// conversion, NaN propagation as torch's amax/clamp/cast do).
+//
+// Work layout (vector path): a "unit" is one (token, K|V, head) row of D
+// elements, handled by D/8 lanes that each load 8 consecutive elements
+// (16 bytes for bf16/fp16), reduce |x| max across the unit with lane
+// shuffles, and write 8 FP8 bytes.  Consecutive units are consecutive heads
+// of one token, so a 256-thread block streams 16 contiguous 256-byte rows
+// per tensor and writes 128-byte rows into the slot.
+#include "common.h"
+
+namespace prism {
+namespace {
+
+constexpr float kFp8Max = 448.0f;
+constexpr float kScaleFloor = 1.0e-6f;  // the Python float 1e-6 rounded to fp32
+
+template <int IN_DTYPE>
+struct InVec8;  // 8 input elements -> 8 floats
+
+template <>
+struct InVec8<PRISM_DTYPE_BF16> {
+  __device__ static void load(const void* p, float (&x)[8]) {
+    u32x4 w = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[2 * i] = __uint_as_float(w[i] << 16);
+      x[2 * i + 1] = __uint_as_float(w[i] & 0xFFFF0000u);
+    }
+  }
+};
+
+template <>
+struct InVec8<PRISM_DTYPE_F16> {
+  __device__ static void load(const void* p, float (&x)[8]) {
+    u32x4 w = *reinterpret_cast<const u32x4*>(p);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[2 * i] = f16_bits_to_f32(w[i] & 0xFFFFu);
+      x[2 * i + 1] = f16_bits_to_f32(w[i] >> 16);
+    }
+  }
+};
+
+template <>
+struct InVec8<PRISM_DTYPE_F32> {
+  __device__ static void load(const void* p, float (&x)[8]) {
+    const floatx4* f = reinterpret_cast<const floatx4*>(p);
+    floatx4 a = f[0], b = f[1];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      x[i] = a[i];
+      x[4 + i] = b[i];
+    }
+  }
+};
+
+__device__ __forceinline__ float load_scalar(const void* base, int dtype, int64_t idx) {
+  if (dtype == PRISM_DTYPE_F32) return static_cast<const float*>(base)[idx];
+  uint32_t bits = static_cast<const uint16_t*>(base)[idx];
+  return dtype == PRISM_DTYPE_BF16 ? bf16_bits_to_f32(bits) : f16_bits_to_f32(bits);
+}
+
+// Vector path: LANES = D / 8 lanes per unit, power of two <= 64.
+template <int IN_DTYPE, int LANES, bool SCALED>
+__global__ void __launch_bounds__(256)
+kv_store_vec_kernel(const char* __restrict__ key, const char* __restrict__ value,
+                    int64_t key_tok_stride_bytes, int64_t value_tok_stride_bytes,
+                    uint8_t* __restrict__ k_cache, uint8_t* __restrict__ v_cache,
+                    float* __restrict__ k_scale, float* __restrict__ v_scale,
+                    const int32_t* __restrict__ slot_mapping, int64_t num_units, int num_heads,
+                    int64_t num_slots) {
+  constexpr int IN_BYTES = (IN_DTYPE == PRISM_DTYPE_F32) ? 4 : 2;
+  constexpr int D = LANES * 8;
+  const int64_t unit = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) / LANES;
+  const int sub = threadIdx.x % LANES;
+  if (unit >= num_units) return;  // whole units leave together
+  const int two_h = 2 * num_heads;
+  const int64_t token = unit / two_h;
+  const int rem = static_cast<int>(unit - token * two_h);
+  const int which = rem >= num_heads;  // 0 = K, 1 = V
+  const int head = rem - which * num_heads;
+  const int32_t slot = slot_mapping[token];
+  if (slot < 0 || slot >= num_slots) return;
+
+  const char* src = which ? value : key;
+  const int64_t tok_stride = which ? value_tok_stride_bytes : key_tok_stride_bytes;
+  const char* row = src + token * tok_stride + static_cast<int64_t>(head) * D * IN_BYTES;
+  float x[8];
+  InVec8<IN_DTYPE>::load(row + sub * 8 * IN_BYTES, x);
+
+  uint8_t* cache = which ? v_cache : k_cache;
+  uint8_t* dst = cache + (static_cast<int64_t>(slot) * num_heads + head) * D + sub * 8;
+  u32x2 packed;
+  if constexpr (SCALED) {
+    float amax = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) amax = nan_max(amax, fabsf(x[i]));
+#pragma unroll
+    for (int off = 1; off < LANES; off <<= 1) amax = nan_max(amax, __shfl_xor(amax, off, LANES));
+    float s = amax / kFp8Max;
+    s = (s < kScaleFloor) ? kScaleFloor : s;  // clamp(min=) keeping NaN
+    float q[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) q[i] = nan_min(nan_max(x[i] / s, -kFp8Max), kFp8Max);
+    packed[0] = fp8_encode4(q[0], q[1], q[2], q[3]);
+    packed[1] = fp8_encode4(q[4], q[5], q[6], q[7]);
+    if (sub == 0) {
+      float* scales = which ? v_scale : k_scale;
+      scales[static_cast<int64_t>(slot) * num_heads + head] = s;
+    }
+  } else {
+    packed[0] = fp8_encode4(x[0], x[1], x[2], x[3]);
+    packed[1] = fp8_encode4(x[4], x[5], x[6], x[7]);
+  }
+  *reinterpret_cast<u32x2*>(dst) = packed;
+}
+
+// Scalar path: one thread per unit (any head_dim, any alignment, any cache
+// dtype).  Used for shapes the vector path does not cover.
+__global__ void __launch_bounds__(256)
+kv_store_scalar_kernel(const void* __restrict__ key, const void* __restrict__ value, int in_dtype,
+                       int64_t k_st, int64_t k_sh, int64_t k_sd, int64_t v_st, int64_t v_sh,
+                       int64_t v_sd, void* __restrict__ k_cache, void* __restrict__ v_cache,
+                       int cache_dtype, float* __restrict__ k_scale, float* __restrict__ v_scale,
+                       const int32_t* __restrict__ slot_mapping, int64_t num_units, int num_heads,
+                       int head_dim, int64_t num_slots) {
+  const int64_t unit = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+  if (unit >= num_units) return;
+  const int two_h = 2 * num_heads;
+  const int64_t token = unit / two_h;
+  const int rem = static_cast<int>(unit - token * two_h);
+  const int which = rem >= num_heads;
+  const int head = rem - which * num_heads;
+  const int32_t slot = slot_mapping[token];
+  if (slot < 0 || slot >= num_slots) return;
+  const void* src = which ? value : key;
+  const int64_t base = which ? (token * v_st + head * v_sh) : (token * k_st + head * k_sh);
+  const int64_t sd = which ? v_sd : k_sd;
+  void* cache = which ? v_cache : k_cache;
+  const int64_t out_base = (static_cast<int64_t>(slot) * num_heads + head) * head_dim;
+  const bool scaled = k_scale != nullptr;
+  float s = 1.0f;
+  if (scaled) {
+    float amax = 0.0f;
+    for (int d = 0; d < head_dim; ++d) amax = nan_max(amax, fabsf(load_scalar(src, in_dtype, base + d * sd)));
+    s = amax / kFp8Max;
+    s = (s < kScaleFloor) ? kScaleFloor : s;
+    float* scales = which ? v_scale : k_scale;
+    scales[static_cast<int64_t>(slot) * num_heads + head] = s;
+  }
+  for (int d = 0; d < head_dim; ++d) {
+    float x = load_scalar(src, in_dtype, base + d * sd);
+    if (cache_dtype == PRISM_DTYPE_FP8_E4M3FN) {
+      if (scaled) x = nan_min(nan_max(x / s, -kFp8Max), kFp8Max);
+      static_cast<uint8_t*>(cache)[out_base + d] = static_cast<uint8_t>(fp8_encode4(x, 0.f, 0.f, 0.f) & 0xFFu);
+    } else if (cache_dtype == PRISM_DTYPE_F32) {
+      static_cast<float*>(cache)[out_base + d] = x;
+    } else if (cache_dtype == PRISM_DTYPE_BF16) {
+      // Inputs of the cache's own dtype are copied bit for bit.
+      uint16_t bits = (in_dtype == PRISM_DTYPE_BF16)
+                          ? static_cast<const uint16_t*>(src)[base + d * sd]
+                          : f32_to_bf16_bits(x);
+      static_cast<uint16_t*>(cache)[out_base + d] = bits;
+    } else {
+      uint16_t bits = (in_dtype == PRISM_DTYPE_F16)
+                          ? static_cast<const uint16_t*>(src)[base + d * sd]
+                          : f32_to_f16_bits(x);
+      static_cast<uint16_t*>(cache)[out_base + d] = bits;
+    }
+  }
+}
+
+template <int IN_DTYPE, int LANES>
+int launch_vec(const void* key, const void* value, int64_t k_tok_bytes, int64_t v_tok_bytes,
+               void* k_cache, void* v_cache, float* k_scale, float* v_scale, const int32_t* slots,
+               int64_t num_units, int num_heads, int64_t num_slots, hipStream_t stream) {
+  const int64_t threads = num_units * LANES;
+  const int64_t blocks = ceil_div(threads, 256);
+  if (blocks > INT32_MAX) {
+    set_error("prism_kv_store: too many tokens for one launch");
+    return PRISM_ERR_INVALID;
+  }
+  if (k_scale) {
+    hipLaunchKernelGGL((kv_store_vec_kernel<IN_DTYPE, LANES, true>), dim3(blocks), dim3(256), 0, stream,
+                       static_cast<const char*>(key), static_cast<const char*>(value), k_tok_bytes,
+                       v_tok_bytes, static_cast<uint8_t*>(k_cache), static_cast<uint8_t*>(v_cache),
+                       k_scale, v_scale, slots, num_units, num_heads, num_slots);
+  } else {
+    hipLaunchKernelGGL((kv_store_vec_kernel<IN_DTYPE, LANES, false>), dim3(blocks), dim3(256), 0, stream,
+                       static_cast<const char*>(key), static_cast<const char*>(value), k_tok_bytes,
+                       v_tok_bytes, static_cast<uint8_t*>(k_cache), static_cast<uint8_t*>(v_cache),
+                       nullptr, nullptr, slots, num_units, num_heads, num_slots);
+  }
+  return check_launch("kv_store_vec_kernel launch");
+}
+
+template <int IN_DTYPE>
+int dispatch_lanes(int lanes, const void* key, const void* value, int64_t kb, int64_t vb, void* kc,
+                   void* vc, float* ks, float* vs, const int32_t* slots, int64_t units, int heads,
+                   int64_t num_slots, hipStream_t stream) {
+  switch (lanes) {
+    case 1: return launch_vec<IN_DTYPE, 1>(key, value, kb, vb, kc, vc, ks, vs, slots, units, heads, num_slots, stream);
+    case 2: return launch_vec<IN_DTYPE, 2>(key, value, kb, vb, kc, vc, ks, vs, slots, units, heads, num_slots, stream);
+    case 4: return launch_vec<IN_DTYPE, 4>(key, value, kb, vb, kc, vc, ks, vs, slots, units, heads, num_slots, stream);
+    case 8: return launch_vec<IN_DTYPE, 8>(key, value, kb, vb, kc, vc, ks, vs, slots, units, heads, num_slots, stream);
+    case 16: return launch_vec<IN_DTYPE, 16>(key, value, kb, vb, kc, vc, ks, vs, slots, units, heads, num_slots, stream);
+    case 32: return launch_vec<IN_DTYPE, 32>(key, value, kb, vb, kc, vc, ks, vs, slots, units, heads, num_slots, stream);
+    case 64: return launch_vec<IN_DTYPE, 64>(key, value, kb, vb, kc, vc, ks, vs, slots, units, heads, num_slots, stream);
+    default: return PRISM_ERR_LAYOUT;
+  }
+}
+
+}  // namespace
+}  // namespace prism
+
+extern "C" int prism_kv_store(const void* key, const void* value, int in_dtype,
+                              const int64_t key_strides[3], const int64_t value_strides[3],
+                              void* k_cache, void* v_cache, int cache_dtype, float* k_scale,
+                              float* v_scale, const int32_t* slot_mapping, int64_t num_tokens,
+                              int num_heads, int head_dim, int64_t num_slots, void* stream_ptr) {
+  using namespace prism;
+  clear_error();
+  if (num_tokens < 0 || num_heads <= 0 || head_dim <= 0 || num_slots < 0) {
+    set_error("prism_kv_store: invalid geometry tokens=%lld heads=%d head_dim=%d slots=%lld",
+              static_cast<long long>(num_tokens), num_heads, head_dim, static_cast<long long>(num_slots));
+    return PRISM_ERR_INVALID;
+  }
+  if (in_dtype != PRISM_DTYPE_F32 && in_dtype != PRISM_DTYPE_BF16 && in_dtype != PRISM_DTYPE_F16) {
+    set_error("prism_kv_store: unsupported input dtype code %d", in_dtype);
+    return PRISM_ERR_INVALID;
+  }
+  if (dtype_size(cache_dtype) == 0) {
+    set_error("prism_kv_store: unsupported cache dtype code %d", cache_dtype);
+    return PRISM_ERR_INVALID;
+  }
+  if ((k_scale == nullptr) != (v_scale == nullptr)) {
+    set_error("prism_kv_store: K/V scale caches must be provided together");
+    return PRISM_ERR_INVALID;
+  }
+  if (k_scale && cache_dtype != PRISM_DTYPE_FP8_E4M3FN) {
+    set_error("prism_kv_store: token-head scales require FP8 K/V payload caches");
+    return PRISM_ERR_INVALID;
+  }
+  if (!key || !value || !k_cache || !v_cache || !slot_mapping || !key_strides || !value_strides) {
+    if (num_tokens == 0) return PRISM_OK;
+    set_error("prism_kv_store: null pointer argument");
+    return PRISM_ERR_INVALID;
+  }
+  if (num_tokens == 0) return PRISM_OK;
+  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  const int64_t units = num_tokens * 2 * num_heads;
+  const int in_bytes = dtype_size(in_dtype);
+  const int lanes = head_dim / 8;
+  const bool dense_rows = key_strides[2] == 1 && value_strides[2] == 1 && key_strides[1] == head_dim &&
+                          value_strides[1] == head_dim;
+  const bool pow2_lanes = head_dim % 8 == 0 && lanes >= 1 && lanes <= 64 && (lanes & (lanes - 1)) == 0;
+  const int64_t kb = key_strides[0] * in_bytes;
+  const int64_t vb = value_strides[0] * in_bytes;
+  const bool vec_aligned = aligned(key, 16) && aligned(value, 16) && kb % 16 == 0 && vb % 16 == 0 &&
+                           aligned(k_cache, 8) && aligned(v_cache, 8);
+  if (cache_dtype == PRISM_DTYPE_FP8_E4M3FN && dense_rows && pow2_lanes && vec_aligned) {
+    switch (in_dtype) {
+      case PRISM_DTYPE_BF16:
+        return dispatch_lanes<PRISM_DTYPE_BF16>(lanes, key, value, kb, vb, k_cache, v_cache, k_scale, v_scale,
+                                                slot_mapping, units, num_heads, num_slots, stream);
+      case PRISM_DTYPE_F16:
+        return dispatch_lanes<PRISM_DTYPE_F16>(lanes, key, value, kb, vb, k_cache, v_cache, k_scale, v_scale,
+                                               slot_mapping, units, num_heads, num_slots, stream);
+      default:
+        return dispatch_lanes<PRISM_DTYPE_F32>(lanes, key, value, kb, vb, k_cache, v_cache, k_scale, v_scale,
+                                               slot_mapping, units, num_heads, num_slots, stream);
+    }
+  }
+  const int64_t blocks = ceil_div(units, 256);
+  hipLaunchKernelGGL(kv_store_scalar_kernel, dim3(blocks), dim3(256), 0, stream, key, value, in_dtype,
+                     key_strides[0], key_strides[1], key_strides[2], value_strides[0], value_strides[1],
+                     value_strides[2], k_cache, v_cache, cache_dtype, k_scale, v_scale, slot_mapping, units,
+                     num_heads, head_dim, num_slots);
+  return check_launch("kv_store_scalar_kernel launch");
+}

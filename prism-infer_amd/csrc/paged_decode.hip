@@ -1,0 +1,805 @@
+// Paged decode attention over scaled-FP8 (or unit-scale FP8 / 16-bit / fp32)
+// KV pages, one query token per sequence, grouped-query attention.
+//
+// Semantics follow prism_infer/ops/paged_decode.py:83-180: query head hq reads
+// kv head hq / G; a token t of sequence b is attended iff
+// t < min(context_lens[b], *max_context_len, W * P) and its block id is valid;
+// K and V are dequantised with their per-token, per-head fp32 scales; online
+// softmax in fp32; a sequence with no attended token outputs zeros.
+//
+// Fast path (FP8 cache, head_dim 128, <= 8 kv heads, G <= 16):
+//   grid (batch, splits); one workgroup per (sequence, split of SPLIT tokens)
+//   with one wave per kv head, so the workgroup streams a contiguous
+//   [32 tokens x Hkv x 128 B] slab of K and of V per tile.  Per 32-token tile
+//   and wave:
+//     QK: 2 x 4 MFMA f32_16x16x32_bf16, A = K rows (fp8 -> bf16 exact),
+//         B = Q^T (G valid columns of 16).  Lane (g, c) receives the scores of
+//         q head c for tokens 4g+i and 16+4g+i.
+//     softmax: k_scale * sm_scale * log2(e) applied to the fp32 scores, exp2,
+//         max/sum across the 4 lane groups with lane shuffles.
+//     PV: 2 x 8 MFMA f32_16x16x32_bf16, A = P * v_scale as a bf16 hi/lo pair
+//         (fp32-like accuracy), whose k slots are
+//         exactly the 8 tokens the lane already holds scores for, B = V with
+//         output column c of N-tile j mapped to dim 8c + j, so each lane loads
+//         8 contiguous bytes per token and the byte transpose is one v_perm
+//         plus two native fp8 -> bf16 conversions per 4 values.
+//   Sequences longer than SPLIT write (m, l, acc) partials and a combine
+//   kernel merges them; single-split sequences are written directly.
+// Generic path (any other supported shape): one wave per (sequence, q head),
+//   lane-per-token scores, lane-per-dim accumulation, no split-K.
+#include "common.h"
+
+namespace prism {
+namespace {
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr int kTile = 32;          // tokens per tile
+constexpr int kHeadDim = 128;      // fast-path head_dim
+
+struct DecodeArgs {
+  const void* q;
+  int64_t q_sb, q_sh, q_sd;
+  const uint8_t* k;
+  const uint8_t* v;
+  int64_t k_sblk, k_stok, k_sh;  // bytes
+  int64_t v_sblk, v_stok, v_sh;  // bytes
+  const float* ks;
+  const float* vs;
+  int64_t ks_sblk, ks_stok, ks_sh;  // elements
+  int64_t vs_sblk, vs_stok, vs_sh;
+  const int32_t* bt;
+  int64_t bt_sb, bt_sn;
+  const int32_t* ctx;
+  const int32_t* max_ctx;
+  void* out;
+  int64_t o_sb, o_sh, o_sd;
+  float* part_acc;  // [B][S][Hq][D]
+  float* part_ml;   // [B][S][Hq][2]
+  int batch, num_heads, num_kv_heads, groups, page_size, width, head_dim;
+  int64_t num_blocks;
+  int split;     // tokens per split (multiple of kTile)
+  int max_splits;
+  float scale_log2;  // sm_scale * log2(e)
+  int cache_dtype;
+};
+
+__device__ __forceinline__ int effective_len(const DecodeArgs& a, int b) {
+  int ctx = a.ctx[b];
+  int mx = *a.max_ctx;
+  int64_t cap = static_cast<int64_t>(a.width) * a.page_size;
+  int64_t n = ctx < mx ? ctx : mx;
+  if (n > cap) n = cap;
+  return n > 0 ? static_cast<int>(n) : 0;
+}
+
+template <int QDT>
+__device__ __forceinline__ float load_q(const void* q, int64_t idx) {
+  if constexpr (QDT == PRISM_DTYPE_F32) return static_cast<const float*>(q)[idx];
+  else if constexpr (QDT == PRISM_DTYPE_BF16) return bf16_bits_to_f32(static_cast<const uint16_t*>(q)[idx]);
+  else return f16_bits_to_f32(static_cast<const uint16_t*>(q)[idx]);
+}
+
+template <int QDT>
+__device__ __forceinline__ void store_out(void* out, int64_t idx, float v) {
+  if constexpr (QDT == PRISM_DTYPE_F32) static_cast<float*>(out)[idx] = v;
+  else if constexpr (QDT == PRISM_DTYPE_BF16) static_cast<uint16_t*>(out)[idx] = f32_to_bf16_bits(v);
+  else static_cast<uint16_t*>(out)[idx] = f32_to_f16_bits(v);
+}
+
+// Two fp8 bytes (the selected 16-bit half of `w`) -> bf16x2, exact.
+template <bool HI>
+__device__ __forceinline__ bf16x2 fp8x2_to_bf16x2(uint32_t w) {
+  return __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI);
+}
+
+template <bool HI>
+__device__ __forceinline__ f16x2 fp8x2_to_f16x2(uint32_t w) {
+  return __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, HI);
+}
+
+// 8 fp8 bytes (two dwords) -> 8 bf16 in order.
+__device__ __forceinline__ bf16x8 fp8x8_to_bf16x8(uint32_t w0, uint32_t w1) {
+  bf16x2 a = fp8x2_to_bf16x2<false>(w0), b = fp8x2_to_bf16x2<true>(w0);
+  bf16x2 c = fp8x2_to_bf16x2<false>(w1), d = fp8x2_to_bf16x2<true>(w1);
+  bf16x8 r = {a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+  return r;
+}
+
+__device__ __forceinline__ f16x8 fp8x8_to_f16x8(uint32_t w0, uint32_t w1) {
+  f16x2 a = fp8x2_to_f16x2<false>(w0), b = fp8x2_to_f16x2<true>(w0);
+  f16x2 c = fp8x2_to_f16x2<false>(w1), d = fp8x2_to_f16x2<true>(w1);
+  f16x8 r = {a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
+  return r;
+}
+
+struct TileRegs {
+  u32x4 k[2][2];   // [half][part]: 32 bytes of K row (c + 16 * half), dims 32g..32g+31
+  u32x2 v[8];      // V rows of tokens {4g+i, 16+4g+i}, dims 8c..8c+7
+  float ksc[8];    // k scale of the same 8 tokens
+  float vsc[8];    // v scale
+  uint32_t kvalid; // bit e: token of slot e is attended
+};
+
+// Token order of the 8 per-lane "slots": e < 4 -> 4g + e; e >= 4 -> 16 + 4g + (e - 4).
+__device__ __forceinline__ int slot_token(int g, int e) { return (e < 4) ? (4 * g + e) : (16 + 4 * g + e - 4); }
+
+template <bool SCALED, bool PAGE_ALIGNED>
+__device__ __forceinline__ void load_tile(const DecodeArgs& a, int b, int h, int g, int c, int t0, int t_end,
+                                          TileRegs& r) {
+  const int32_t* bt_row = a.bt + static_cast<int64_t>(b) * a.bt_sb;
+  r.kvalid = 0;
+  if constexpr (PAGE_ALIGNED) {
+    // The whole tile lies in one page.
+    const int page = t0 / a.page_size;
+    const int off0 = t0 - page * a.page_size;
+    const int32_t blk = bt_row[page * a.bt_sn];
+    if (blk < 0 || blk >= a.num_blocks) {
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh)
+        r.k[hh][0] = r.k[hh][1] = u32x4{0, 0, 0, 0};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        r.v[e] = u32x2{0, 0};
+        r.ksc[e] = r.vsc[e] = 0.f;
+      }
+      return;
+    }
+    const uint8_t* kbase = a.k + blk * a.k_sblk + static_cast<int64_t>(off0) * a.k_stok + h * a.k_sh;
+    const uint8_t* vbase = a.v + blk * a.v_sblk + static_cast<int64_t>(off0) * a.v_stok + h * a.v_sh;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const u32x4* p = reinterpret_cast<const u32x4*>(kbase + (c + 16 * hh) * a.k_stok + 32 * g);
+      r.k[hh][0] = p[0];
+      r.k[hh][1] = p[1];
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int tk = slot_token(g, e);
+      r.v[e] = *reinterpret_cast<const u32x2*>(vbase + tk * a.v_stok + 8 * c);
+      if (SCALED) {
+        const int64_t row = blk * a.ks_sblk + static_cast<int64_t>(off0 + tk) * a.ks_stok + h * a.ks_sh;
+        const int64_t vrow = blk * a.vs_sblk + static_cast<int64_t>(off0 + tk) * a.vs_stok + h * a.vs_sh;
+        r.ksc[e] = a.ks[row];
+        r.vsc[e] = a.vs[vrow];
+      } else {
+        r.ksc[e] = r.vsc[e] = 1.f;
+      }
+      if (t0 + tk < t_end) r.kvalid |= 1u << e;
+    }
+  } else {
+    // Tiles may straddle pages: resolve every row separately.
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const int tok = t0 + c + 16 * hh;
+      r.k[hh][0] = r.k[hh][1] = u32x4{0, 0, 0, 0};
+      if (tok < t_end) {
+        const int page = tok / a.page_size;
+        const int32_t blk = bt_row[page * a.bt_sn];
+        if (blk >= 0 && blk < a.num_blocks) {
+          const u32x4* p = reinterpret_cast<const u32x4*>(
+              a.k + blk * a.k_sblk + static_cast<int64_t>(tok - page * a.page_size) * a.k_stok + h * a.k_sh + 32 * g);
+          r.k[hh][0] = p[0];
+          r.k[hh][1] = p[1];
+        }
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int tok = t0 + slot_token(g, e);
+      r.v[e] = u32x2{0, 0};
+      r.ksc[e] = r.vsc[e] = 0.f;
+      if (tok < t_end) {
+        const int page = tok / a.page_size;
+        const int off = tok - page * a.page_size;
+        const int32_t blk = bt_row[page * a.bt_sn];
+        if (blk >= 0 && blk < a.num_blocks) {
+          r.v[e] = *reinterpret_cast<const u32x2*>(a.v + blk * a.v_sblk + static_cast<int64_t>(off) * a.v_stok +
+                                                   h * a.v_sh + 8 * c);
+          if (SCALED) {
+            r.ksc[e] = a.ks[blk * a.ks_sblk + static_cast<int64_t>(off) * a.ks_stok + h * a.ks_sh];
+            r.vsc[e] = a.vs[blk * a.vs_sblk + static_cast<int64_t>(off) * a.vs_stok + h * a.vs_sh];
+          } else {
+            r.ksc[e] = r.vsc[e] = 1.f;
+          }
+          r.kvalid |= 1u << e;
+        }
+      }
+    }
+  }
+}
+
+// Query operand type per q dtype: bf16 MFMA for bf16 (and the hi/lo split of
+// fp32), f16 MFMA for fp16.
+template <int QDT>
+struct QOperand {
+  bf16x8 hi[4];
+  bf16x8 lo[4];  // used for fp32 queries only
+};
+
+template <>
+struct QOperand<PRISM_DTYPE_F16> {
+  f16x8 hi[4];
+};
+
+template <int QDT, bool SCALED, bool PAGE_ALIGNED>
+__global__ void __launch_bounds__(512)
+paged_decode_split_kernel(const DecodeArgs a) {
+  const int lane = threadIdx.x & 63;
+  const int h = threadIdx.x >> 6;  // kv head of this wave
+  const int g = lane >> 4;
+  const int c = lane & 15;
+  const int b = blockIdx.x;
+  const int s = blockIdx.y;
+  const int G = a.groups;
+
+  const int n_eff = effective_len(a, b);
+  const int t_begin = s * a.split;
+  if (t_begin >= n_eff) {
+    if (s == 0) {
+      // No attended token: zeros (the reference kernel's l == 0 branch).
+      for (int idx = lane; idx < G * kHeadDim; idx += 64) {
+        const int qh = h * G + idx / kHeadDim;
+        const int d = idx % kHeadDim;
+        store_out<QDT>(a.out, b * a.o_sb + qh * a.o_sh + d * a.o_sd, 0.f);
+      }
+    }
+    return;
+  }
+  const int t_end = min(t_begin + a.split, n_eff);
+  const int nsplit = (n_eff + a.split - 1) / a.split;
+
+  // ---- query operand (B of QK): column c = q head h*G + c, k slot 8g+e of
+  // chunk cc <-> dim 32g + 8cc + e.
+  QOperand<QDT> qop;
+  {
+    const bool qvalid = c < G;
+    const int64_t qbase = static_cast<int64_t>(b) * a.q_sb + static_cast<int64_t>(h * G + (qvalid ? c : 0)) * a.q_sh;
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int d = 32 * g + 8 * cc + e;
+        const float x = qvalid ? load_q<QDT>(a.q, qbase + d * a.q_sd) : 0.f;
+        if constexpr (QDT == PRISM_DTYPE_F16) {
+          qop.hi[cc][e] = static_cast<_Float16>(x);
+        } else {
+          const __bf16 hi = static_cast<__bf16>(x);
+          qop.hi[cc][e] = hi;
+          if constexpr (QDT == PRISM_DTYPE_F32) qop.lo[cc][e] = static_cast<__bf16>(x - static_cast<float>(hi));
+        }
+      }
+    }
+  }
+
+  floatx4 acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY;  // running max (log2 domain) of q head c
+  float l_run = 0.f;        // this lane's share of the running sum
+
+  TileRegs cur, nxt;
+  load_tile<SCALED, PAGE_ALIGNED>(a, b, h, g, c, t_begin, t_end, cur);
+  for (int t0 = t_begin; t0 < t_end; t0 += kTile) {
+    if (t0 + kTile < t_end) load_tile<SCALED, PAGE_ALIGNED>(a, b, h, g, c, t0 + kTile, t_end, nxt);
+
+    // ---- QK
+    floatx4 sc[2];
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      floatx4 accs = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc) {
+        const uint32_t w0 = cur.k[hh][cc >> 1][(cc & 1) * 2];
+        const uint32_t w1 = cur.k[hh][cc >> 1][(cc & 1) * 2 + 1];
+        if constexpr (QDT == PRISM_DTYPE_F16) {
+          accs = __builtin_amdgcn_mfma_f32_16x16x32_f16(fp8x8_to_f16x8(w0, w1), qop.hi[cc], accs, 0, 0, 0);
+        } else {
+          const bf16x8 kb = fp8x8_to_bf16x8(w0, w1);
+          accs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qop.hi[cc], accs, 0, 0, 0);
+          if constexpr (QDT == PRISM_DTYPE_F32)
+            accs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qop.lo[cc], accs, 0, 0, 0);
+        }
+      }
+      sc[hh] = accs;
+    }
+
+    // ---- online softmax (log2 domain).  Value e of this lane: half e/4, row e%4.
+    float x[8];
+    float tmax = -INFINITY;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const bool ok = ((cur.kvalid >> e) & 1u) && c < G;
+      const float v = sc[e >> 2][e & 3] * (cur.ksc[e] * a.scale_log2);
+      x[e] = ok ? v : -INFINITY;
+      tmax = fmaxf(tmax, x[e]);
+    }
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+    const float m_new = fmaxf(m_run, tmax);
+    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+    const float alpha = exp2f(m_run - m_use);
+    m_run = m_new;
+    // P * v_scale as a bf16 hi/lo pair (about 16 significant bits): the PV
+    // product then matches fp32 accumulation closely (V itself is exact).
+    float psum = 0.f;
+    bf16x8 pa, pa_lo;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float p = exp2f(x[e] - m_use);  // 0 for masked slots
+      psum += p;
+      const float pv = ((cur.kvalid >> e) & 1u) ? p * cur.vsc[e] : 0.f;
+      const __bf16 hi = static_cast<__bf16>(pv);
+      pa[e] = hi;
+      pa_lo[e] = static_cast<__bf16>(pv - static_cast<float>(hi));
+    }
+    l_run = l_run * alpha + psum;
+
+    // Rescale accumulator rows (q heads 4g+i) by their alpha.
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float ai = __shfl(alpha, 4 * g + i);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) acc[j][i] *= ai;
+    }
+
+    // Rows past the end of the split may hold anything (NaN codes included);
+    // their V bytes are zeroed because the PV MFMA would turn 0 * NaN into NaN.
+    // (Done here, at use, so the prefetch of this tile stays asynchronous.)
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      if (!((cur.kvalid >> e) & 1u)) cur.v[e] = u32x2{0, 0};
+
+    // ---- PV: B operand of N-tile j = byte j of the lane's 8 V rows.
+#pragma unroll
+    for (int jp = 0; jp < 4; ++jp) {  // column pairs (2jp, 2jp+1)
+      const int j = 2 * jp;
+      const int dw = j >> 2;
+      const int jj = j & 3;
+      const uint32_t sel = (jj) | ((4 + jj) << 8) | ((jj + 1) << 16) | ((5 + jj) << 24);
+      bf16x8 b0, b1;
+#pragma unroll
+      for (int ep = 0; ep < 4; ++ep) {  // slot pairs (2ep, 2ep+1)
+        const uint32_t lo = cur.v[2 * ep][dw];
+        const uint32_t hi = cur.v[2 * ep + 1][dw];
+        const uint32_t pr = __builtin_amdgcn_perm(hi, lo, sel);
+        const bf16x2 cj = fp8x2_to_bf16x2<false>(pr);
+        const bf16x2 cj1 = fp8x2_to_bf16x2<true>(pr);
+        b0[2 * ep] = cj[0];
+        b0[2 * ep + 1] = cj[1];
+        b1[2 * ep] = cj1[0];
+        b1[2 * ep + 1] = cj1[1];
+      }
+      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, b0, acc[j], 0, 0, 0);
+      acc[j + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, b1, acc[j + 1], 0, 0, 0);
+      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa_lo, b0, acc[j], 0, 0, 0);
+      acc[j + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa_lo, b1, acc[j + 1], 0, 0, 0);
+    }
+
+    if (t0 + kTile < t_end) cur = nxt;
+  }
+
+  // ---- finish: total l per q head c, then per accumulator row 4g+i.
+  float l_tot = l_run + __shfl_xor(l_run, 16);
+  l_tot += __shfl_xor(l_tot, 32);
+  if (nsplit == 1) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int qr = 4 * g + i;
+      const float li = __shfl(l_tot, qr);
+      if (qr < G) {
+        const float inv = li > 0.f ? 1.f / li : 0.f;
+        const int64_t base = static_cast<int64_t>(b) * a.o_sb + static_cast<int64_t>(h * G + qr) * a.o_sh;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) store_out<QDT>(a.out, base + (8 * c + j) * a.o_sd, acc[j][i] * inv);
+      }
+    }
+  } else {
+    const int64_t row0 = (static_cast<int64_t>(b) * a.max_splits + s) * a.num_heads;
+    for (int i = 0; i < 4; ++i) {
+      const int qr = 4 * g + i;
+      const float li = __shfl(l_tot, qr);
+      const float mi = __shfl(m_run, qr);
+      if (qr < G) {
+        const int64_t hq = h * G + qr;
+        floatx4* dstp = reinterpret_cast<floatx4*>(a.part_acc + (row0 + hq) * kHeadDim + 8 * c);
+        dstp[0] = floatx4{acc[0][i], acc[1][i], acc[2][i], acc[3][i]};
+        dstp[1] = floatx4{acc[4][i], acc[5][i], acc[6][i], acc[7][i]};
+        if (c == 0) {
+          a.part_ml[(row0 + hq) * 2 + 0] = mi;
+          a.part_ml[(row0 + hq) * 2 + 1] = li;
+        }
+      }
+    }
+  }
+}
+
+// Merge split-K partials: grid (batch, num_heads), one wave each.
+template <int QDT>
+__global__ void __launch_bounds__(64) paged_decode_combine_kernel(const DecodeArgs a) {
+  const int b = blockIdx.x;
+  const int hq = blockIdx.y;
+  const int lane = threadIdx.x;
+  const int n_eff = effective_len(a, b);
+  const int nsplit = (n_eff + a.split - 1) / a.split;
+  if (nsplit <= 1) return;
+  const int64_t row0 = static_cast<int64_t>(b) * a.max_splits * a.num_heads + hq;
+  float m_max = -INFINITY;
+  for (int s = lane; s < nsplit; s += 64) m_max = fmaxf(m_max, a.part_ml[(row0 + static_cast<int64_t>(s) * a.num_heads) * 2]);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) m_max = fmaxf(m_max, __shfl_xor(m_max, off));
+  const float m_use = (m_max == -INFINITY) ? 0.f : m_max;
+  float l_sum = 0.f;
+  for (int s = lane; s < nsplit; s += 64) {
+    const int64_t r = (row0 + static_cast<int64_t>(s) * a.num_heads) * 2;
+    l_sum += a.part_ml[r + 1] * exp2f(a.part_ml[r] - m_use);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) l_sum += __shfl_xor(l_sum, off);
+  float o0 = 0.f, o1 = 0.f;
+  for (int s = 0; s < nsplit; ++s) {
+    const int64_t r = row0 + static_cast<int64_t>(s) * a.num_heads;
+    const float w = exp2f(a.part_ml[r * 2] - m_use);
+    const float* src = a.part_acc + r * kHeadDim;
+    o0 += w * src[lane];
+    o1 += w * src[lane + 64];
+  }
+  const float inv = l_sum > 0.f ? 1.f / l_sum : 0.f;
+  const int64_t base = static_cast<int64_t>(b) * a.o_sb + static_cast<int64_t>(hq) * a.o_sh;
+  store_out<QDT>(a.out, base + lane * a.o_sd, o0 * inv);
+  store_out<QDT>(a.out, base + (lane + 64) * a.o_sd, o1 * inv);
+}
+
+// ---------------------------------------------------------------- generic path
+
+constexpr int kGenericMaxDim = 256;
+
+__device__ __forceinline__ float load_cache(const uint8_t* base, int dtype, int64_t elem) {
+  switch (dtype) {
+    case PRISM_DTYPE_FP8_E4M3FN: {
+      uint32_t bytev = base[elem];
+      return __builtin_amdgcn_cvt_f32_fp8(bytev, 0);
+    }
+    case PRISM_DTYPE_BF16: return bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(base)[elem]);
+    case PRISM_DTYPE_F16: return f16_bits_to_f32(reinterpret_cast<const uint16_t*>(base)[elem]);
+    default: return reinterpret_cast<const float*>(base)[elem];
+  }
+}
+
+// Strides of k/v here are in ELEMENTS of the cache dtype.
+template <int QDT>
+__global__ void __launch_bounds__(64) paged_decode_generic_kernel(const DecodeArgs a) {
+  __shared__ float q_s[kGenericMaxDim];
+  __shared__ float p_s[64];
+  __shared__ int valid_s[64];
+  __shared__ int64_t vrow_s[64];
+  const int b = blockIdx.x;
+  const int hq = blockIdx.y;
+  const int lane = threadIdx.x;
+  const int D = a.head_dim;
+  const int hk = hq / a.groups;
+  const bool scaled = a.ks != nullptr;
+  for (int d = lane; d < D; d += 64)
+    q_s[d] = load_q<QDT>(a.q, static_cast<int64_t>(b) * a.q_sb + static_cast<int64_t>(hq) * a.q_sh + d * a.q_sd);
+  __syncthreads();
+  const int n_eff = effective_len(a, b);
+  const int32_t* bt_row = a.bt + static_cast<int64_t>(b) * a.bt_sb;
+  float m_run = -INFINITY, l_run = 0.f;
+  float acc[kGenericMaxDim / 64];
+#pragma unroll
+  for (int k = 0; k < kGenericMaxDim / 64; ++k) acc[k] = 0.f;
+  for (int t0 = 0; t0 < n_eff; t0 += 64) {
+    const int tok = t0 + lane;
+    bool valid = tok < n_eff;
+    int64_t krow = 0, vrow = 0;
+    float ksc = 1.f, vsc = 1.f;
+    if (valid) {
+      const int page = tok / a.page_size;
+      const int off = tok - page * a.page_size;
+      const int32_t blk = bt_row[page * a.bt_sn];
+      valid = blk >= 0 && blk < a.num_blocks;
+      if (valid) {
+        krow = blk * a.k_sblk + static_cast<int64_t>(off) * a.k_stok + hk * a.k_sh;
+        vrow = blk * a.v_sblk + static_cast<int64_t>(off) * a.v_stok + hk * a.v_sh;
+        if (scaled) {
+          ksc = a.ks[blk * a.ks_sblk + static_cast<int64_t>(off) * a.ks_stok + hk * a.ks_sh];
+          vsc = a.vs[blk * a.vs_sblk + static_cast<int64_t>(off) * a.vs_stok + hk * a.vs_sh];
+        }
+      }
+    }
+    float xs = -INFINITY;
+    if (valid) {
+      float dot = 0.f;
+      for (int d = 0; d < D; ++d) dot += q_s[d] * load_cache(a.k, a.cache_dtype, krow + d);
+      xs = dot * ksc * a.scale_log2;
+    }
+    float tmax = xs;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) tmax = fmaxf(tmax, __shfl_xor(tmax, off));
+    const float m_new = fmaxf(m_run, tmax);
+    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+    const float alpha = exp2f(m_run - m_use);
+    m_run = m_new;
+    const float p = valid ? exp2f(xs - m_use) : 0.f;
+    float psum = p;
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) psum += __shfl_xor(psum, off);
+    l_run = l_run * alpha + psum;
+    p_s[lane] = valid ? p * vsc : 0.f;
+    vrow_s[lane] = vrow;
+    valid_s[lane] = valid;
+    __syncthreads();
+    const int chunk = min(64, n_eff - t0);
+#pragma unroll
+    for (int k = 0; k < kGenericMaxDim / 64; ++k) {
+      const int d = lane + 64 * k;
+      if (d < D) {
+        float sum = acc[k] * alpha;
+        for (int t = 0; t < chunk; ++t)
+          if (valid_s[t]) sum += p_s[t] * load_cache(a.v, a.cache_dtype, vrow_s[t] + d);
+        acc[k] = sum;
+      }
+    }
+    __syncthreads();
+  }
+  const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
+  const int64_t base = static_cast<int64_t>(b) * a.o_sb + static_cast<int64_t>(hq) * a.o_sh;
+#pragma unroll
+  for (int k = 0; k < kGenericMaxDim / 64; ++k) {
+    const int d = lane + 64 * k;
+    if (d < D) store_out<QDT>(a.out, base + d * a.o_sd, acc[k] * inv);
+  }
+}
+
+// ---------------------------------------------------------------- host side
+
+struct Geometry {
+  bool fast;
+  int split;
+  int max_splits;
+  int64_t ws_bytes;
+  int64_t acc_off, ml_off;
+};
+
+bool fast_geometry(int num_heads, int num_kv_heads, int head_dim, int cache_dtype) {
+  if (cache_dtype != PRISM_DTYPE_FP8_E4M3FN || head_dim != kHeadDim) return false;
+  if (num_kv_heads <= 0 || num_kv_heads > 8 || num_heads % num_kv_heads) return false;
+  return num_heads / num_kv_heads <= 16;
+}
+
+int choose_split(int batch, int num_kv_heads, int page_size, int width) {
+  const char* env = getenv("PRISM_DECODE_SPLIT");
+  if (env) {
+    int v = atoi(env);
+    if (v >= kTile) return static_cast<int>(align_up(v, kTile));
+  }
+  const int64_t cap = static_cast<int64_t>(width) * page_size;
+  const int64_t tiles = static_cast<int64_t>(batch) * ceil_div(cap, kTile);
+  const int64_t target = static_cast<int64_t>(device_cu_count()) * 8;
+  int64_t per = tiles / (target > 0 ? target : 1);
+  if (per < 2) per = 2;
+  // round down to a power of two number of tiles
+  int64_t p2 = 1;
+  while (p2 * 2 <= per) p2 *= 2;
+  int64_t split = p2 * kTile;
+  const int64_t cap_tiles = align_up(cap, kTile);
+  if (split > cap_tiles) split = cap_tiles > 0 ? cap_tiles : kTile;
+  (void)num_kv_heads;
+  return static_cast<int>(split);
+}
+
+Geometry geometry(int batch, int num_heads, int num_kv_heads, int head_dim, int page_size, int width,
+                  int cache_dtype) {
+  Geometry geo{};
+  geo.fast = fast_geometry(num_heads, num_kv_heads, head_dim, cache_dtype);
+  if (!geo.fast) return geo;
+  geo.split = choose_split(batch, num_kv_heads, page_size, width);
+  const int64_t cap = static_cast<int64_t>(width) * page_size;
+  geo.max_splits = static_cast<int>(cap > 0 ? ceil_div(cap, geo.split) : 1);
+  if (geo.max_splits <= 1) {
+    geo.ws_bytes = 0;
+    return geo;
+  }
+  const int64_t rows = static_cast<int64_t>(batch) * geo.max_splits * num_heads;
+  geo.acc_off = 0;
+  geo.ml_off = align_up(rows * head_dim * 4, 256);
+  geo.ws_bytes = geo.ml_off + align_up(rows * 2 * 4, 256);
+  return geo;
+}
+
+template <int QDT>
+int launch_all(int stage, const DecodeArgs& args, const Geometry& geo, bool page_aligned, hipStream_t stream) {
+  const bool scaled = args.ks != nullptr;
+  if (!geo.fast) {
+    if (stage == 2) return PRISM_OK;
+    hipLaunchKernelGGL(paged_decode_generic_kernel<QDT>, dim3(args.batch, args.num_heads), dim3(64), 0, stream,
+                       args);
+    return check_launch("paged_decode_generic_kernel launch");
+  }
+  if (stage != 2) {
+    dim3 grid(args.batch, geo.max_splits);
+    dim3 block(64 * args.num_kv_heads);
+#define PRISM_LAUNCH_SPLIT(S, A) \
+  hipLaunchKernelGGL((paged_decode_split_kernel<QDT, S, A>), grid, block, 0, stream, args)
+    if (scaled && page_aligned) PRISM_LAUNCH_SPLIT(true, true);
+    else if (scaled) PRISM_LAUNCH_SPLIT(true, false);
+    else if (page_aligned) PRISM_LAUNCH_SPLIT(false, true);
+    else PRISM_LAUNCH_SPLIT(false, false);
+#undef PRISM_LAUNCH_SPLIT
+    int rc = check_launch("paged_decode_split_kernel launch");
+    if (rc) return rc;
+  }
+  if (stage != 1 && geo.max_splits > 1) {
+    hipLaunchKernelGGL(paged_decode_combine_kernel<QDT>, dim3(args.batch, args.num_heads), dim3(64), 0, stream,
+                       args);
+    return check_launch("paged_decode_combine_kernel launch");
+  }
+  return PRISM_OK;
+}
+
+}  // namespace
+}  // namespace prism
+
+extern "C" int64_t prism_paged_decode_workspace_bytes(int batch, int num_heads, int num_kv_heads, int head_dim,
+                                                      int page_size, int max_blocks_per_seq, int cache_dtype) {
+  if (batch < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || page_size <= 0 || max_blocks_per_seq < 0)
+    return -1;
+  return prism::geometry(batch, num_heads, num_kv_heads, head_dim, page_size, max_blocks_per_seq, cache_dtype)
+      .ws_bytes;
+}
+
+extern "C" int prism_paged_decode_split_tokens(int batch, int num_heads, int num_kv_heads, int head_dim,
+                                               int page_size, int max_blocks_per_seq, int cache_dtype) {
+  if (batch < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || page_size <= 0 || max_blocks_per_seq < 0)
+    return -1;
+  prism::Geometry geo =
+      prism::geometry(batch, num_heads, num_kv_heads, head_dim, page_size, max_blocks_per_seq, cache_dtype);
+  return geo.fast ? geo.split : 0;
+}
+
+extern "C" int prism_paged_decode_stage(
+    int stage, const void* q, int q_dtype, const int64_t q_strides[3], const void* k_cache, const void* v_cache,
+    int cache_dtype, const int64_t k_strides[4], const int64_t v_strides[4], const float* k_scale,
+    const float* v_scale, const int64_t ks_strides[3], const int64_t vs_strides[3], const int32_t* block_tables,
+    const int64_t bt_strides[2], const int32_t* context_lens, const int32_t* max_context_len, void* out,
+    const int64_t out_strides[3], int batch, int num_heads, int num_kv_heads, int head_dim, int page_size,
+    int64_t num_blocks, int max_blocks_per_seq, float scale, void* workspace, int64_t workspace_bytes,
+    void* stream_ptr) {
+  using namespace prism;
+  clear_error();
+  if (stage < 0 || stage > 2) {
+    set_error("prism_paged_decode: stage must be 0, 1 or 2");
+    return PRISM_ERR_INVALID;
+  }
+  if (batch < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || page_size <= 0 ||
+      max_blocks_per_seq < 0 || num_blocks < 0) {
+    set_error("prism_paged_decode: invalid geometry");
+    return PRISM_ERR_INVALID;
+  }
+  if (num_heads % num_kv_heads) {
+    set_error("prism_paged_decode: num_heads must be divisible by num_kv_heads, got %d and %d", num_heads,
+              num_kv_heads);
+    return PRISM_ERR_INVALID;
+  }
+  if (q_dtype != PRISM_DTYPE_F32 && q_dtype != PRISM_DTYPE_BF16 && q_dtype != PRISM_DTYPE_F16) {
+    set_error("prism_paged_decode: unsupported query dtype code %d", q_dtype);
+    return PRISM_ERR_INVALID;
+  }
+  if (dtype_size(cache_dtype) == 0) {
+    set_error("prism_paged_decode: unsupported cache dtype code %d", cache_dtype);
+    return PRISM_ERR_INVALID;
+  }
+  if ((k_scale == nullptr) != (v_scale == nullptr)) {
+    set_error("prism_paged_decode: K/V scale caches must be provided together");
+    return PRISM_ERR_INVALID;
+  }
+  if (k_scale && cache_dtype != PRISM_DTYPE_FP8_E4M3FN) {
+    set_error("prism_paged_decode: token-head scales require FP8 E4M3FN K/V payload caches");
+    return PRISM_ERR_INVALID;
+  }
+  if (head_dim > kGenericMaxDim) {
+    set_error("prism_paged_decode: supports head_dim <= %d, got %d", kGenericMaxDim, head_dim);
+    return PRISM_ERR_INVALID;
+  }
+  if (k_strides[3] != 1 || v_strides[3] != 1) {
+    set_error("prism_paged_decode: K/V caches need a unit head_dim stride");
+    return PRISM_ERR_LAYOUT;
+  }
+  if (batch == 0) return PRISM_OK;
+  if (!q || !k_cache || !v_cache || !block_tables || !context_lens || !max_context_len || !out) {
+    set_error("prism_paged_decode: null pointer argument");
+    return PRISM_ERR_INVALID;
+  }
+  const int esz = dtype_size(cache_dtype);
+  Geometry geo = geometry(batch, num_heads, num_kv_heads, head_dim, page_size, max_blocks_per_seq, cache_dtype);
+  if (geo.fast) {
+    // 16-byte row loads need 16-byte aligned rows.
+    const bool ok = aligned(k_cache, 16) && aligned(v_cache, 16) && k_strides[0] % 16 == 0 && k_strides[1] % 16 == 0 &&
+                    k_strides[2] % 16 == 0 && v_strides[0] % 16 == 0 && v_strides[1] % 16 == 0 &&
+                    v_strides[2] % 16 == 0;
+    if (!ok) geo.fast = false, geo.ws_bytes = 0, geo.max_splits = 1;
+  }
+  if (geo.fast && geo.ws_bytes > 0) {
+    if (!workspace || workspace_bytes < geo.ws_bytes) {
+      set_error("prism_paged_decode: workspace too small (%lld < %lld bytes)", static_cast<long long>(workspace_bytes),
+                static_cast<long long>(geo.ws_bytes));
+      return PRISM_ERR_INVALID;
+    }
+    if (!aligned(workspace, 256)) {
+      set_error("prism_paged_decode: workspace must be 256-byte aligned");
+      return PRISM_ERR_LAYOUT;
+    }
+  }
+  DecodeArgs args{};
+  args.q = q;
+  args.q_sb = q_strides[0];
+  args.q_sh = q_strides[1];
+  args.q_sd = q_strides[2];
+  args.k = static_cast<const uint8_t*>(k_cache);
+  args.v = static_cast<const uint8_t*>(v_cache);
+  // The fast path addresses K/V in bytes; the generic path in elements.
+  const int64_t mul = geo.fast ? esz : 1;
+  args.k_sblk = k_strides[0] * mul;
+  args.k_stok = k_strides[1] * mul;
+  args.k_sh = k_strides[2] * mul;
+  args.v_sblk = v_strides[0] * mul;
+  args.v_stok = v_strides[1] * mul;
+  args.v_sh = v_strides[2] * mul;
+  args.ks = k_scale;
+  args.vs = v_scale;
+  if (k_scale) {
+    args.ks_sblk = ks_strides[0];
+    args.ks_stok = ks_strides[1];
+    args.ks_sh = ks_strides[2];
+    args.vs_sblk = vs_strides[0];
+    args.vs_stok = vs_strides[1];
+    args.vs_sh = vs_strides[2];
+  }
+  args.bt = block_tables;
+  args.bt_sb = bt_strides[0];
+  args.bt_sn = bt_strides[1];
+  args.ctx = context_lens;
+  args.max_ctx = max_context_len;
+  args.out = out;
+  args.o_sb = out_strides[0];
+  args.o_sh = out_strides[1];
+  args.o_sd = out_strides[2];
+  if (geo.fast && geo.ws_bytes > 0) {
+    args.part_acc = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + geo.acc_off);
+    args.part_ml = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + geo.ml_off);
+  }
+  args.batch = batch;
+  args.num_heads = num_heads;
+  args.num_kv_heads = num_kv_heads;
+  args.groups = num_heads / num_kv_heads;
+  args.page_size = page_size;
+  args.width = max_blocks_per_seq;
+  args.head_dim = head_dim;
+  args.num_blocks = num_blocks;
+  args.split = geo.fast ? geo.split : 0;
+  args.max_splits = geo.fast ? geo.max_splits : 1;
+  args.scale_log2 = scale * kLog2e;
+  args.cache_dtype = cache_dtype;
+  const bool page_aligned = (page_size % kTile) == 0;
+  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  switch (q_dtype) {
+    case PRISM_DTYPE_BF16: return launch_all<PRISM_DTYPE_BF16>(stage, args, geo, page_aligned, stream);
+    case PRISM_DTYPE_F16: return launch_all<PRISM_DTYPE_F16>(stage, args, geo, page_aligned, stream);
+    default: return launch_all<PRISM_DTYPE_F32>(stage, args, geo, page_aligned, stream);
+  }
+}
+
+extern "C" int prism_paged_decode(const void* q, int q_dtype, const int64_t q_strides[3], const void* k_cache,
+                                  const void* v_cache, int cache_dtype, const int64_t k_strides[4],
+                                  const int64_t v_strides[4], const float* k_scale, const float* v_scale,
+                                  const int64_t ks_strides[3], const int64_t vs_strides[3],
+                                  const int32_t* block_tables, const int64_t bt_strides[2],
+                                  const int32_t* context_lens, const int32_t* max_context_len, void* out,
+                                  const int64_t out_strides[3], int batch, int num_heads, int num_kv_heads,
+                                  int head_dim, int page_size, int64_t num_blocks, int max_blocks_per_seq,
+                                  float scale, void* workspace, int64_t workspace_bytes, void* stream) {
+  return prism_paged_decode_stage(0, q, q_dtype, q_strides, k_cache, v_cache, cache_dtype, k_strides, v_strides,
+                                  k_scale, v_scale, ks_strides, vs_strides, block_tables, bt_strides, context_lens,
+                                  max_context_len, out, out_strides, batch, num_heads, num_kv_heads, head_dim,
+                                  page_size, num_blocks, max_blocks_per_seq, scale, workspace, workspace_bytes,
+                                  stream);
+}

@@ -1,0 +1,246 @@
+"""GPU parity: HIP paged decode against the CPU oracle (tolerance 2e-2 abs / 1e-2 rel, bf16)."""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+import oracle
+from _helpers import assert_decode_close, compact_to_cpu, require_gpu
+
+pytestmark = pytest.mark.gpu
+
+FP8 = torch.float8_e4m3fn
+
+
+def _quantize_cpu(source: torch.Tensor):
+    """Scaled-FP8 pages of ``source`` [N, P, H, D] through the oracle."""
+
+    n, p, h, d = source.shape
+    flat = source.reshape(n * p, h, d)
+    k = torch.zeros(n, p, h, d, dtype=FP8)
+    s = torch.zeros(n, p, h, dtype=torch.float32)
+    k2 = torch.zeros_like(k)
+    s2 = torch.zeros_like(s)
+    oracle.store_scaled(flat, flat, k, k2, torch.arange(n * p, dtype=torch.int32), s, s2)
+    return k, s
+
+
+def _decode_gpu(q, k, v, ks, vs, tables, lens, scale, max_ctx=None):
+    from prism_infer.ops.paged_decode import paged_decode_attention
+
+    dev = torch.device("cuda")
+    to = lambda t: None if t is None else (t.view(torch.uint8).to(dev).view(FP8) if t.dtype == FP8 else t.to(dev))
+    out = paged_decode_attention(
+        to(q), to(k), to(v), to(tables), to(lens), scale,
+        k_scale_cache=to(ks), v_scale_cache=to(vs),
+        max_context_len=None if max_ctx is None else torch.tensor([max_ctx], dtype=torch.int32, device=dev),
+    )
+    torch.cuda.synchronize()
+    return out.cpu()
+
+
+def _oracle(q, k, v, ks, vs, tables, lens, scale, max_ctx=None):
+    return oracle.decode_kernel_semantics(q, k, v, tables, lens, scale, k_scale_cache=ks, v_scale_cache=vs,
+                                          max_context_len=max_ctx)
+
+
+def test_reference_scaled_decode_case_seed_20260720():
+    """The reference's scaled decode case: B=2, 8q/2kv heads, D=128, 16-token pages, ctx 17/33."""
+
+    require_gpu()
+    g = torch.Generator().manual_seed(20260720)
+    q = torch.randn(2, 8, 128, generator=g).to(torch.bfloat16)
+    k_src = (torch.randn(6, 16, 2, 128, generator=g) * 23.0).to(torch.bfloat16)
+    v_src = (torch.randn(6, 16, 2, 128, generator=g) * 15.0).to(torch.bfloat16)
+    k, ks = _quantize_cpu(k_src)
+    v, vs = _quantize_cpu(v_src)
+    tables = torch.arange(6, dtype=torch.int32).view(2, 3)
+    lens = torch.tensor([17, 33], dtype=torch.int32)
+    got = _decode_gpu(q, k, v, ks, vs, tables, lens, 128 ** -0.5)
+    want = oracle.decode_reference_fp32(q, k, v, ks, vs, tables, lens, 128 ** -0.5)
+    assert_decode_close(got, want, label="ref-20260720")
+    assert_decode_close(got, _oracle(q, k, v, ks, vs, tables, lens, 128 ** -0.5), label="ref-20260720-f64")
+
+
+@pytest.mark.parametrize("batch", [1, 2, 4, 8])
+def test_qwen_batch_context_matrix_scaled_fp8(batch):
+    """B x ctx matrix of the reference's Qwen test (32q/8kv, D=128, P=256), scaled FP8."""
+
+    require_gpu()
+    g = torch.Generator().manual_seed(20260711 + batch)
+    for ctx in (128, 256, 1024, 4096):
+        per = math.ceil(ctx / 256)
+        n = batch * per
+        q = torch.randn(batch, 32, 128, generator=g).to(torch.bfloat16)
+        k, ks = _quantize_cpu(torch.randn(n, 256, 8, 128, generator=g).to(torch.bfloat16))
+        v, vs = _quantize_cpu(torch.randn(n, 256, 8, 128, generator=g).to(torch.bfloat16))
+        tables = torch.randperm(n, generator=g).to(torch.int32).view(batch, per)
+        lens = torch.full((batch,), ctx, dtype=torch.int32)
+        got = _decode_gpu(q, k, v, ks, vs, tables, lens, 128 ** -0.5)
+        assert_decode_close(got, _oracle(q, k, v, ks, vs, tables, lens, 128 ** -0.5), label=f"B{batch} ctx{ctx}")
+
+
+def test_ragged_lengths_invalid_blocks_and_empty_rows():
+    """Ragged lengths (not multiples of the tile), -1 blocks inside a table, ctx=0 rows, a tiny max_context_len."""
+
+    require_gpu()
+    g = torch.Generator().manual_seed(5)
+    batch, width, pool = 6, 12, 80
+    q = torch.randn(batch, 32, 128, generator=g).to(torch.bfloat16)
+    k, ks = _quantize_cpu(torch.randn(pool, 256, 8, 128, generator=g).to(torch.bfloat16))
+    v, vs = _quantize_cpu(torch.randn(pool, 256, 8, 128, generator=g).to(torch.bfloat16))
+    tables = torch.randperm(pool, generator=g)[: batch * width].to(torch.int32).view(batch, width)
+    lens = torch.tensor([1, 33, 257, 3000, 0, 2900], dtype=torch.int32)
+    tables[3, 2] = -1          # a hole inside a long context: skipped, not an error
+    tables[5, 7:] = -1         # trailing holes
+    got = _decode_gpu(q, k, v, ks, vs, tables, lens, 0.0883)
+    want = _oracle(q, k, v, ks, vs, tables, lens, 0.0883)
+    assert_decode_close(got, want, label="ragged")
+    assert torch.all(got[4] == 0), "ctx=0 row must be zeros"
+    got2 = _decode_gpu(q, k, v, ks, vs, tables, lens, 0.0883, max_ctx=40)
+    assert_decode_close(got2, _oracle(q, k, v, ks, vs, tables, lens, 0.0883, max_ctx=40), label="max_ctx=40")
+
+
+@pytest.mark.parametrize("qdtype", [torch.float16, torch.float32])
+def test_query_dtypes_and_strided_query(qdtype):
+    require_gpu()
+    g = torch.Generator().manual_seed(9)
+    pool = 40
+    qfull = torch.randn(3, 64, 128, generator=g).to(qdtype)
+    q = qfull[:, ::2]  # non-contiguous head stride
+    k, ks = _quantize_cpu(torch.randn(pool, 256, 8, 128, generator=g).to(torch.bfloat16))
+    v, vs = _quantize_cpu(torch.randn(pool, 256, 8, 128, generator=g).to(torch.bfloat16))
+    tables = torch.randperm(pool, generator=g)[:36].to(torch.int32).view(3, 12)
+    lens = torch.tensor([700, 3072, 2048], dtype=torch.int32)
+    got = _decode_gpu(q, k, v, ks, vs, tables, lens, 128 ** -0.5)
+    assert got.dtype == qdtype
+    assert_decode_close(got, _oracle(q, k, v, ks, vs, tables, lens, 128 ** -0.5), label=str(qdtype))
+
+
+def test_small_gqa_generic_path_and_unscaled_caches():
+    """head_dim 16 / page 4 (generic kernel), unit-scale FP8 and bf16 caches."""
+
+    require_gpu()
+    g = torch.Generator().manual_seed(20260625 + 16 + 4)
+    q = torch.randn(3, 4, 16, generator=g).to(torch.bfloat16)
+    k_src = torch.randn(9, 4, 2, 16, generator=g).to(torch.bfloat16)
+    v_src = torch.randn(9, 4, 2, 16, generator=g).to(torch.bfloat16)
+    tables = torch.tensor([[0, -1, -1], [1, 2, -1], [3, 4, 5]], dtype=torch.int32)
+    lens = torch.tensor([1, 5, 9], dtype=torch.int32)
+    # bf16 cache
+    got = _decode_gpu(q, k_src, v_src, None, None, tables, lens, 0.25)
+    assert_decode_close(got, _oracle(q, k_src, v_src, None, None, tables, lens, 0.25), label="bf16 cache")
+    # unit-scale fp8
+    k8, v8 = k_src.to(FP8), v_src.to(FP8)
+    got = _decode_gpu(q, k8, v8, None, None, tables, lens, 0.25)
+    assert_decode_close(got, _oracle(q, k8, v8, None, None, tables, lens, 0.25), label="unit fp8")
+    # scaled fp8 at head_dim 16
+    k, ks = _quantize_cpu(k_src * 9)
+    v, vs = _quantize_cpu(v_src * 3)
+    got = _decode_gpu(q, k, v, ks, vs, tables, lens, 0.25)
+    assert_decode_close(got, _oracle(q, k, v, ks, vs, tables, lens, 0.25), label="scaled D16")
+
+
+def test_unit_scale_fp8_fast_path():
+    require_gpu()
+    g = torch.Generator().manual_seed(21)
+    q = torch.randn(2, 32, 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(10, 256, 8, 128, generator=g).to(FP8)
+    v = torch.randn(10, 256, 8, 128, generator=g).to(FP8)
+    tables = torch.arange(10, dtype=torch.int32).view(2, 5)
+    lens = torch.tensor([1111, 1280], dtype=torch.int32)
+    got = _decode_gpu(q, k, v, None, None, tables, lens, 128 ** -0.5)
+    assert_decode_close(got, _oracle(q, k, v, None, None, tables, lens, 128 ** -0.5), label="unit fp8 fast")
+
+
+@pytest.mark.parametrize("name", ["decode_single", "decode_qwen_vl"])
+def test_single_sequence_configs(name):
+    require_gpu()
+    from prism_infer import workloads
+
+    w = getattr(workloads, name)(torch.device("cuda"))
+    out = __import__("prism_infer.ops.paged_decode", fromlist=["x"]).paged_decode_attention(
+        w.q, w.k_cache, w.v_cache, w.block_tables, w.context_lens, w.scale,
+        k_scale_cache=w.k_scale, v_scale_cache=w.v_scale, max_context_len=w.max_context_len)
+    q, k, v, ks, vs, tables, lens, mx = compact_to_cpu(w)
+    assert_decode_close(out, _oracle(q, k, v, ks, vs, tables, lens, w.scale, mx), label=name)
+    # the reference CPU path (bf16 dequant + SDPA in bf16) agrees within the same tolerance
+    ref = oracle.decode_reference_qdtype(q, k, v, tables, lens, w.scale, k_scale_cache=ks, v_scale_cache=vs)
+    assert_decode_close(out, ref, atol=3e-2, label=name + " vs bf16 reference path")
+
+
+def test_mixed_batch_north_star_config():
+    """B=64, lengths U[1k,16k], 32 sequences sharing a 4096-token prefix, 8192-page pool."""
+
+    require_gpu()
+    from prism_infer.ops.paged_decode import paged_decode_attention
+    from prism_infer.workloads import decode_mixed
+
+    w = decode_mixed(torch.device("cuda"))
+    out = paged_decode_attention(w.q, w.k_cache, w.v_cache, w.block_tables, w.context_lens, w.scale,
+                                 k_scale_cache=w.k_scale, v_scale_cache=w.v_scale,
+                                 max_context_len=w.max_context_len)
+    q, k, v, ks, vs, tables, lens, mx = compact_to_cpu(w)
+    want = oracle.decode_kernel_semantics(q, k, v, tables, lens, w.scale, k_scale_cache=ks, v_scale_cache=vs,
+                                          max_context_len=mx, compute_dtype=torch.float32)
+    assert_decode_close(out, want, label="decode_mixed")
+
+
+def test_page_permutation_invariance_on_gpu():
+    """Same logical K/V in different physical pages gives the same output bit for bit."""
+
+    require_gpu()
+    g = torch.Generator().manual_seed(31)
+    q = torch.randn(2, 32, 128, generator=g).to(torch.bfloat16)
+    k, ks = _quantize_cpu(torch.randn(16, 256, 8, 128, generator=g).to(torch.bfloat16))
+    v, vs = _quantize_cpu(torch.randn(16, 256, 8, 128, generator=g).to(torch.bfloat16))
+    tables = torch.arange(16, dtype=torch.int32).view(2, 8)
+    lens = torch.tensor([2000, 1500], dtype=torch.int32)
+    perm = torch.randperm(16, generator=g)
+    inv = torch.argsort(perm)
+    kp = k.view(torch.uint8)[perm].view(FP8)
+    vp = v.view(torch.uint8)[perm].view(FP8)
+    tables_p = inv[tables.long()].to(torch.int32)
+    a = _decode_gpu(q, k, v, ks, vs, tables, lens, 0.09)
+    b = _decode_gpu(q, kp, vp, ks[perm], vs[perm], tables_p, lens, 0.09)
+    assert torch.equal(a, b)
+
+
+def test_graph_replay_follows_device_metadata():
+    """Captured decode follows updated context_lens / max_context_len / tables on replay."""
+
+    require_gpu()
+    from prism_infer.ops.paged_decode import paged_decode_attention
+
+    g = torch.Generator().manual_seed(20260722)
+    dev = torch.device("cuda")
+    q = torch.randn(2, 32, 128, generator=g).to(torch.bfloat16).to(dev)
+    k, ks = _quantize_cpu(torch.randn(8, 256, 8, 128, generator=g).to(torch.bfloat16))
+    v, vs = _quantize_cpu(torch.randn(8, 256, 8, 128, generator=g).to(torch.bfloat16))
+    kd, vd = k.view(torch.uint8).to(dev).view(FP8), v.view(torch.uint8).to(dev).view(FP8)
+    ksd, vsd = ks.to(dev), vs.to(dev)
+    tables = torch.arange(8, dtype=torch.int32, device=dev).view(2, 4)
+    lens = torch.tensor([4, 4], dtype=torch.int32, device=dev)
+    mx = torch.tensor([4], dtype=torch.int32, device=dev)
+    run = lambda: paged_decode_attention(q, kd, vd, tables, lens, 0.09, k_scale_cache=ksd, v_scale_cache=vsd,
+                                         max_context_len=mx)
+    run()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = run()
+    for new_len, swap in ((25, False), (1000, True), (700, False)):
+        lens.fill_(new_len)
+        mx.fill_(new_len)
+        if swap:
+            tables.copy_(tables.flip(0))
+        graph.replay()
+        torch.cuda.synchronize()
+        eager = run()
+        torch.cuda.synchronize()
+        want = _oracle(q.cpu(), k, v, ks, vs, tables.cpu(), lens.cpu(), 0.09)
+        assert_decode_close(captured, want, label=f"replay len {new_len}")
+        assert torch.equal(captured.cpu(), eager.cpu())
