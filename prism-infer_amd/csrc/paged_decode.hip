@@ -57,6 +57,7 @@ struct DecodeArgs {
   float* part_ml;   // [B][S][Hq][2]
   int batch, num_heads, num_kv_heads, groups, page_size, width, head_dim;
   int64_t num_blocks;
+  int q_vec;     // q rows are 16-byte aligned with unit dim stride
   int split;     // tokens per split (multiple of kTile)
   int max_splits;
   float scale_log2;  // sm_scale * log2(e)
@@ -129,21 +130,14 @@ __device__ __forceinline__ void load_tile(const DecodeArgs& a, int b, int h, int
   const int32_t* bt_row = a.bt + static_cast<int64_t>(b) * a.bt_sb;
   r.kvalid = 0;
   if constexpr (PAGE_ALIGNED) {
-    // The whole tile lies in one page.
+    // The whole tile lies in one page.  Branch-free: an absent block reads
+    // page 0 (always allocated on this path) and the tile is masked, so the
+    // compiler can keep this prefetch asynchronous.
     const int page = t0 / a.page_size;
     const int off0 = t0 - page * a.page_size;
-    const int32_t blk = bt_row[page * a.bt_sn];
-    if (blk < 0 || blk >= a.num_blocks) {
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh)
-        r.k[hh][0] = r.k[hh][1] = u32x4{0, 0, 0, 0};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        r.v[e] = u32x2{0, 0};
-        r.ksc[e] = r.vsc[e] = 0.f;
-      }
-      return;
-    }
+    const int32_t blk_raw = bt_row[page * a.bt_sn];
+    const bool blk_ok = blk_raw >= 0 && blk_raw < a.num_blocks;
+    const int64_t blk = blk_ok ? blk_raw : 0;
     const uint8_t* kbase = a.k + blk * a.k_sblk + static_cast<int64_t>(off0) * a.k_stok + h * a.k_sh;
     const uint8_t* vbase = a.v + blk * a.v_sblk + static_cast<int64_t>(off0) * a.v_stok + h * a.v_sh;
 #pragma unroll
@@ -152,19 +146,19 @@ __device__ __forceinline__ void load_tile(const DecodeArgs& a, int b, int h, int
       r.k[hh][0] = p[0];
       r.k[hh][1] = p[1];
     }
+    const float* ksb = a.ks + blk * a.ks_sblk + static_cast<int64_t>(off0) * a.ks_stok + h * a.ks_sh;
+    const float* vsb = a.vs + blk * a.vs_sblk + static_cast<int64_t>(off0) * a.vs_stok + h * a.vs_sh;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       const int tk = slot_token(g, e);
       r.v[e] = *reinterpret_cast<const u32x2*>(vbase + tk * a.v_stok + 8 * c);
       if (SCALED) {
-        const int64_t row = blk * a.ks_sblk + static_cast<int64_t>(off0 + tk) * a.ks_stok + h * a.ks_sh;
-        const int64_t vrow = blk * a.vs_sblk + static_cast<int64_t>(off0 + tk) * a.vs_stok + h * a.vs_sh;
-        r.ksc[e] = a.ks[row];
-        r.vsc[e] = a.vs[vrow];
+        r.ksc[e] = ksb[tk * a.ks_stok];
+        r.vsc[e] = vsb[tk * a.vs_stok];
       } else {
         r.ksc[e] = r.vsc[e] = 1.f;
       }
-      if (t0 + tk < t_end) r.kvalid |= 1u << e;
+      r.kvalid |= (blk_ok && t0 + tk < t_end) ? (1u << e) : 0u;
     }
   } else {
     // Tiles may straddle pages: resolve every row separately.
@@ -221,7 +215,7 @@ struct QOperand<PRISM_DTYPE_F16> {
   f16x8 hi[4];
 };
 
-template <int QDT, bool SCALED, bool PAGE_ALIGNED>
+template <int QDT, bool SCALED, bool PAGE_ALIGNED, bool QVEC>
 __global__ void __launch_bounds__(512)
 paged_decode_split_kernel(const DecodeArgs a) {
   const int lane = threadIdx.x & 63;
@@ -250,22 +244,52 @@ paged_decode_split_kernel(const DecodeArgs a) {
 
   // ---- query operand (B of QK): column c = q head h*G + c, k slot 8g+e of
   // chunk cc <-> dim 32g + 8cc + e.
+  // First tile's loads go out before the query is read and converted.
+  TileRegs ta, tb;
+  load_tile<SCALED, PAGE_ALIGNED>(a, b, h, g, c, t_begin, t_end, ta);
+
   QOperand<QDT> qop;
   {
+    // Lanes c >= G read q head h*G (a valid row) and zero their copy, so the
+    // loads carry no branch.
     const bool qvalid = c < G;
     const int64_t qbase = static_cast<int64_t>(b) * a.q_sb + static_cast<int64_t>(h * G + (qvalid ? c : 0)) * a.q_sh;
 #pragma unroll
     for (int cc = 0; cc < 4; ++cc) {
+      float x[8];
+      const int64_t d0 = 32 * g + 8 * cc;
+      if constexpr (QVEC) {
+        if constexpr (QDT == PRISM_DTYPE_F32) {
+          const floatx4* p = reinterpret_cast<const floatx4*>(static_cast<const float*>(a.q) + qbase + d0);
+          const floatx4 lo = p[0], hi = p[1];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) x[e] = lo[e], x[4 + e] = hi[e];
+        } else {
+          const u32x4 w = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.q) + qbase + d0);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            if constexpr (QDT == PRISM_DTYPE_BF16) {
+              x[2 * e] = bf16_bits_to_f32(w[e] & 0xFFFFu);
+              x[2 * e + 1] = bf16_bits_to_f32(w[e] >> 16);
+            } else {
+              x[2 * e] = f16_bits_to_f32(w[e] & 0xFFFFu);
+              x[2 * e + 1] = f16_bits_to_f32(w[e] >> 16);
+            }
+          }
+        }
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) x[e] = load_q<QDT>(a.q, qbase + (d0 + e) * a.q_sd);
+      }
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int d = 32 * g + 8 * cc + e;
-        const float x = qvalid ? load_q<QDT>(a.q, qbase + d * a.q_sd) : 0.f;
+        const float xv = qvalid ? x[e] : 0.f;
         if constexpr (QDT == PRISM_DTYPE_F16) {
-          qop.hi[cc][e] = static_cast<_Float16>(x);
+          qop.hi[cc][e] = static_cast<_Float16>(xv);
         } else {
-          const __bf16 hi = static_cast<__bf16>(x);
+          const __bf16 hi = static_cast<__bf16>(xv);
           qop.hi[cc][e] = hi;
-          if constexpr (QDT == PRISM_DTYPE_F32) qop.lo[cc][e] = static_cast<__bf16>(x - static_cast<float>(hi));
+          if constexpr (QDT == PRISM_DTYPE_F32) qop.lo[cc][e] = static_cast<__bf16>(xv - static_cast<float>(hi));
         }
       }
     }
@@ -277,11 +301,8 @@ paged_decode_split_kernel(const DecodeArgs a) {
   float m_run = -INFINITY;  // running max (log2 domain) of q head c
   float l_run = 0.f;        // this lane's share of the running sum
 
-  TileRegs cur, nxt;
-  load_tile<SCALED, PAGE_ALIGNED>(a, b, h, g, c, t_begin, t_end, cur);
-  for (int t0 = t_begin; t0 < t_end; t0 += kTile) {
-    if (t0 + kTile < t_end) load_tile<SCALED, PAGE_ALIGNED>(a, b, h, g, c, t0 + kTile, t_end, nxt);
-
+  // One 32-token tile of this wave's kv head: QK, online softmax, PV.
+  auto compute = [&](TileRegs& cur) {
     // ---- QK
     floatx4 sc[2];
 #pragma unroll
@@ -375,7 +396,23 @@ paged_decode_split_kernel(const DecodeArgs a) {
       acc[j + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa_lo, b1, acc[j + 1], 0, 0, 0);
     }
 
-    if (t0 + kTile < t_end) cur = nxt;
+  };
+
+  // Ping-pong prefetch: the next tile's loads are in flight while the current
+  // one is computed.  The loads are unconditional (past the end they re-read
+  // the current tile, a cache hit) so the waitcnt pass can count them exactly.
+  int t0 = t_begin;
+  while (true) {
+    int tn = (t0 + kTile < t_end) ? t0 + kTile : t0;
+    load_tile<SCALED, PAGE_ALIGNED>(a, b, h, g, c, tn, t_end, tb);
+    compute(ta);
+    t0 += kTile;
+    if (t0 >= t_end) break;
+    tn = (t0 + kTile < t_end) ? t0 + kTile : t0;
+    load_tile<SCALED, PAGE_ALIGNED>(a, b, h, g, c, tn, t_end, ta);
+    compute(tb);
+    t0 += kTile;
+    if (t0 >= t_end) break;
   }
 
   // ---- finish: total l per q head c, then per accumulator row 4g+i.
@@ -618,8 +655,13 @@ int launch_all(int stage, const DecodeArgs& args, const Geometry& geo, bool page
   if (stage != 2) {
     dim3 grid(args.batch, geo.max_splits);
     dim3 block(64 * args.num_kv_heads);
-#define PRISM_LAUNCH_SPLIT(S, A) \
-  hipLaunchKernelGGL((paged_decode_split_kernel<QDT, S, A>), grid, block, 0, stream, args)
+#define PRISM_LAUNCH_SPLIT(S, A)                                                                   \
+  do {                                                                                             \
+    if (args.q_vec)                                                                                \
+      hipLaunchKernelGGL((paged_decode_split_kernel<QDT, S, A, true>), grid, block, 0, stream, args);  \
+    else                                                                                           \
+      hipLaunchKernelGGL((paged_decode_split_kernel<QDT, S, A, false>), grid, block, 0, stream, args); \
+  } while (0)
     if (scaled && page_aligned) PRISM_LAUNCH_SPLIT(true, true);
     else if (scaled) PRISM_LAUNCH_SPLIT(true, false);
     else if (page_aligned) PRISM_LAUNCH_SPLIT(false, true);
@@ -716,7 +758,8 @@ extern "C" int prism_paged_decode_stage(
     const bool ok = aligned(k_cache, 16) && aligned(v_cache, 16) && k_strides[0] % 16 == 0 && k_strides[1] % 16 == 0 &&
                     k_strides[2] % 16 == 0 && v_strides[0] % 16 == 0 && v_strides[1] % 16 == 0 &&
                     v_strides[2] % 16 == 0;
-    if (!ok) geo.fast = false, geo.ws_bytes = 0, geo.max_splits = 1;
+    // The branch-free tile loader reads page 0 for absent blocks: needs >= 1 page.
+    if (!ok || num_blocks < 1) geo.fast = false, geo.ws_bytes = 0, geo.max_splits = 1;
   }
   if (geo.fast && geo.ws_bytes > 0) {
     if (!workspace || workspace_bytes < geo.ws_bytes) {
@@ -775,6 +818,11 @@ extern "C" int prism_paged_decode_stage(
   args.width = max_blocks_per_seq;
   args.head_dim = head_dim;
   args.num_blocks = num_blocks;
+  {
+    const int qsz = dtype_size(q_dtype);
+    const int64_t per16 = 16 / qsz;
+    args.q_vec = q_strides[2] == 1 && aligned(q, 16) && q_strides[0] % per16 == 0 && q_strides[1] % per16 == 0;
+  }
   args.split = geo.fast ? geo.split : 0;
   args.max_splits = geo.fast ? geo.max_splits : 1;
   args.scale_log2 = scale * kLog2e;
