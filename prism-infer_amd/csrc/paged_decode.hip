@@ -64,9 +64,16 @@ struct DecodeArgs {
   int cache_dtype;
 };
 
+// Read-only int32 metadata (block tables, context lengths) through the
+// constant address space: uniform indices then become scalar loads, which
+// neither wait on nor delay the vector-memory counter.
+__device__ __forceinline__ int32_t ld_meta(const int32_t* p) {
+  return *reinterpret_cast<const __attribute__((address_space(4))) int32_t*>(reinterpret_cast<uintptr_t>(p));
+}
+
 __device__ __forceinline__ int effective_len(const DecodeArgs& a, int b) {
-  int ctx = a.ctx[b];
-  int mx = *a.max_ctx;
+  int ctx = ld_meta(a.ctx + b);
+  int mx = ld_meta(a.max_ctx);
   int64_t cap = static_cast<int64_t>(a.width) * a.page_size;
   int64_t n = ctx < mx ? ctx : mx;
   if (n > cap) n = cap;
@@ -486,6 +493,495 @@ __global__ void __launch_bounds__(64) paged_decode_combine_kernel(const DecodeAr
   store_out<QDT>(a.out, base + (lane + 64) * a.o_sd, o1 * inv);
 }
 
+// ---------------------------------------------------------------- streaming path
+//
+// Persistent, tile-balanced kernel for the canonical page layout
+// ([num_blocks][P % 32 == 0][8 kv heads][128] FP8, scales [num_blocks][P][8]):
+//
+// * One workgroup (8 waves, wave = kv head) per CU.  The tiles of all
+//   sequences, concatenated in batch order (32 tokens each), are split into
+//   gridDim.x equal contiguous ranges, so every CU streams the same number of
+//   bytes whatever the context-length mix.  A range that spans several
+//   sequences emits one (m, l, acc) partial per (workgroup, sequence) pair; as
+//   ranges are contiguous and monotone, the pairs form a staircase and
+//   `wg + seq` indexes them uniquely.  The combine kernel merges them.
+// * Each tile is one contiguous slab per tensor: K [32 tok][8 h][128 B],
+//   V likewise, and the fp32 scales.  The workgroup copies a tile straight
+//   into LDS with global_load_lds (16 B per lane for K/V, 4 B for scales),
+//   double-buffered, so a full tile (66 KB) is in flight while the previous
+//   one is computed and no VGPRs hold prefetched data.  16-byte chunks of a
+//   head row are XOR-swizzled by token so that the row-parallel K reads and
+//   the transposed V reads hit distinct banks.  Scales are stored [head][tok]
+//   so a lane's four consecutive tokens are one 16-byte LDS read.
+// * K operands come from ds_read_b128; V operands from ds_read_b64_tr_b8,
+//   which hands lane i of each 16-lane group byte i of eight 16-byte rows --
+//   exactly the MFMA B-operand layout (k slot = token, column = dim).
+
+constexpr int kSKv = 8;                                // kv heads on this path
+constexpr int kSRow = kSKv * kHeadDim;                 // 1024 bytes per token row
+constexpr int kSKBytes = kTile * kSRow;                // 32 KB of K per tile
+constexpr int kSScaleBytes = kTile * kSKv * 4;         // 1 KB of k scales per tile
+constexpr int kSStage = 2 * kSKBytes + 2 * kSScaleBytes;  // 67584 bytes
+constexpr int kSMaxBatch = 1024;
+constexpr int kSThreads = 64 * kSKv;
+
+__device__ __forceinline__ int stream_swz(int t) { return ((t & 7) + ((t & 16) >> 2)) & 7; }
+
+typedef __attribute__((address_space(3))) void lds_void;
+
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const lds_void*)p));
+}
+
+
+// Global tile index -> (sequence, local tile) by walking the prefix sums.
+__device__ __forceinline__ void advance_seq(const int* tstart, int batch, int64_t tile, int& b) {
+  while (b + 1 < batch && tstart[b + 1] <= tile) ++b;
+  b = __builtin_amdgcn_readfirstlane(b);  // uniform: lets the metadata reads use scalar loads
+}
+
+// Locate a global tile: local token offset and physical block of sequence b.
+// Plain scalars (not a struct) so nothing is kept in memory across tiles.
+__device__ __forceinline__ void stream_tile(const DecodeArgs& a, const int* tstart, int64_t tile, int b, int& t0,
+                                            int& blk, int& ok) {
+  const int lt = __builtin_amdgcn_readfirstlane(static_cast<int>(tile - tstart[b]));
+  t0 = lt * kTile;
+  const int page = __builtin_amdgcn_readfirstlane(t0 / a.page_size);
+  const int32_t raw = ld_meta(a.bt + static_cast<int64_t>(b) * a.bt_sb + static_cast<int64_t>(page) * a.bt_sn);
+  ok = raw >= 0 && raw < a.num_blocks;
+  blk = ok ? raw : 0;
+}
+
+// Workgroup barrier without a memory fence.  __syncthreads() adds a
+// workgroup-scope release that waits for every outstanding load-to-LDS,
+// including the prefetch of the next tile; the stream kernel instead waits
+// for exactly the current tile's loads (s_waitcnt vmcnt) before this barrier.
+// The empty asm keeps the compiler from moving LDS accesses across it.
+__device__ __forceinline__ void stream_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// Eight ds_read_b64_tr_b8 of 16-byte chunks (j ^ swz) of one head row, issued
+// back to back with one lgkmcnt wait.  Written as asm because the compiler's
+// waitcnt pass cannot tell this LDS read from the in-flight load-to-LDS of the
+// other stage and would drain the whole prefetch (vmcnt(0)) before it.
+__device__ __forceinline__ void lds_read_tr8_x8(const uint8_t* row, int swz, uint64_t (&out)[8]) {
+  const uint32_t base = lds_addr(row);
+  uint32_t ad[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) ad[j] = base + ((j ^ swz) << 4);
+  asm volatile(
+      "ds_read_b64_tr_b8 %0, %8\n\t"
+      "ds_read_b64_tr_b8 %1, %9\n\t"
+      "ds_read_b64_tr_b8 %2, %10\n\t"
+      "ds_read_b64_tr_b8 %3, %11\n\t"
+      "ds_read_b64_tr_b8 %4, %12\n\t"
+      "ds_read_b64_tr_b8 %5, %13\n\t"
+      "ds_read_b64_tr_b8 %6, %14\n\t"
+      "ds_read_b64_tr_b8 %7, %15\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(out[0]), "=&v"(out[1]), "=&v"(out[2]), "=&v"(out[3]), "=&v"(out[4]), "=&v"(out[5]), "=&v"(out[6]),
+        "=&v"(out[7])
+      : "v"(ad[0]), "v"(ad[1]), "v"(ad[2]), "v"(ad[3]), "v"(ad[4]), "v"(ad[5]), "v"(ad[6]), "v"(ad[7])
+      : "memory");
+}
+
+// Issue the loads of one tile straight into `stage` (9 per lane: 4 K, 4 V,
+// 1 scale).  Written as asm so the compiler's waitcnt pass does not track
+// these load-to-LDS operations: it cannot tell the two stage buffers apart
+// and would otherwise drain every outstanding load before each LDS read.  The
+// kernel waits for them explicitly (s_waitcnt vmcnt + s_barrier); compiler-
+// issued vector loads elsewhere can only over-wait because of them.
+__device__ __forceinline__ void stream_issue(const DecodeArgs& a, int t0, int blk, uint8_t* stage, int wave,
+                                             int lane) {
+  const int off0 = t0 % a.page_size;
+  const uint8_t* kbase = a.k + blk * a.k_sblk + static_cast<int64_t>(off0) * kSRow;
+  const uint8_t* vbase = a.v + blk * a.v_sblk + static_cast<int64_t>(off0) * kSRow;
+  const uint8_t* kp[4];
+  const uint8_t* vp[4];
+  uint32_t lk[4], lv[4];
+  const uint32_t sbase = __builtin_amdgcn_readfirstlane(lds_addr(stage));
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int p = r * (kSThreads * 16) + wave * 1024 + lane * 16;  // LDS byte offset in the K slab
+    const int t = p >> 10;
+    const int hh = (p >> 7) & 7;
+    const int kk = ((p >> 4) & 7) ^ stream_swz(t);
+    const int goff = t * kSRow + hh * kHeadDim + kk * 16;
+    kp[r] = kbase + goff;
+    vp[r] = vbase + goff;
+    lk[r] = __builtin_amdgcn_readfirstlane(sbase + r * (kSThreads * 16) + wave * 1024);
+    lv[r] = lk[r] + kSKBytes;
+  }
+  // scales: waves 0-3 k, 4-7 v; LDS layout [head][token]
+  const int which = wave >> 2;
+  const int p = (wave & 3) * 64 + lane;  // 0..255
+  const int hh = p >> 5;
+  const int t = p & 31;
+  const float* sp = (which ? a.vs : a.ks) + blk * a.ks_sblk + static_cast<int64_t>(off0 + t) * kSKv + hh;
+  const uint32_t ls = __builtin_amdgcn_readfirstlane(sbase + 2 * kSKBytes + which * kSScaleBytes + (wave & 3) * 256);
+  asm volatile(
+      "s_mov_b32 m0, %[lk0]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[k0], off\n\t"
+      "s_mov_b32 m0, %[lv0]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v0], off\n\t"
+      "s_mov_b32 m0, %[lk1]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[k1], off\n\t"
+      "s_mov_b32 m0, %[lv1]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v1], off\n\t"
+      "s_mov_b32 m0, %[lk2]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[k2], off\n\t"
+      "s_mov_b32 m0, %[lv2]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v2], off\n\t"
+      "s_mov_b32 m0, %[lk3]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[k3], off\n\t"
+      "s_mov_b32 m0, %[lv3]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v3], off\n\t"
+      "s_mov_b32 m0, %[ls]\n\ts_nop 0\n\tglobal_load_lds_dword %[sp], off"
+      :
+      : [k0] "v"(kp[0]), [k1] "v"(kp[1]), [k2] "v"(kp[2]), [k3] "v"(kp[3]), [v0] "v"(vp[0]), [v1] "v"(vp[1]),
+        [v2] "v"(vp[2]), [v3] "v"(vp[3]), [sp] "v"(sp), [lk0] "s"(lk[0]), [lk1] "s"(lk[1]), [lk2] "s"(lk[2]),
+        [lk3] "s"(lk[3]), [lv0] "s"(lv[0]), [lv1] "s"(lv[1]), [lv2] "s"(lv[2]), [lv3] "s"(lv[3]), [ls] "s"(ls)
+      : "memory", "m0");
+}
+
+template <int QDT, bool QVEC>
+__device__ __forceinline__ void stream_load_q(const DecodeArgs& a, int b, int h, int g, int c, QOperand<QDT>& qop) {
+  const int G = a.groups;
+  const bool qvalid = c < G;
+  const int64_t qbase = static_cast<int64_t>(b) * a.q_sb + static_cast<int64_t>(h * G + (qvalid ? c : 0)) * a.q_sh;
+#pragma unroll
+  for (int cc = 0; cc < 4; ++cc) {
+    float x[8];
+    const int64_t d0 = 32 * g + 8 * cc;
+    if constexpr (QVEC) {
+      if constexpr (QDT == PRISM_DTYPE_F32) {
+        const floatx4* p = reinterpret_cast<const floatx4*>(static_cast<const float*>(a.q) + qbase + d0);
+        const floatx4 lo = p[0], hi = p[1];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[e] = lo[e], x[4 + e] = hi[e];
+      } else {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.q) + qbase + d0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if constexpr (QDT == PRISM_DTYPE_BF16) {
+            x[2 * e] = bf16_bits_to_f32(w[e] & 0xFFFFu);
+            x[2 * e + 1] = bf16_bits_to_f32(w[e] >> 16);
+          } else {
+            x[2 * e] = f16_bits_to_f32(w[e] & 0xFFFFu);
+            x[2 * e + 1] = f16_bits_to_f32(w[e] >> 16);
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = load_q<QDT>(a.q, qbase + (d0 + e) * a.q_sd);
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float xv = qvalid ? x[e] : 0.f;
+      if constexpr (QDT == PRISM_DTYPE_F16) {
+        qop.hi[cc][e] = static_cast<_Float16>(xv);
+      } else {
+        const __bf16 hi = static_cast<__bf16>(xv);
+        qop.hi[cc][e] = hi;
+        if constexpr (QDT == PRISM_DTYPE_F32) qop.lo[cc][e] = static_cast<__bf16>(xv - static_cast<float>(hi));
+      }
+    }
+  }
+}
+
+template <int QDT, bool QVEC>
+__global__ void __launch_bounds__(kSThreads, 1)
+paged_decode_stream_kernel(const DecodeArgs a) {
+  // Two separate stage buffers (not one array): the compiler's LDS-DMA wait
+  // tracking can then tell the stage being read from the one being filled.
+  __shared__ __attribute__((aligned(16))) uint8_t stage0[kSStage];
+  __shared__ __attribute__((aligned(16))) uint8_t stage1[kSStage];
+  __shared__ int tstart[kSMaxBatch + 1];
+  __shared__ int scan[kSThreads];
+  const int lane = threadIdx.x & 63;
+  const int h = threadIdx.x >> 6;
+  const int g = lane >> 4;
+  const int c = lane & 15;
+  const int G = a.groups;
+  const int B = a.batch;
+
+  // ---- prefix sums of per-sequence tile counts (every workgroup computes them)
+  if (threadIdx.x == 0) tstart[0] = 0;
+  for (int base = 0; base < B; base += kSThreads) {
+    __syncthreads();
+    const int bb = base + threadIdx.x;
+    const int n = bb < B ? (effective_len(a, bb) + kTile - 1) / kTile : 0;
+    // inclusive scan of n across the block (Hillis-Steele through LDS)
+    scan[threadIdx.x] = n;
+    __syncthreads();
+    for (int off = 1; off < kSThreads; off <<= 1) {
+      const int v = threadIdx.x >= off ? scan[threadIdx.x - off] : 0;
+      __syncthreads();
+      scan[threadIdx.x] += v;
+      __syncthreads();
+    }
+    if (bb < B) tstart[bb + 1] = tstart[base] + scan[threadIdx.x];
+  }
+  __syncthreads();
+  const int64_t total = tstart[B];
+  const int64_t nwg = gridDim.x;
+  const int64_t s = static_cast<int64_t>(blockIdx.x) * total / nwg;
+  const int64_t e = static_cast<int64_t>(blockIdx.x + 1) * total / nwg;
+  if (s >= e) return;  // uniform across the workgroup
+
+  int b = 0;
+  advance_seq(tstart, B, s, b);
+  int cur_t0, cur_blk, cur_ok;
+  stream_tile(a, tstart, s, b, cur_t0, cur_blk, cur_ok);
+  stream_issue(a, cur_t0, cur_blk, stage0, h, lane);
+
+  QOperand<QDT> qop;
+  stream_load_q<QDT, QVEC>(a, b, h, g, c, qop);
+  int n_eff = effective_len(a, b);
+
+  floatx4 acc[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY;
+  float l_run = 0.f;
+
+  // One tile: prefetch the next into `next_stage`, compute `stage`.
+  // Returns false after the last tile of this workgroup's range.
+  auto step = [&](uint8_t* stage, uint8_t* next_stage, int64_t tile) -> bool {
+    const bool more = tile + 1 < e;
+    int bn = b;
+    int nxt_t0 = cur_t0, nxt_blk = cur_blk, nxt_ok = cur_ok;
+    if (more) {
+      advance_seq(tstart, B, tile + 1, bn);
+      stream_tile(a, tstart, tile + 1, bn, nxt_t0, nxt_blk, nxt_ok);
+      stream_issue(a, nxt_t0, nxt_blk, next_stage, h, lane);
+      __builtin_amdgcn_s_waitcnt(0xF79);  // vmcnt(9): this tile's 9 loads have landed
+    } else {
+      __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0)
+    }
+    stream_barrier();
+
+    if (cur_ok) {
+      const uint8_t* lk = stage;
+      const uint8_t* lv = stage + kSKBytes;
+      const float* lks = reinterpret_cast<const float*>(stage + 2 * kSKBytes);
+      const float* lvs = lks + kTile * kSKv;
+      // ---- QK
+      floatx4 sc[2];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const int t = c + 16 * hh;
+        const uint8_t* row = lk + t * kSRow + h * kHeadDim;
+        const u32x4 k0 = *reinterpret_cast<const u32x4*>(row + (((2 * g) ^ stream_swz(t)) << 4));
+        const u32x4 k1 = *reinterpret_cast<const u32x4*>(row + (((2 * g + 1) ^ stream_swz(t)) << 4));
+        floatx4 accs = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+          const u32x4& kw = (cc < 2) ? k0 : k1;
+          const uint32_t w0 = kw[(cc & 1) * 2];
+          const uint32_t w1 = kw[(cc & 1) * 2 + 1];
+          if constexpr (QDT == PRISM_DTYPE_F16) {
+            accs = __builtin_amdgcn_mfma_f32_16x16x32_f16(fp8x8_to_f16x8(w0, w1), qop.hi[cc], accs, 0, 0, 0);
+          } else {
+            const bf16x8 kb = fp8x8_to_bf16x8(w0, w1);
+            accs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qop.hi[cc], accs, 0, 0, 0);
+            if constexpr (QDT == PRISM_DTYPE_F32)
+              accs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qop.lo[cc], accs, 0, 0, 0);
+          }
+        }
+        sc[hh] = accs;
+      }
+      // scales of this lane's 8 tokens (4g..4g+3, 16+4g..16+4g+3)
+      const floatx4 ks0 = *reinterpret_cast<const floatx4*>(lks + h * kTile + 4 * g);
+      const floatx4 ks1 = *reinterpret_cast<const floatx4*>(lks + h * kTile + 16 + 4 * g);
+      const floatx4 vs0 = *reinterpret_cast<const floatx4*>(lvs + h * kTile + 4 * g);
+      const floatx4 vs1 = *reinterpret_cast<const floatx4*>(lvs + h * kTile + 16 + 4 * g);
+      // ---- online softmax
+      float x[8];
+      float tmax = -INFINITY;
+      uint32_t valid = 0;
+#pragma unroll
+      for (int ee = 0; ee < 8; ++ee) {
+        const int tk = slot_token(g, ee);
+        const bool ok = (cur_t0 + tk < n_eff) && c < G;
+        valid |= (cur_t0 + tk < n_eff) ? (1u << ee) : 0u;
+        const float ksv = ee < 4 ? ks0[ee] : ks1[ee - 4];
+        const float v = sc[ee >> 2][ee & 3] * (ksv * a.scale_log2);
+        x[ee] = ok ? v : -INFINITY;
+        tmax = fmaxf(tmax, x[ee]);
+      }
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+      const float m_new = fmaxf(m_run, tmax);
+      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+      const float alpha = exp2f(m_run - m_use);
+      m_run = m_new;
+      float psum = 0.f;
+      bf16x8 pa, pa_lo;
+#pragma unroll
+      for (int ee = 0; ee < 8; ++ee) {
+        const float p = exp2f(x[ee] - m_use);
+        psum += p;
+        const float vsv = ee < 4 ? vs0[ee] : vs1[ee - 4];
+        const float pv = ((valid >> ee) & 1u) ? p * vsv : 0.f;
+        const __bf16 hi = static_cast<__bf16>(pv);
+        pa[ee] = hi;
+        pa_lo[ee] = static_cast<__bf16>(pv - static_cast<float>(hi));
+      }
+      l_run = l_run * alpha + psum;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float ai = __shfl(alpha, 4 * g + i);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j][i] *= ai;
+      }
+      // ---- PV: lane (g, i) points at token slot_token(g, i/2), half i&1
+      {
+        const int r = c >> 1;
+        const int t = slot_token(g, r);
+        // byte r of a transposed read comes from k slot r: keep only the bytes
+        // of attended tokens (rows past the sequence end may hold NaN codes and
+        // the MFMA would turn 0 * NaN into NaN).
+        uint32_t keep0 = 0, keep1 = 0;
+#pragma unroll
+        for (int rr = 0; rr < 4; ++rr) {
+          keep0 |= ((valid >> rr) & 1u) ? (0xFFu << (8 * rr)) : 0u;
+          keep1 |= ((valid >> (rr + 4)) & 1u) ? (0xFFu << (8 * rr)) : 0u;
+        }
+        const uint8_t* vrow = lv + t * kSRow + h * kHeadDim + ((c & 1) << 3);
+        uint64_t vt[8];
+        lds_read_tr8_x8(vrow, stream_swz(t), vt);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          const uint32_t w0 = static_cast<uint32_t>(vt[j]) & keep0;
+          const uint32_t w1 = static_cast<uint32_t>(vt[j] >> 32) & keep1;
+          const bf16x8 bv = fp8x8_to_bf16x8(w0, w1);
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, bv, acc[j], 0, 0, 0);
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa_lo, bv, acc[j], 0, 0, 0);
+        }
+      }
+    }
+    stream_barrier();  // every wave is done with this stage before it is refilled
+
+    const bool seq_ends = !more || bn != b;
+    if (seq_ends) {
+      // flush the (workgroup, sequence) partial
+      float l_tot = l_run + __shfl_xor(l_run, 16);
+      l_tot += __shfl_xor(l_tot, 32);
+      const int64_t pidx = static_cast<int64_t>(blockIdx.x) + b;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int qr = 4 * g + i;
+        const float li = __shfl(l_tot, qr);
+        const float mi = __shfl(m_run, qr);
+        if (qr < G) {
+          const int64_t row = pidx * a.num_heads + h * G + qr;
+          float* dst = a.part_acc + row * kHeadDim + c;
+#pragma unroll
+          for (int j = 0; j < 8; ++j) dst[16 * j] = acc[j][i];
+          if (c == 0) {
+            a.part_ml[row * 2 + 0] = mi;
+            a.part_ml[row * 2 + 1] = li;
+          }
+        }
+      }
+      if (more) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+        m_run = -INFINITY;
+        l_run = 0.f;
+        b = bn;
+        n_eff = effective_len(a, b);
+        stream_load_q<QDT, QVEC>(a, b, h, g, c, qop);
+      }
+    }
+    cur_t0 = nxt_t0;
+    cur_blk = nxt_blk;
+    cur_ok = nxt_ok;
+    return more;
+  };
+
+  for (int64_t tile = s;;) {
+    if (!step(stage0, stage1, tile++)) break;
+    if (!step(stage1, stage0, tile++)) break;
+  }
+}
+
+// Merge the streaming partials: grid (batch, num_heads), one wave each.
+// The contributing workgroups are handled lane-parallel: lane i reads the
+// (m, l) of workgroup w_lo + i (+64k), the weights go through LDS, then each
+// lane accumulates two output dims over the workgroups.
+constexpr int kSMaxWg = 1024;
+
+template <int QDT>
+__global__ void __launch_bounds__(64) paged_decode_stream_combine_kernel(const DecodeArgs a, int nwg) {
+  __shared__ float wts[kSMaxWg];
+  const int b = blockIdx.x;
+  const int hq = blockIdx.y;
+  const int lane = threadIdx.x;
+  int64_t before = 0, total = 0;
+  for (int bb = lane; bb < a.batch; bb += 64) {
+    const int64_t n = (effective_len(a, bb) + kTile - 1) / kTile;
+    total += n;
+    if (bb < b) before += n;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    total += __shfl_xor(total, off);
+    before += __shfl_xor(before, off);
+  }
+  const int64_t n_b = (effective_len(a, b) + kTile - 1) / kTile;
+  const int64_t base = static_cast<int64_t>(b) * a.o_sb + static_cast<int64_t>(hq) * a.o_sh;
+  if (n_b == 0) {
+    store_out<QDT>(a.out, base + lane * a.o_sd, 0.f);
+    store_out<QDT>(a.out, base + (lane + 64) * a.o_sd, 0.f);
+    return;
+  }
+  // workgroups whose range [w*total/nwg, (w+1)*total/nwg) meets [before, before + n_b)
+  const int64_t first_tile = before, last_tile = before + n_b - 1;
+  auto owner = [&](int64_t tile) {  // the workgroup whose range holds `tile`
+    int64_t w = (tile * nwg) / total;
+    while (w > 0 && (w * total) / nwg > tile) --w;
+    while (((w + 1) * total) / nwg <= tile) ++w;
+    return w;
+  };
+  const int64_t w_lo = owner(first_tile);
+  const int64_t w_hi = owner(last_tile);
+  const int count = static_cast<int>(w_hi - w_lo + 1);
+  // pass 1: (m, l) lane-parallel; workgroups with an empty range wrote nothing
+  float m_max = -INFINITY;
+  for (int i = lane; i < count; i += 64) {
+    const int64_t w = w_lo + i;
+    const bool has = (w * total) / nwg < ((w + 1) * total) / nwg;
+    const float m = has ? a.part_ml[((w + b) * a.num_heads + hq) * 2] : -INFINITY;
+    wts[i] = m;
+    m_max = fmaxf(m_max, m);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) m_max = fmaxf(m_max, __shfl_xor(m_max, off));
+  const float m_use = (m_max == -INFINITY) ? 0.f : m_max;
+  float l_sum = 0.f;
+  for (int i = lane; i < count; i += 64) {
+    const int64_t w = w_lo + i;
+    const float m = wts[i];
+    const float wgt = (m == -INFINITY) ? 0.f : exp2f(m - m_use);
+    if (wgt > 0.f) l_sum += wgt * a.part_ml[((w + b) * a.num_heads + hq) * 2 + 1];
+    wts[i] = wgt;
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) l_sum += __shfl_xor(l_sum, off);
+  __syncthreads();
+  // pass 2: weighted sum of the accumulators
+  float o0 = 0.f, o1 = 0.f;
+#pragma unroll 4
+  for (int i = 0; i < count; ++i) {
+    const float wgt = wts[i];
+    if (wgt == 0.f) continue;
+    const float* src = a.part_acc + ((w_lo + i + b) * a.num_heads + hq) * kHeadDim;
+    o0 += wgt * src[lane];
+    o1 += wgt * src[lane + 64];
+  }
+  const float inv = l_sum > 0.f ? 1.f / l_sum : 0.f;
+  store_out<QDT>(a.out, base + lane * a.o_sd, o0 * inv);
+  store_out<QDT>(a.out, base + (lane + 64) * a.o_sd, o1 * inv);
+}
+
 // ---------------------------------------------------------------- generic path
 
 constexpr int kGenericMaxDim = 256;
@@ -595,7 +1091,16 @@ struct Geometry {
   int max_splits;
   int64_t ws_bytes;
   int64_t acc_off, ml_off;
+  // streaming path (canonical layout only; chosen per call from the strides)
+  bool stream_shape;
+  int stream_nwg;
+  int64_t stream_acc_off, stream_ml_off;
 };
+
+bool stream_disabled() {
+  const char* env = getenv("PRISM_DECODE_PATH");
+  return env && env[0] == 's' && env[1] == 'p';  // "split" forces the per-split kernel
+}
 
 bool fast_geometry(int num_heads, int num_kv_heads, int head_dim, int cache_dtype) {
   if (cache_dtype != PRISM_DTYPE_FP8_E4M3FN || head_dim != kHeadDim) return false;
@@ -634,17 +1139,48 @@ Geometry geometry(int batch, int num_heads, int num_kv_heads, int head_dim, int 
   geo.max_splits = static_cast<int>(cap > 0 ? ceil_div(cap, geo.split) : 1);
   if (geo.max_splits <= 1) {
     geo.ws_bytes = 0;
-    return geo;
+  } else {
+    const int64_t rows = static_cast<int64_t>(batch) * geo.max_splits * num_heads;
+    geo.acc_off = 0;
+    geo.ml_off = align_up(rows * head_dim * 4, 256);
+    geo.ws_bytes = geo.ml_off + align_up(rows * 2 * 4, 256);
   }
-  const int64_t rows = static_cast<int64_t>(batch) * geo.max_splits * num_heads;
-  geo.acc_off = 0;
-  geo.ml_off = align_up(rows * head_dim * 4, 256);
-  geo.ws_bytes = geo.ml_off + align_up(rows * 2 * 4, 256);
+  geo.stream_shape = num_kv_heads == kSKv && page_size % kTile == 0 && batch <= kSMaxBatch && !stream_disabled() &&
+                     device_cu_count() <= kSMaxWg;
+  if (geo.stream_shape) {
+    geo.stream_nwg = device_cu_count();
+    const int64_t rows = (static_cast<int64_t>(geo.stream_nwg) + batch) * num_heads;
+    geo.stream_acc_off = 0;
+    geo.stream_ml_off = align_up(rows * head_dim * 4, 256);
+    const int64_t need = geo.stream_ml_off + align_up(rows * 2 * 4, 256);
+    if (need > geo.ws_bytes) geo.ws_bytes = need;
+  }
   return geo;
 }
 
 template <int QDT>
-int launch_all(int stage, const DecodeArgs& args, const Geometry& geo, bool page_aligned, hipStream_t stream) {
+int launch_stream(int stage, const DecodeArgs& args, const Geometry& geo, hipStream_t stream) {
+  if (stage != 2) {
+    if (args.q_vec)
+      hipLaunchKernelGGL((paged_decode_stream_kernel<QDT, true>), dim3(geo.stream_nwg), dim3(kSThreads), 0, stream, args);
+    else
+      hipLaunchKernelGGL((paged_decode_stream_kernel<QDT, false>), dim3(geo.stream_nwg), dim3(kSThreads), 0, stream,
+                         args);
+    int rc = check_launch("paged_decode_stream_kernel launch");
+    if (rc) return rc;
+  }
+  if (stage != 1) {
+    hipLaunchKernelGGL(paged_decode_stream_combine_kernel<QDT>, dim3(args.batch, args.num_heads), dim3(64), 0, stream,
+                       args, geo.stream_nwg);
+    return check_launch("paged_decode_stream_combine_kernel launch");
+  }
+  return PRISM_OK;
+}
+
+template <int QDT>
+int launch_all(int stage, const DecodeArgs& args, const Geometry& geo, bool page_aligned, bool use_stream,
+               hipStream_t stream) {
+  if (use_stream) return launch_stream<QDT>(stage, args, geo, stream);
   const bool scaled = args.ks != nullptr;
   if (!geo.fast) {
     if (stage == 2) return PRISM_OK;
@@ -828,11 +1364,21 @@ extern "C" int prism_paged_decode_stage(
   args.scale_log2 = scale * kLog2e;
   args.cache_dtype = cache_dtype;
   const bool page_aligned = (page_size % kTile) == 0;
+  // Streaming path: canonical contiguous page layout with scales.
+  const bool use_stream = geo.fast && geo.stream_shape && k_scale != nullptr && k_strides[1] == kSRow &&
+                          k_strides[2] == kHeadDim && v_strides[1] == kSRow && v_strides[2] == kHeadDim &&
+                          ks_strides[1] == kSKv && ks_strides[2] == 1 && vs_strides[1] == kSKv && vs_strides[2] == 1 &&
+                          ks_strides[0] == vs_strides[0] && aligned(k_scale, 16) && aligned(v_scale, 16) &&
+                          ks_strides[0] % 4 == 0;
+  if (use_stream) {
+    args.part_acc = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + geo.stream_acc_off);
+    args.part_ml = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + geo.stream_ml_off);
+  }
   hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
   switch (q_dtype) {
-    case PRISM_DTYPE_BF16: return launch_all<PRISM_DTYPE_BF16>(stage, args, geo, page_aligned, stream);
-    case PRISM_DTYPE_F16: return launch_all<PRISM_DTYPE_F16>(stage, args, geo, page_aligned, stream);
-    default: return launch_all<PRISM_DTYPE_F32>(stage, args, geo, page_aligned, stream);
+    case PRISM_DTYPE_BF16: return launch_all<PRISM_DTYPE_BF16>(stage, args, geo, page_aligned, use_stream, stream);
+    case PRISM_DTYPE_F16: return launch_all<PRISM_DTYPE_F16>(stage, args, geo, page_aligned, use_stream, stream);
+    default: return launch_all<PRISM_DTYPE_F32>(stage, args, geo, page_aligned, use_stream, stream);
   }
 }
 
