@@ -107,6 +107,8 @@ def main() -> int:
     parser.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-extras", action="store_true", help="skip store/compaction/single-sequence extras")
+    parser.add_argument("--copy-probe", action="store_true",
+                        help="only run a plain 1 GiB device copy (reference for rocprof FETCH/WRITE_SIZE scaling)")
     args = parser.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -128,6 +130,14 @@ def main() -> int:
     _native.lib()
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
+    if args.copy_probe:
+        src = torch.ones(1 << 30, dtype=torch.uint8, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_probe_bytes_read": src.numel(), "copy_probe_bytes_written": dst.numel(), "calls": 5}))
+        return 0
 
     # ---- headline workload: decode_mixed, one pool per rotated layer
     _log(f"building decode_mixed x {args.layers} layers")

@@ -62,6 +62,7 @@ struct DecodeArgs {
   int max_splits;
   float scale_log2;  // sm_scale * log2(e)
   int cache_dtype;
+  int debug;         // measurement aid for the stream kernel (0 in normal use)
 };
 
 // Read-only int32 metadata (block tables, context lengths) through the
@@ -105,19 +106,22 @@ __device__ __forceinline__ f16x2 fp8x2_to_f16x2(uint32_t w) {
   return __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, HI);
 }
 
-// 8 fp8 bytes (two dwords) -> 8 bf16 in order.
+// 8 fp8 bytes (two dwords) -> 8 bf16 in order.  Assembled from whole dwords
+// (see fp8x4_to_bf16x4_bits for why lanes are not extracted one by one).
 __device__ __forceinline__ bf16x8 fp8x8_to_bf16x8(uint32_t w0, uint32_t w1) {
-  bf16x2 a = fp8x2_to_bf16x2<false>(w0), b = fp8x2_to_bf16x2<true>(w0);
-  bf16x2 c = fp8x2_to_bf16x2<false>(w1), d = fp8x2_to_bf16x2<true>(w1);
-  bf16x8 r = {a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
-  return r;
+  const u32x4 r = {__builtin_bit_cast(uint32_t, fp8x2_to_bf16x2<false>(w0)),
+                   __builtin_bit_cast(uint32_t, fp8x2_to_bf16x2<true>(w0)),
+                   __builtin_bit_cast(uint32_t, fp8x2_to_bf16x2<false>(w1)),
+                   __builtin_bit_cast(uint32_t, fp8x2_to_bf16x2<true>(w1))};
+  return __builtin_bit_cast(bf16x8, r);
 }
 
 __device__ __forceinline__ f16x8 fp8x8_to_f16x8(uint32_t w0, uint32_t w1) {
-  f16x2 a = fp8x2_to_f16x2<false>(w0), b = fp8x2_to_f16x2<true>(w0);
-  f16x2 c = fp8x2_to_f16x2<false>(w1), d = fp8x2_to_f16x2<true>(w1);
-  f16x8 r = {a[0], a[1], b[0], b[1], c[0], c[1], d[0], d[1]};
-  return r;
+  const u32x4 r = {__builtin_bit_cast(uint32_t, fp8x2_to_f16x2<false>(w0)),
+                   __builtin_bit_cast(uint32_t, fp8x2_to_f16x2<true>(w0)),
+                   __builtin_bit_cast(uint32_t, fp8x2_to_f16x2<false>(w1)),
+                   __builtin_bit_cast(uint32_t, fp8x2_to_f16x2<true>(w1))};
+  return __builtin_bit_cast(f16x8, r);
 }
 
 struct TileRegs {
@@ -496,36 +500,47 @@ __global__ void __launch_bounds__(64) paged_decode_combine_kernel(const DecodeAr
 // ---------------------------------------------------------------- streaming path
 //
 // Persistent, tile-balanced kernel for the canonical page layout
-// ([num_blocks][P % 32 == 0][8 kv heads][128] FP8, scales [num_blocks][P][8]):
+// ([num_blocks][P % 16 == 0][8 kv heads][128] FP8, scales [num_blocks][P][8]):
 //
-// * One workgroup (8 waves, wave = kv head) per CU.  The tiles of all
-//   sequences, concatenated in batch order (32 tokens each), are split into
-//   gridDim.x equal contiguous ranges, so every CU streams the same number of
-//   bytes whatever the context-length mix.  A range that spans several
-//   sequences emits one (m, l, acc) partial per (workgroup, sequence) pair; as
-//   ranges are contiguous and monotone, the pairs form a staircase and
-//   `wg + seq` indexes them uniquely.  The combine kernel merges them.
-// * Each tile is one contiguous slab per tensor: K [32 tok][8 h][128 B],
-//   V likewise, and the fp32 scales.  The workgroup copies a tile straight
-//   into LDS with global_load_lds (16 B per lane for K/V, 4 B for scales),
-//   double-buffered, so a full tile (66 KB) is in flight while the previous
-//   one is computed and no VGPRs hold prefetched data.  16-byte chunks of a
-//   head row are XOR-swizzled by token so that the row-parallel K reads and
-//   the transposed V reads hit distinct banks.  Scales are stored [head][tok]
-//   so a lane's four consecutive tokens are one 16-byte LDS read.
-// * K operands come from ds_read_b128; V operands from ds_read_b64_tr_b8,
-//   which hands lane i of each 16-lane group byte i of eight 16-byte rows --
-//   exactly the MFMA B-operand layout (k slot = token, column = dim).
+// * One workgroup (8 waves, wave = kv head) per CU.  The 16-token tiles of all
+//   sequences, concatenated in batch order, are split into gridDim.x equal
+//   contiguous ranges, so every CU streams the same number of bytes whatever
+//   the context-length mix.  A range spanning several sequences emits one
+//   (m, l, acc) partial per (workgroup, sequence) pair; as ranges are
+//   contiguous and monotone the pairs form a staircase and `wg + seq` indexes
+//   them uniquely.  The combine kernel merges them.
+// * A tile is one contiguous slab per tensor (K [16 tok][8 h][128 B], V
+//   likewise, and the fp32 scales).  The workgroup copies tiles straight into
+//   LDS with global_load_lds (16 B per lane), four stages deep, so three tiles
+//   (about 100 KB) are in flight while one is computed and no VGPRs hold
+//   prefetched data.  16-byte chunks of a head row are XOR-swizzled by token
+//   so row-parallel K reads and transposed V reads spread over the banks.
+//   Scales are stored [head][token] so a lane's four tokens are one 16-byte read.
+// * QK: 4 MFMA f32_16x16x32_bf16 per tile (A = K rows fp8 -> bf16, exact;
+//   B = Q^T).  Lane (g, c) gets the scores of q head c for tokens 4g..4g+3.
+// * PV: MFMA f32_16x16x16_bf16, whose four k slots per lane are exactly those
+//   four tokens, so P needs no data movement; P * v_scale is split into a
+//   bf16 hi/lo pair (two MFMAs) for fp32-like accuracy.  The V operand comes
+//   from ds_read_b64_tr_b8, which hands lane i of each 16-lane group byte i of
+//   eight 16-byte rows: rows 0-3 = tokens 4g..4g+3 at dims 16j.., rows 4-7 =
+//   the same tokens at dims 16(j+1).., i.e. two N-tiles per read.
+// * Softmax rescaling is lazy: the running max moves only when a score
+//   exceeds it by more than 2^8, which after the first tiles is rare.
 
-constexpr int kSKv = 8;                                // kv heads on this path
-constexpr int kSRow = kSKv * kHeadDim;                 // 1024 bytes per token row
-constexpr int kSKBytes = kTile * kSRow;                // 32 KB of K per tile
-constexpr int kSScaleBytes = kTile * kSKv * 4;         // 1 KB of k scales per tile
-constexpr int kSStage = 2 * kSKBytes + 2 * kSScaleBytes;  // 67584 bytes
+constexpr int kSKv = 8;                                 // kv heads on this path
+constexpr int kSTile = 16;                              // tokens per tile
+constexpr int kSStages = 2;                             // pipeline depth per workgroup
+constexpr int kSWgPerCu = 2;                            // independent workgroups per CU
+constexpr int kSRow = kSKv * kHeadDim;                  // 1024 bytes per token row
+constexpr int kSKBytes = kSTile * kSRow;                // 16 KB of K per tile
+constexpr int kSScaleBytes = kSTile * kSKv * 4;         // 512 B of k scales per tile
+constexpr int kSStage = 2 * kSKBytes + 2 * kSScaleBytes;  // 33792 bytes
 constexpr int kSMaxBatch = 1024;
 constexpr int kSThreads = 64 * kSKv;
+constexpr int kSLoadsPerStage = 5;                      // per lane: 2 K, 2 V, 1 scale
+constexpr float kSRescaleThreshold = 8.0f;              // log2 domain
 
-__device__ __forceinline__ int stream_swz(int t) { return ((t & 7) + ((t & 16) >> 2)) & 7; }
+__device__ __forceinline__ int stream_swz(int t) { return ((2 * t) + (t >> 2)) & 7; }
 
 typedef __attribute__((address_space(3))) void lds_void;
 
@@ -533,19 +548,43 @@ __device__ __forceinline__ uint32_t lds_addr(const void* p) {
   return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const lds_void*)p));
 }
 
+// Four ds_read_b64_tr_b8 issued back to back with one lgkmcnt wait.  Written
+// as asm because the compiler's waitcnt pass cannot tell this LDS read from
+// the in-flight load-to-LDS of other stages and would drain the whole
+// prefetch (vmcnt(0)) before it.
+__device__ __forceinline__ void lds_read_tr8_x4(const uint32_t (&ad)[4], uint64_t (&out)[4]) {
+  asm volatile(
+      "ds_read_b64_tr_b8 %0, %4\n\t"
+      "ds_read_b64_tr_b8 %1, %5\n\t"
+      "ds_read_b64_tr_b8 %2, %6\n\t"
+      "ds_read_b64_tr_b8 %3, %7\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(out[0]), "=&v"(out[1]), "=&v"(out[2]), "=&v"(out[3])
+      : "v"(ad[0]), "v"(ad[1]), "v"(ad[2]), "v"(ad[3])
+      : "memory");
+}
 
-// Global tile index -> (sequence, local tile) by walking the prefix sums.
+
+// Max over the four 16-lane groups (lanes l, l^16, l^32, l^48) with the
+// gfx950 lane-swap instructions (VALU, no LDS round trip).
+__device__ __forceinline__ float wave_max_across_groups(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
+}
+
+// Global tile index -> sequence, by walking the prefix sums.
 __device__ __forceinline__ void advance_seq(const int* tstart, int batch, int64_t tile, int& b) {
   while (b + 1 < batch && tstart[b + 1] <= tile) ++b;
   b = __builtin_amdgcn_readfirstlane(b);  // uniform: lets the metadata reads use scalar loads
 }
 
-// Locate a global tile: local token offset and physical block of sequence b.
-// Plain scalars (not a struct) so nothing is kept in memory across tiles.
+// Locate a global tile: first token of the tile and its physical block.
 __device__ __forceinline__ void stream_tile(const DecodeArgs& a, const int* tstart, int64_t tile, int b, int& t0,
                                             int& blk, int& ok) {
   const int lt = __builtin_amdgcn_readfirstlane(static_cast<int>(tile - tstart[b]));
-  t0 = lt * kTile;
+  t0 = lt * kSTile;
   const int page = __builtin_amdgcn_readfirstlane(t0 / a.page_size);
   const int32_t raw = ld_meta(a.bt + static_cast<int64_t>(b) * a.bt_sb + static_cast<int64_t>(page) * a.bt_sn);
   ok = raw >= 0 && raw < a.num_blocks;
@@ -554,8 +593,8 @@ __device__ __forceinline__ void stream_tile(const DecodeArgs& a, const int* tsta
 
 // Workgroup barrier without a memory fence.  __syncthreads() adds a
 // workgroup-scope release that waits for every outstanding load-to-LDS,
-// including the prefetch of the next tile; the stream kernel instead waits
-// for exactly the current tile's loads (s_waitcnt vmcnt) before this barrier.
+// including the prefetch of later tiles; the stream kernel instead waits for
+// exactly the current tile's loads (s_waitcnt vmcnt) before this barrier.
 // The empty asm keeps the compiler from moving LDS accesses across it.
 __device__ __forceinline__ void stream_barrier() {
   asm volatile("" ::: "memory");
@@ -563,79 +602,68 @@ __device__ __forceinline__ void stream_barrier() {
   asm volatile("" ::: "memory");
 }
 
-// Eight ds_read_b64_tr_b8 of 16-byte chunks (j ^ swz) of one head row, issued
-// back to back with one lgkmcnt wait.  Written as asm because the compiler's
-// waitcnt pass cannot tell this LDS read from the in-flight load-to-LDS of the
-// other stage and would drain the whole prefetch (vmcnt(0)) before it.
-__device__ __forceinline__ void lds_read_tr8_x8(const uint8_t* row, int swz, uint64_t (&out)[8]) {
-  const uint32_t base = lds_addr(row);
-  uint32_t ad[8];
+// Per-lane, loop-invariant parts of a tile's load addresses.
+struct StreamLanePlan {
+  int32_t goff[2];   // byte offset of this lane's K/V chunks inside the tile slab
+  int32_t soff;      // element offset of this lane's scale inside the tile's scales
+  uint32_t lk[2];    // LDS offsets (from the stage base) of the K chunks' wave slice
+  uint32_t ls;       // LDS offset of the scale slice
+  int which;         // 0: k scales, 1: v scales
+};
+
+__device__ __forceinline__ StreamLanePlan stream_plan(int wave, int lane) {
+  StreamLanePlan pl;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) ad[j] = base + ((j ^ swz) << 4);
-  asm volatile(
-      "ds_read_b64_tr_b8 %0, %8\n\t"
-      "ds_read_b64_tr_b8 %1, %9\n\t"
-      "ds_read_b64_tr_b8 %2, %10\n\t"
-      "ds_read_b64_tr_b8 %3, %11\n\t"
-      "ds_read_b64_tr_b8 %4, %12\n\t"
-      "ds_read_b64_tr_b8 %5, %13\n\t"
-      "ds_read_b64_tr_b8 %6, %14\n\t"
-      "ds_read_b64_tr_b8 %7, %15\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(out[0]), "=&v"(out[1]), "=&v"(out[2]), "=&v"(out[3]), "=&v"(out[4]), "=&v"(out[5]), "=&v"(out[6]),
-        "=&v"(out[7])
-      : "v"(ad[0]), "v"(ad[1]), "v"(ad[2]), "v"(ad[3]), "v"(ad[4]), "v"(ad[5]), "v"(ad[6]), "v"(ad[7])
-      : "memory");
+  for (int r = 0; r < 2; ++r) {
+    const int p = r * (kSThreads * 16) + wave * 1024 + lane * 16;  // byte in the K slab
+    const int t = p >> 10;
+    const int hh = (p >> 7) & 7;
+    const int chunk = ((p >> 4) & 7) ^ stream_swz(t);
+    pl.goff[r] = t * kSRow + hh * kHeadDim + chunk * 16;
+    pl.lk[r] = r * (kSThreads * 16) + wave * 1024;
+  }
+  // scales: waves 0/1 k, 2/3 v, 4-7 repeat 0-3 (same bytes, L2 hits) so
+  // every wave issues the same number of loads.  LDS layout [head][token].
+  const int w4 = wave & 3;
+  pl.which = w4 >> 1;
+  const int p = (w4 & 1) * 64 + lane;  // 0..127
+  const int hh = p >> 4;
+  const int t = p & 15;
+  pl.soff = t * kSKv + hh;
+  pl.ls = 2 * kSKBytes + pl.which * kSScaleBytes + (w4 & 1) * 256;
+  return pl;
 }
 
-// Issue the loads of one tile straight into `stage` (9 per lane: 4 K, 4 V,
-// 1 scale).  Written as asm so the compiler's waitcnt pass does not track
-// these load-to-LDS operations: it cannot tell the two stage buffers apart
-// and would otherwise drain every outstanding load before each LDS read.  The
-// kernel waits for them explicitly (s_waitcnt vmcnt + s_barrier); compiler-
-// issued vector loads elsewhere can only over-wait because of them.
-__device__ __forceinline__ void stream_issue(const DecodeArgs& a, int t0, int blk, uint8_t* stage, int wave,
-                                             int lane) {
+// Issue the loads of one tile into `stage` (5 per lane).  Written as asm so
+// the compiler's waitcnt pass does not track these load-to-LDS operations (it
+// cannot tell the stage buffers apart and would drain every outstanding load
+// before each LDS read).  The kernel waits for them explicitly (s_waitcnt
+// vmcnt + s_barrier); compiler-issued vector loads elsewhere can only
+// over-wait because of them.
+__device__ __forceinline__ void stream_issue(const DecodeArgs& a, const StreamLanePlan& pl, int t0, int blk,
+                                             uint32_t stage_lds) {
   const int off0 = t0 % a.page_size;
   const uint8_t* kbase = a.k + blk * a.k_sblk + static_cast<int64_t>(off0) * kSRow;
   const uint8_t* vbase = a.v + blk * a.v_sblk + static_cast<int64_t>(off0) * kSRow;
-  const uint8_t* kp[4];
-  const uint8_t* vp[4];
-  uint32_t lk[4], lv[4];
-  const uint32_t sbase = __builtin_amdgcn_readfirstlane(lds_addr(stage));
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int p = r * (kSThreads * 16) + wave * 1024 + lane * 16;  // LDS byte offset in the K slab
-    const int t = p >> 10;
-    const int hh = (p >> 7) & 7;
-    const int kk = ((p >> 4) & 7) ^ stream_swz(t);
-    const int goff = t * kSRow + hh * kHeadDim + kk * 16;
-    kp[r] = kbase + goff;
-    vp[r] = vbase + goff;
-    lk[r] = __builtin_amdgcn_readfirstlane(sbase + r * (kSThreads * 16) + wave * 1024);
-    lv[r] = lk[r] + kSKBytes;
-  }
-  // scales: waves 0-3 k, 4-7 v; LDS layout [head][token]
-  const int which = wave >> 2;
-  const int p = (wave & 3) * 64 + lane;  // 0..255
-  const int hh = p >> 5;
-  const int t = p & 31;
-  const float* sp = (which ? a.vs : a.ks) + blk * a.ks_sblk + static_cast<int64_t>(off0 + t) * kSKv + hh;
-  const uint32_t ls = __builtin_amdgcn_readfirstlane(sbase + 2 * kSKBytes + which * kSScaleBytes + (wave & 3) * 256);
+  const float* sp = (pl.which ? a.vs : a.ks) + blk * a.ks_sblk + static_cast<int64_t>(off0) * kSKv + pl.soff;
+  const uint8_t* k0 = kbase + pl.goff[0];
+  const uint8_t* k1 = kbase + pl.goff[1];
+  const uint8_t* v0 = vbase + pl.goff[0];
+  const uint8_t* v1 = vbase + pl.goff[1];
+  const uint32_t lk0 = __builtin_amdgcn_readfirstlane(stage_lds + pl.lk[0]);
+  const uint32_t lk1 = __builtin_amdgcn_readfirstlane(stage_lds + pl.lk[1]);
+  const uint32_t lv0 = lk0 + kSKBytes;
+  const uint32_t lv1 = lk1 + kSKBytes;
+  const uint32_t ls = __builtin_amdgcn_readfirstlane(stage_lds + pl.ls);
   asm volatile(
       "s_mov_b32 m0, %[lk0]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[k0], off\n\t"
       "s_mov_b32 m0, %[lv0]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v0], off\n\t"
       "s_mov_b32 m0, %[lk1]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[k1], off\n\t"
       "s_mov_b32 m0, %[lv1]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v1], off\n\t"
-      "s_mov_b32 m0, %[lk2]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[k2], off\n\t"
-      "s_mov_b32 m0, %[lv2]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v2], off\n\t"
-      "s_mov_b32 m0, %[lk3]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[k3], off\n\t"
-      "s_mov_b32 m0, %[lv3]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v3], off\n\t"
       "s_mov_b32 m0, %[ls]\n\ts_nop 0\n\tglobal_load_lds_dword %[sp], off"
       :
-      : [k0] "v"(kp[0]), [k1] "v"(kp[1]), [k2] "v"(kp[2]), [k3] "v"(kp[3]), [v0] "v"(vp[0]), [v1] "v"(vp[1]),
-        [v2] "v"(vp[2]), [v3] "v"(vp[3]), [sp] "v"(sp), [lk0] "s"(lk[0]), [lk1] "s"(lk[1]), [lk2] "s"(lk[2]),
-        [lk3] "s"(lk[3]), [lv0] "s"(lv[0]), [lv1] "s"(lv[1]), [lv2] "s"(lv[2]), [lv3] "s"(lv[3]), [ls] "s"(ls)
+      : [k0] "v"(k0), [k1] "v"(k1), [v0] "v"(v0), [v1] "v"(v1), [sp] "v"(sp), [lk0] "s"(lk0), [lk1] "s"(lk1),
+        [lv0] "s"(lv0), [lv1] "s"(lv1), [ls] "s"(ls)
       : "memory", "m0");
 }
 
@@ -685,13 +713,22 @@ __device__ __forceinline__ void stream_load_q(const DecodeArgs& a, int b, int h,
   }
 }
 
+typedef short shortx4 __attribute__((ext_vector_type(4)));
+
+// 4 fp8 bytes (one dword) -> 4 bf16 bit patterns, exact.  Built from whole
+// dwords: extracting single bf16 lanes of the converted pairs (bit_cast of
+// element [1] to short) was lowered by this compiler (ROCm 7.2 clang) to a
+// v_perm that duplicates element [0].
+__device__ __forceinline__ shortx4 fp8x4_to_bf16x4_bits(uint32_t w) {
+  const u32x2 r = {__builtin_bit_cast(uint32_t, fp8x2_to_bf16x2<false>(w)),
+                   __builtin_bit_cast(uint32_t, fp8x2_to_bf16x2<true>(w))};
+  return __builtin_bit_cast(shortx4, r);
+}
+
 template <int QDT, bool QVEC>
-__global__ void __launch_bounds__(kSThreads, 1)
+__global__ void __launch_bounds__(kSThreads, kSWgPerCu)
 paged_decode_stream_kernel(const DecodeArgs a) {
-  // Two separate stage buffers (not one array): the compiler's LDS-DMA wait
-  // tracking can then tell the stage being read from the one being filled.
-  __shared__ __attribute__((aligned(16))) uint8_t stage0[kSStage];
-  __shared__ __attribute__((aligned(16))) uint8_t stage1[kSStage];
+  __shared__ __attribute__((aligned(16))) uint8_t stages[kSStages * kSStage];
   __shared__ int tstart[kSMaxBatch + 1];
   __shared__ int scan[kSThreads];
   const int lane = threadIdx.x & 63;
@@ -706,9 +743,8 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   for (int base = 0; base < B; base += kSThreads) {
     __syncthreads();
     const int bb = base + threadIdx.x;
-    const int n = bb < B ? (effective_len(a, bb) + kTile - 1) / kTile : 0;
-    // inclusive scan of n across the block (Hillis-Steele through LDS)
-    scan[threadIdx.x] = n;
+    const int n = bb < B ? (effective_len(a, bb) + kSTile - 1) / kSTile : 0;
+    scan[threadIdx.x] = n;  // inclusive Hillis-Steele scan through LDS
     __syncthreads();
     for (int off = 1; off < kSThreads; off <<= 1) {
       const int v = threadIdx.x >= off ? scan[threadIdx.x - off] : 0;
@@ -725,12 +761,48 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   const int64_t e = static_cast<int64_t>(blockIdx.x + 1) * total / nwg;
   if (s >= e) return;  // uniform across the workgroup
 
+  const StreamLanePlan pl = stream_plan(h, lane);
+  const uint32_t stage0 = lds_addr(stages);
+  const int64_t count = e - s;
+
+  // ---- issue-side tile iterator: sequence ib, local tile ilt of int_ tiles;
+  // the block id is re-read only when the page changes.
+  int ib = 0;
+  advance_seq(tstart, B, s, ib);
+  int ilt = __builtin_amdgcn_readfirstlane(static_cast<int>(s - tstart[ib]));
+  int intl = __builtin_amdgcn_readfirstlane(tstart[ib + 1] - tstart[ib]);
+  int ipage = -1, iblk = 0;
+  int64_t issued = 0;
+  auto issue_next = [&]() {
+    const int t0 = ilt * kSTile;
+    const int page = __builtin_amdgcn_readfirstlane(t0 / a.page_size);
+    if (page != ipage) {
+      ipage = page;
+      const int32_t raw = ld_meta(a.bt + static_cast<int64_t>(ib) * a.bt_sb + static_cast<int64_t>(page) * a.bt_sn);
+      iblk = (raw >= 0 && raw < a.num_blocks) ? raw : 0;
+    }
+    if (!(a.debug & 2)) stream_issue(a, pl, t0, iblk, stage0 + static_cast<uint32_t>(issued % kSStages) * kSStage);
+    ++issued;
+    if (++ilt == intl && issued < count) {  // next sequence with tiles
+      do {
+        ++ib;
+        intl = __builtin_amdgcn_readfirstlane(tstart[ib + 1] - tstart[ib]);
+      } while (intl == 0 && ib + 1 < B);
+      ib = __builtin_amdgcn_readfirstlane(ib);
+      ilt = 0;
+      ipage = -1;
+    }
+  };
+#pragma unroll
+  for (int i = 0; i < kSStages - 1; ++i)
+    if (issued < count) issue_next();
+
+  // ---- compute-side iterator (same walk, one tile behind)
   int b = 0;
   advance_seq(tstart, B, s, b);
-  int cur_t0, cur_blk, cur_ok;
-  stream_tile(a, tstart, s, b, cur_t0, cur_blk, cur_ok);
-  stream_issue(a, cur_t0, cur_blk, stage0, h, lane);
-
+  int lt = __builtin_amdgcn_readfirstlane(static_cast<int>(s - tstart[b]));
+  int ntl = __builtin_amdgcn_readfirstlane(tstart[b + 1] - tstart[b]);
+  int cpage = -1, cok = 0;
   QOperand<QDT> qop;
   stream_load_q<QDT, QVEC>(a, b, h, g, c, qop);
   int n_eff = effective_len(a, b);
@@ -738,130 +810,134 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   floatx4 acc[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY;
-  float l_run = 0.f;
+  float m_run = -INFINITY;  // running max (log2 domain) of q head c
+  float l_run = 0.f;        // this lane's share of the running sum
 
-  // One tile: prefetch the next into `next_stage`, compute `stage`.
-  // Returns false after the last tile of this workgroup's range.
-  auto step = [&](uint8_t* stage, uint8_t* next_stage, int64_t tile) -> bool {
-    const bool more = tile + 1 < e;
-    int bn = b;
-    int nxt_t0 = cur_t0, nxt_blk = cur_blk, nxt_ok = cur_ok;
-    if (more) {
-      advance_seq(tstart, B, tile + 1, bn);
-      stream_tile(a, tstart, tile + 1, bn, nxt_t0, nxt_blk, nxt_ok);
-      stream_issue(a, nxt_t0, nxt_blk, next_stage, h, lane);
-      __builtin_amdgcn_s_waitcnt(0xF79);  // vmcnt(9): this tile's 9 loads have landed
-    } else {
-      __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0)
+  // Per-lane LDS offsets inside a stage (loop invariant).
+  const uint32_t k_off0 = c * kSRow + h * kHeadDim + (((2 * g) ^ stream_swz(c)) << 4);
+  const uint32_t k_off1 = c * kSRow + h * kHeadDim + (((2 * g + 1) ^ stream_swz(c)) << 4);
+  const uint32_t s_off = 2 * kSKBytes + (h * kSTile + 4 * g) * 4;
+  uint32_t v_off[4];
+  {
+    const int r = c >> 1;              // row of the 8x16 byte matrix this lane addresses
+    const int t = 4 * g + (r & 3);     // token
+    const int half = c & 1;
+#pragma unroll
+    for (int jp = 0; jp < 4; ++jp) {
+      const int chunk = 2 * jp + (r >> 2);
+      v_off[jp] = kSKBytes + t * kSRow + h * kHeadDim + ((chunk ^ stream_swz(t)) << 4) + half * 8;
     }
-    stream_barrier();
+  }
 
-    if (cur_ok) {
-      const uint8_t* lk = stage;
-      const uint8_t* lv = stage + kSKBytes;
-      const float* lks = reinterpret_cast<const float*>(stage + 2 * kSKBytes);
-      const float* lvs = lks + kTile * kSKv;
-      // ---- QK
-      floatx4 sc[2];
-#pragma unroll
-      for (int hh = 0; hh < 2; ++hh) {
-        const int t = c + 16 * hh;
-        const uint8_t* row = lk + t * kSRow + h * kHeadDim;
-        const u32x4 k0 = *reinterpret_cast<const u32x4*>(row + (((2 * g) ^ stream_swz(t)) << 4));
-        const u32x4 k1 = *reinterpret_cast<const u32x4*>(row + (((2 * g + 1) ^ stream_swz(t)) << 4));
-        floatx4 accs = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int cc = 0; cc < 4; ++cc) {
-          const u32x4& kw = (cc < 2) ? k0 : k1;
-          const uint32_t w0 = kw[(cc & 1) * 2];
-          const uint32_t w1 = kw[(cc & 1) * 2 + 1];
-          if constexpr (QDT == PRISM_DTYPE_F16) {
-            accs = __builtin_amdgcn_mfma_f32_16x16x32_f16(fp8x8_to_f16x8(w0, w1), qop.hi[cc], accs, 0, 0, 0);
-          } else {
-            const bf16x8 kb = fp8x8_to_bf16x8(w0, w1);
-            accs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qop.hi[cc], accs, 0, 0, 0);
-            if constexpr (QDT == PRISM_DTYPE_F32)
-              accs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qop.lo[cc], accs, 0, 0, 0);
-          }
-        }
-        sc[hh] = accs;
+  for (int64_t done = 0; done < count; ++done) {
+    // Wait for this tile's loads (the younger tiles' loads may stay in flight),
+    // then one barrier: every wave's loads have landed and every wave has
+    // finished the previous tile, whose stage the refill below reuses.
+    const int64_t younger = issued - done - 1;
+    static_assert(kSStages >= 2 && kSStages <= 4, "wait table covers 1..3 younger tiles");
+    if (kSStages > 3 && younger >= 3) __builtin_amdgcn_s_waitcnt(0xF70 | (3 * kSLoadsPerStage));
+    else if (kSStages > 2 && younger >= 2) __builtin_amdgcn_s_waitcnt(0xF70 | (2 * kSLoadsPerStage));
+    else if (younger >= 1) __builtin_amdgcn_s_waitcnt(0xF70 | (1 * kSLoadsPerStage));
+    else __builtin_amdgcn_s_waitcnt(0xF70);
+    stream_barrier();
+    if (issued < count) issue_next();
+
+    const int t0 = lt * kSTile;
+    {
+      const int page = __builtin_amdgcn_readfirstlane(t0 / a.page_size);
+      if (page != cpage) {
+        cpage = page;
+        const int32_t raw = ld_meta(a.bt + static_cast<int64_t>(b) * a.bt_sb + static_cast<int64_t>(page) * a.bt_sn);
+        cok = raw >= 0 && raw < a.num_blocks;
       }
-      // scales of this lane's 8 tokens (4g..4g+3, 16+4g..16+4g+3)
-      const floatx4 ks0 = *reinterpret_cast<const floatx4*>(lks + h * kTile + 4 * g);
-      const floatx4 ks1 = *reinterpret_cast<const floatx4*>(lks + h * kTile + 16 + 4 * g);
-      const floatx4 vs0 = *reinterpret_cast<const floatx4*>(lvs + h * kTile + 4 * g);
-      const floatx4 vs1 = *reinterpret_cast<const floatx4*>(lvs + h * kTile + 16 + 4 * g);
-      // ---- online softmax
-      float x[8];
+    }
+    if (cok && !(a.debug & 1)) {
+      const uint32_t slot = static_cast<uint32_t>(done % kSStages) * kSStage;
+      const uint8_t* stp = stages + slot;
+      // ---- all LDS reads of the tile first, so their latencies overlap
+      const u32x4 k0 = *reinterpret_cast<const u32x4*>(stp + k_off0);
+      const u32x4 k1 = *reinterpret_cast<const u32x4*>(stp + k_off1);
+      const floatx4 ks = *reinterpret_cast<const floatx4*>(stp + s_off);
+      const floatx4 vs = *reinterpret_cast<const floatx4*>(stp + s_off + kSScaleBytes);
+      uint32_t ad[4];
+#pragma unroll
+      for (int jp = 0; jp < 4; ++jp) ad[jp] = stage0 + slot + v_off[jp];
+      uint64_t vt[4];
+      lds_read_tr8_x4(ad, vt);
+      // ---- QK over 16 tokens: two independent MFMA chains
+      floatx4 sca = {0.f, 0.f, 0.f, 0.f}, scb = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int cc = 0; cc < 4; ++cc) {
+        const u32x4& kw = (cc < 2) ? k0 : k1;
+        const uint32_t w0 = kw[(cc & 1) * 2];
+        const uint32_t w1 = kw[(cc & 1) * 2 + 1];
+        floatx4& sc = (cc & 1) ? scb : sca;
+        if constexpr (QDT == PRISM_DTYPE_F16) {
+          sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(fp8x8_to_f16x8(w0, w1), qop.hi[cc], sc, 0, 0, 0);
+        } else {
+          const bf16x8 kb = fp8x8_to_bf16x8(w0, w1);
+          sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qop.hi[cc], sc, 0, 0, 0);
+          if constexpr (QDT == PRISM_DTYPE_F32)
+            sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qop.lo[cc], sc, 0, 0, 0);
+        }
+      }
+      // ---- online softmax with lazy rescaling
+      float x[4];
       float tmax = -INFINITY;
       uint32_t valid = 0;
 #pragma unroll
-      for (int ee = 0; ee < 8; ++ee) {
-        const int tk = slot_token(g, ee);
-        const bool ok = (cur_t0 + tk < n_eff) && c < G;
-        valid |= (cur_t0 + tk < n_eff) ? (1u << ee) : 0u;
-        const float ksv = ee < 4 ? ks0[ee] : ks1[ee - 4];
-        const float v = sc[ee >> 2][ee & 3] * (ksv * a.scale_log2);
-        x[ee] = ok ? v : -INFINITY;
-        tmax = fmaxf(tmax, x[ee]);
+      for (int i = 0; i < 4; ++i) {
+        const bool tv = t0 + 4 * g + i < n_eff;
+        valid |= tv ? (1u << i) : 0u;
+        x[i] = (tv && c < G) ? (sca[i] + scb[i]) * (ks[i] * a.scale_log2) : -INFINITY;
+        tmax = fmaxf(tmax, x[i]);
       }
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-      const float m_new = fmaxf(m_run, tmax);
-      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-      const float alpha = exp2f(m_run - m_use);
-      m_run = m_new;
-      float psum = 0.f;
-      bf16x8 pa, pa_lo;
+      tmax = wave_max_across_groups(tmax);
+      const bool raise = tmax > m_run + kSRescaleThreshold;
+      if (__builtin_amdgcn_ballot_w64(raise) != 0) {  // wave-uniform branch
+        const float m_new = raise ? tmax : m_run;
+        const float alpha = raise ? exp2f(m_run - m_new) : 1.f;
+        m_run = m_new;
+        l_run *= alpha;
 #pragma unroll
-      for (int ee = 0; ee < 8; ++ee) {
-        const float p = exp2f(x[ee] - m_use);
-        psum += p;
-        const float vsv = ee < 4 ? vs0[ee] : vs1[ee - 4];
-        const float pv = ((valid >> ee) & 1u) ? p * vsv : 0.f;
-        const __bf16 hi = static_cast<__bf16>(pv);
-        pa[ee] = hi;
-        pa_lo[ee] = static_cast<__bf16>(pv - static_cast<float>(hi));
+        for (int i = 0; i < 4; ++i) {
+          const float ai = __shfl(alpha, 4 * g + i);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) acc[j][i] *= ai;
+        }
       }
-      l_run = l_run * alpha + psum;
+      const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
+      shortx4 pa, pa_lo;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float ai = __shfl(alpha, 4 * g + i);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[j][i] *= ai;
+        const float p = exp2f(x[i] - m_use);  // 0 for masked slots
+        l_run += p;
+        const float pv = ((valid >> i) & 1u) ? p * vs[i] : 0.f;
+        const __bf16 hi = static_cast<__bf16>(pv);
+        pa[i] = __builtin_bit_cast(short, hi);
+        pa_lo[i] = __builtin_bit_cast(short, static_cast<__bf16>(pv - static_cast<float>(hi)));
       }
-      // ---- PV: lane (g, i) points at token slot_token(g, i/2), half i&1
-      {
-        const int r = c >> 1;
-        const int t = slot_token(g, r);
-        // byte r of a transposed read comes from k slot r: keep only the bytes
-        // of attended tokens (rows past the sequence end may hold NaN codes and
-        // the MFMA would turn 0 * NaN into NaN).
-        uint32_t keep0 = 0, keep1 = 0;
+      // ---- PV: one transposed read feeds N-tiles 2jp and 2jp+1.  Bytes of
+      // tokens past the end of the sequence are zeroed (rows there may hold
+      // NaN codes and the MFMA would turn 0 * NaN into NaN).
+      uint32_t keep = 0;
 #pragma unroll
-        for (int rr = 0; rr < 4; ++rr) {
-          keep0 |= ((valid >> rr) & 1u) ? (0xFFu << (8 * rr)) : 0u;
-          keep1 |= ((valid >> (rr + 4)) & 1u) ? (0xFFu << (8 * rr)) : 0u;
-        }
-        const uint8_t* vrow = lv + t * kSRow + h * kHeadDim + ((c & 1) << 3);
-        uint64_t vt[8];
-        lds_read_tr8_x8(vrow, stream_swz(t), vt);
+      for (int i = 0; i < 4; ++i) keep |= ((valid >> i) & 1u) ? (0xFFu << (8 * i)) : 0u;
 #pragma unroll
-        for (int j = 0; j < 8; ++j) {
-          const uint32_t w0 = static_cast<uint32_t>(vt[j]) & keep0;
-          const uint32_t w1 = static_cast<uint32_t>(vt[j] >> 32) & keep1;
-          const bf16x8 bv = fp8x8_to_bf16x8(w0, w1);
-          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, bv, acc[j], 0, 0, 0);
-          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa_lo, bv, acc[j], 0, 0, 0);
-        }
+      for (int jp = 0; jp < 4; ++jp) {
+        const shortx4 b0 = fp8x4_to_bf16x4_bits(static_cast<uint32_t>(vt[jp]) & keep);
+        const shortx4 b1 = fp8x4_to_bf16x4_bits(static_cast<uint32_t>(vt[jp] >> 32) & keep);
+        acc[2 * jp] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, b0, acc[2 * jp], 0, 0, 0);
+        acc[2 * jp + 1] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, b1, acc[2 * jp + 1], 0, 0, 0);
+        acc[2 * jp] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa_lo, b0, acc[2 * jp], 0, 0, 0);
+        acc[2 * jp + 1] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa_lo, b1, acc[2 * jp + 1], 0, 0, 0);
       }
     }
-    stream_barrier();  // every wave is done with this stage before it is refilled
 
-    const bool seq_ends = !more || bn != b;
+    // ---- advance the compute iterator; flush at the end of a sequence
+    const bool more = done + 1 < count;
+    const bool seq_ends = !more || lt + 1 == ntl;
     if (seq_ends) {
-      // flush the (workgroup, sequence) partial
       float l_tot = l_run + __shfl_xor(l_run, 16);
       l_tot += __shfl_xor(l_tot, 32);
       const int64_t pidx = static_cast<int64_t>(blockIdx.x) + b;
@@ -886,20 +962,19 @@ paged_decode_stream_kernel(const DecodeArgs a) {
         for (int j = 0; j < 8; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
         m_run = -INFINITY;
         l_run = 0.f;
-        b = bn;
+        do {
+          ++b;
+          ntl = __builtin_amdgcn_readfirstlane(tstart[b + 1] - tstart[b]);
+        } while (ntl == 0 && b + 1 < B);
+        b = __builtin_amdgcn_readfirstlane(b);
+        lt = 0;
+        cpage = -1;
         n_eff = effective_len(a, b);
         stream_load_q<QDT, QVEC>(a, b, h, g, c, qop);
       }
+    } else {
+      ++lt;
     }
-    cur_t0 = nxt_t0;
-    cur_blk = nxt_blk;
-    cur_ok = nxt_ok;
-    return more;
-  };
-
-  for (int64_t tile = s;;) {
-    if (!step(stage0, stage1, tile++)) break;
-    if (!step(stage1, stage0, tile++)) break;
   }
 }
 
@@ -917,7 +992,7 @@ __global__ void __launch_bounds__(64) paged_decode_stream_combine_kernel(const D
   const int lane = threadIdx.x;
   int64_t before = 0, total = 0;
   for (int bb = lane; bb < a.batch; bb += 64) {
-    const int64_t n = (effective_len(a, bb) + kTile - 1) / kTile;
+    const int64_t n = (effective_len(a, bb) + kSTile - 1) / kSTile;
     total += n;
     if (bb < b) before += n;
   }
@@ -926,7 +1001,7 @@ __global__ void __launch_bounds__(64) paged_decode_stream_combine_kernel(const D
     total += __shfl_xor(total, off);
     before += __shfl_xor(before, off);
   }
-  const int64_t n_b = (effective_len(a, b) + kTile - 1) / kTile;
+  const int64_t n_b = (effective_len(a, b) + kSTile - 1) / kSTile;
   const int64_t base = static_cast<int64_t>(b) * a.o_sb + static_cast<int64_t>(hq) * a.o_sh;
   if (n_b == 0) {
     store_out<QDT>(a.out, base + lane * a.o_sd, 0.f);
@@ -943,10 +1018,10 @@ __global__ void __launch_bounds__(64) paged_decode_stream_combine_kernel(const D
   };
   const int64_t w_lo = owner(first_tile);
   const int64_t w_hi = owner(last_tile);
-  const int count = static_cast<int>(w_hi - w_lo + 1);
+  const int cnt = static_cast<int>(w_hi - w_lo + 1);
   // pass 1: (m, l) lane-parallel; workgroups with an empty range wrote nothing
   float m_max = -INFINITY;
-  for (int i = lane; i < count; i += 64) {
+  for (int i = lane; i < cnt; i += 64) {
     const int64_t w = w_lo + i;
     const bool has = (w * total) / nwg < ((w + 1) * total) / nwg;
     const float m = has ? a.part_ml[((w + b) * a.num_heads + hq) * 2] : -INFINITY;
@@ -957,7 +1032,7 @@ __global__ void __launch_bounds__(64) paged_decode_stream_combine_kernel(const D
   for (int off = 32; off >= 1; off >>= 1) m_max = fmaxf(m_max, __shfl_xor(m_max, off));
   const float m_use = (m_max == -INFINITY) ? 0.f : m_max;
   float l_sum = 0.f;
-  for (int i = lane; i < count; i += 64) {
+  for (int i = lane; i < cnt; i += 64) {
     const int64_t w = w_lo + i;
     const float m = wts[i];
     const float wgt = (m == -INFINITY) ? 0.f : exp2f(m - m_use);
@@ -970,7 +1045,7 @@ __global__ void __launch_bounds__(64) paged_decode_stream_combine_kernel(const D
   // pass 2: weighted sum of the accumulators
   float o0 = 0.f, o1 = 0.f;
 #pragma unroll 4
-  for (int i = 0; i < count; ++i) {
+  for (int i = 0; i < cnt; ++i) {
     const float wgt = wts[i];
     if (wgt == 0.f) continue;
     const float* src = a.part_acc + ((w_lo + i + b) * a.num_heads + hq) * kHeadDim;
@@ -1145,10 +1220,10 @@ Geometry geometry(int batch, int num_heads, int num_kv_heads, int head_dim, int 
     geo.ml_off = align_up(rows * head_dim * 4, 256);
     geo.ws_bytes = geo.ml_off + align_up(rows * 2 * 4, 256);
   }
-  geo.stream_shape = num_kv_heads == kSKv && page_size % kTile == 0 && batch <= kSMaxBatch && !stream_disabled() &&
-                     device_cu_count() <= kSMaxWg;
+  geo.stream_shape = num_kv_heads == kSKv && page_size % kSTile == 0 && batch <= kSMaxBatch && !stream_disabled() &&
+                     device_cu_count() * kSWgPerCu <= kSMaxWg;
   if (geo.stream_shape) {
-    geo.stream_nwg = device_cu_count();
+    geo.stream_nwg = device_cu_count() * kSWgPerCu;
     const int64_t rows = (static_cast<int64_t>(geo.stream_nwg) + batch) * num_heads;
     geo.stream_acc_off = 0;
     geo.stream_ml_off = align_up(rows * head_dim * 4, 256);
@@ -1363,6 +1438,10 @@ extern "C" int prism_paged_decode_stage(
   args.max_splits = geo.fast ? geo.max_splits : 1;
   args.scale_log2 = scale * kLog2e;
   args.cache_dtype = cache_dtype;
+  {
+    const char* dbg = getenv("PRISM_STREAM_DEBUG");  // 1: skip compute, 2: skip loads
+    args.debug = dbg ? atoi(dbg) : 0;
+  }
   const bool page_aligned = (page_size % kTile) == 0;
   // Streaming path: canonical contiguous page layout with scales.
   const bool use_stream = geo.fast && geo.stream_shape && k_scale != nullptr && k_strides[1] == kSRow &&
