@@ -1172,10 +1172,17 @@ struct Geometry {
   int64_t stream_acc_off, stream_ml_off;
 };
 
-bool stream_disabled() {
+// PRISM_DECODE_PATH=split|stream forces a kernel family (tests, A/B runs);
+// unset, the streaming kernel is used when the batch offers enough tiles to
+// keep every workgroup busy and the per-split kernel otherwise (lower latency
+// for one or a few short sequences).
+int forced_path() {
   const char* env = getenv("PRISM_DECODE_PATH");
-  return env && env[0] == 's' && env[1] == 'p';  // "split" forces the per-split kernel
+  if (!env || env[0] != 's') return 0;
+  return env[1] == 'p' ? 1 : (env[1] == 't' ? 2 : 0);  // 1 = split, 2 = stream
 }
+
+bool stream_disabled() { return forced_path() == 1; }
 
 bool fast_geometry(int num_heads, int num_kv_heads, int head_dim, int cache_dtype) {
   if (cache_dtype != PRISM_DTYPE_FP8_E4M3FN || head_dim != kHeadDim) return false;
@@ -1222,6 +1229,10 @@ Geometry geometry(int batch, int num_heads, int num_kv_heads, int head_dim, int 
   }
   geo.stream_shape = num_kv_heads == kSKv && page_size % kSTile == 0 && batch <= kSMaxBatch && !stream_disabled() &&
                      device_cu_count() * kSWgPerCu <= kSMaxWg;
+  if (geo.stream_shape && forced_path() != 2) {
+    const int64_t cap_tiles = static_cast<int64_t>(batch) * ceil_div(static_cast<int64_t>(width) * page_size, kSTile);
+    if (cap_tiles < 8LL * device_cu_count() * kSWgPerCu) geo.stream_shape = false;
+  }
   if (geo.stream_shape) {
     geo.stream_nwg = device_cu_count() * kSWgPerCu;
     const int64_t rows = (static_cast<int64_t>(geo.stream_nwg) + batch) * num_heads;

@@ -15,6 +15,15 @@ pytestmark = pytest.mark.gpu
 FP8 = torch.float8_e4m3fn
 
 
+@pytest.fixture(params=["auto", "stream", "split"])
+def decode_path(request, monkeypatch):
+    """Run a test with the default kernel choice and with each family forced."""
+
+    if request.param != "auto":
+        monkeypatch.setenv("PRISM_DECODE_PATH", request.param)
+    return request.param
+
+
 def _quantize_cpu(source: torch.Tensor):
     """Scaled-FP8 pages of ``source`` [N, P, H, D] through the oracle."""
 
@@ -66,7 +75,7 @@ def test_reference_scaled_decode_case_seed_20260720():
 
 
 @pytest.mark.parametrize("batch", [1, 2, 4, 8])
-def test_qwen_batch_context_matrix_scaled_fp8(batch):
+def test_qwen_batch_context_matrix_scaled_fp8(batch, decode_path):
     """B x ctx matrix of the reference's Qwen test (32q/8kv, D=128, P=256), scaled FP8."""
 
     require_gpu()
@@ -83,7 +92,7 @@ def test_qwen_batch_context_matrix_scaled_fp8(batch):
         assert_decode_close(got, _oracle(q, k, v, ks, vs, tables, lens, 128 ** -0.5), label=f"B{batch} ctx{ctx}")
 
 
-def test_ragged_lengths_invalid_blocks_and_empty_rows():
+def test_ragged_lengths_invalid_blocks_and_empty_rows(decode_path):
     """Ragged lengths (not multiples of the tile), -1 blocks inside a table, ctx=0 rows, a tiny max_context_len."""
 
     require_gpu()
@@ -105,7 +114,7 @@ def test_ragged_lengths_invalid_blocks_and_empty_rows():
 
 
 @pytest.mark.parametrize("qdtype", [torch.float16, torch.float32])
-def test_query_dtypes_and_strided_query(qdtype):
+def test_query_dtypes_and_strided_query(qdtype, decode_path):
     require_gpu()
     g = torch.Generator().manual_seed(9)
     pool = 40
@@ -172,7 +181,7 @@ def test_single_sequence_configs(name):
     assert_decode_close(out, ref, atol=3e-2, label=name + " vs bf16 reference path")
 
 
-def test_mixed_batch_north_star_config():
+def test_mixed_batch_north_star_config(decode_path):
     """B=64, lengths U[1k,16k], 32 sequences sharing a 4096-token prefix, 8192-page pool."""
 
     require_gpu()
@@ -209,7 +218,7 @@ def test_page_permutation_invariance_on_gpu():
     assert torch.equal(a, b)
 
 
-def test_graph_replay_follows_device_metadata():
+def test_graph_replay_follows_device_metadata(decode_path):
     """Captured decode follows updated context_lens / max_context_len / tables on replay."""
 
     require_gpu()
