@@ -45,16 +45,17 @@ def _validate_paged_decode_inputs(q, k_cache, v_cache, block_tables, context_len
                                   block_n: int = DEFAULT_PAGED_DECODE_BLOCK_N) -> bool:
     """Validate the public paged-decode contract; returns whether scales are used."""
 
-    _validate_paged_decode_runtime(q)
+    # contract (ValueError) first, then where the tensors live (RuntimeError)
     scaled_kv = _validate_paged_scale_pair(k_scale_cache, v_scale_cache)
-    _validate_paged_device_tensors(q, k_cache, v_cache, block_tables, context_lens, max_context_len,
-                                   k_scale_cache, v_scale_cache)
     _validate_paged_query_cache_contract(q, k_cache, v_cache)
     _validate_paged_cache_dtypes(q, k_cache)
     if scaled_kv:
         _validate_paged_scale_cache(k_cache, k_scale_cache, v_scale_cache)
     _validate_paged_metadata(block_tables, context_lens, max_context_len)
     _validate_paged_geometry(q, k_cache, block_tables, context_lens, block_n)
+    _validate_paged_decode_runtime(q)
+    _validate_paged_device_tensors(q, k_cache, v_cache, block_tables, context_lens, max_context_len,
+                                   k_scale_cache, v_scale_cache)
     return scaled_kv
 
 

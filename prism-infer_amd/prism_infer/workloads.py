@@ -128,19 +128,19 @@ def _finish(name, q, pool, tables, lens, seed, used, unique_tokens, shared=0, me
 
 
 def decode_single(device, seed: int = 20260801, *, context_len: int = 2048, pool_pages: int = 64,
-                  name: str = "decode_single") -> DecodeWorkload:
+                  name: str = "decode_single", fill: bool = True) -> DecodeWorkload:
     g = _gen(seed)
     pages_needed = math.ceil(context_len / PAGE_SIZE)
     perm = torch.randperm(pool_pages, generator=g)[:pages_needed]
     q = torch.randn(1, NUM_HEADS, HEAD_DIM, generator=g, dtype=torch.bfloat16).to(device)
     tables = perm.to(torch.int32).reshape(1, -1)
     pool = _alloc_pool(pool_pages, device)
-    return _finish(name, q, pool, tables, [context_len], seed, perm.clone(), context_len)
+    return _finish(name, q, pool, tables, [context_len], seed, perm.clone(), context_len, fill=fill)
 
 
-def decode_qwen_vl(device, seed: int = 20260803) -> DecodeWorkload:
+def decode_qwen_vl(device, seed: int = 20260803, *, fill: bool = True) -> DecodeWorkload:
     ctx = 8 * 196 + 232
-    return decode_single(device, seed, context_len=ctx, name="decode_qwen_vl")
+    return decode_single(device, seed, context_len=ctx, name="decode_qwen_vl", fill=fill)
 
 
 def decode_mixed(device, seed: int = 20260804, *, batch: int = 64, min_len: int = 1024, max_len: int = 16384,
