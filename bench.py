@@ -166,7 +166,7 @@ def main() -> int:
     torch.cuda.synchronize()
     _log(f"timing {args.steps} steps")
     sec_per_step = _time_loop(step, args.steps, torch)
-    # dominant kernel alone (split-K partial kernel), same stream, same rotation
+    # dominant kernel alone (stage 1: the partial kernel without the merge), same stream, same rotation
     for i in range(args.warmup):
         step(i, 1)
     kernel_s = _time_loop(lambda i: step(i, 1), args.steps, torch)
@@ -180,7 +180,10 @@ def main() -> int:
             traffic = json.loads(TRAFFIC_FILE.read_text()).get("hbm_bytes_per_launch")
         except (ValueError, OSError):
             traffic = None
-    split = _native.lib().prism_paged_decode_split_tokens(64, 32, 8, 128, 256, base.block_tables.shape[1], 3)
+    geo_args = (base.batch, 32, 8, 128, 256, base.block_tables.shape[1], 3)
+    split = _native.lib().prism_paged_decode_split_tokens(*geo_args)
+    family = _native.lib().prism_paged_decode_kernel_family(*geo_args)
+    kernel_name = {2: "paged_decode_stream_kernel", 1: "paged_decode_split_kernel"}.get(family, "paged_decode_generic_kernel")
     result = {
         "metric": METRIC,
         "value": round(value, 2),
@@ -214,7 +217,7 @@ def main() -> int:
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
             "traffic": traffic,
-            "kernel": "paged_decode_split_kernel",
+            "kernel": kernel_name,
             "kernel_us": round(kernel_s * 1e6, 2),
             "combine_us": round(combine_s * 1e6, 2),
         },

@@ -129,6 +129,16 @@ int prism_paged_decode_split_tokens(int batch, int num_heads, int num_kv_heads, 
                                     int page_size, int max_blocks_per_seq, int cache_dtype);
 
 /*
+ * Kernel family a scaled-FP8 geometry selects: 0 generic, 1 per-split (split-K
+ * partials + combine), 2 streaming (tile-balanced persistent kernel + merge).
+ * Family 2 additionally needs the canonical dense cache layout at call time
+ * (otherwise family 1 runs).  PRISM_DECODE_PATH=split|stream in the
+ * environment forces a family where the geometry allows it.
+ */
+int prism_paged_decode_kernel_family(int batch, int num_heads, int num_kv_heads, int head_dim,
+                                     int page_size, int max_blocks_per_seq, int cache_dtype);
+
+/*
  * Physical slot compaction.  Replaces the kernels behind
  *   compact_kv_slots(cache, source_slots, destination_slots)
  *   (prism_infer/ops/kv_compaction.py:93-112; gather/scatter kernels :33-86).

@@ -502,18 +502,18 @@ __global__ void __launch_bounds__(64) paged_decode_combine_kernel(const DecodeAr
 // Persistent, tile-balanced kernel for the canonical page layout
 // ([num_blocks][P % 16 == 0][8 kv heads][128] FP8, scales [num_blocks][P][8]):
 //
-// * One workgroup (8 waves, wave = kv head) per CU.  The 16-token tiles of all
-//   sequences, concatenated in batch order, are split into gridDim.x equal
-//   contiguous ranges, so every CU streams the same number of bytes whatever
-//   the context-length mix.  A range spanning several sequences emits one
+// * Two workgroups (8 waves each, wave = kv head) per CU.  The 16-token tiles
+//   of all sequences, concatenated in batch order, are split into gridDim.x
+//   equal contiguous ranges, so every CU streams the same number of bytes
+//   whatever the context-length mix.  A range spanning several sequences emits one
 //   (m, l, acc) partial per (workgroup, sequence) pair; as ranges are
 //   contiguous and monotone the pairs form a staircase and `wg + seq` indexes
 //   them uniquely.  The combine kernel merges them.
 // * A tile is one contiguous slab per tensor (K [16 tok][8 h][128 B], V
 //   likewise, and the fp32 scales).  The workgroup copies tiles straight into
-//   LDS with global_load_lds (16 B per lane), four stages deep, so three tiles
-//   (about 100 KB) are in flight while one is computed and no VGPRs hold
-//   prefetched data.  16-byte chunks of a head row are XOR-swizzled by token
+//   LDS with global_load_lds (16 B per lane), two stages per workgroup, so
+//   while one workgroup computes a tile the CU has up to three more (about
+//   100 KB) in flight and no VGPRs hold prefetched data.  16-byte chunks of a head row are XOR-swizzled by token
 //   so row-parallel K reads and transposed V reads spread over the banks.
 //   Scales are stored [head][token] so a lane's four tokens are one 16-byte read.
 // * QK: 4 MFMA f32_16x16x32_bf16 per tile (A = K rows fp8 -> bf16, exact;
@@ -1318,6 +1318,16 @@ extern "C" int prism_paged_decode_split_tokens(int batch, int num_heads, int num
   prism::Geometry geo =
       prism::geometry(batch, num_heads, num_kv_heads, head_dim, page_size, max_blocks_per_seq, cache_dtype);
   return geo.fast ? geo.split : 0;
+}
+
+extern "C" int prism_paged_decode_kernel_family(int batch, int num_heads, int num_kv_heads, int head_dim,
+                                                int page_size, int max_blocks_per_seq, int cache_dtype) {
+  if (batch < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || page_size <= 0 || max_blocks_per_seq < 0)
+    return -1;
+  prism::Geometry geo =
+      prism::geometry(batch, num_heads, num_kv_heads, head_dim, page_size, max_blocks_per_seq, cache_dtype);
+  if (!geo.fast) return 0;
+  return geo.stream_shape ? 2 : 1;
 }
 
 extern "C" int prism_paged_decode_stage(
