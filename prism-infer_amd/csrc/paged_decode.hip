@@ -55,6 +55,10 @@ struct DecodeArgs {
   int64_t o_sb, o_sh, o_sd;
   float* part_acc;  // [B][S][Hq][D]
   float* part_ml;   // [B][S][Hq][2]
+  int* plan;        // streaming path: shared-page plan at the workspace start
+  int64_t vrow0;    // streaming path: first partial row of the virtual sequences
+  int share;        // streaming path: analyse prefix sharing
+  int stream_nwg;   // streaming path: grid size
   int batch, num_heads, num_kv_heads, groups, page_size, width, head_dim;
   int64_t num_blocks;
   int q_vec;     // q rows are 16-byte aligned with unit dim stride
@@ -580,17 +584,6 @@ __device__ __forceinline__ void advance_seq(const int* tstart, int batch, int64_
   b = __builtin_amdgcn_readfirstlane(b);  // uniform: lets the metadata reads use scalar loads
 }
 
-// Locate a global tile: first token of the tile and its physical block.
-__device__ __forceinline__ void stream_tile(const DecodeArgs& a, const int* tstart, int64_t tile, int b, int& t0,
-                                            int& blk, int& ok) {
-  const int lt = __builtin_amdgcn_readfirstlane(static_cast<int>(tile - tstart[b]));
-  t0 = lt * kSTile;
-  const int page = __builtin_amdgcn_readfirstlane(t0 / a.page_size);
-  const int32_t raw = ld_meta(a.bt + static_cast<int64_t>(b) * a.bt_sb + static_cast<int64_t>(page) * a.bt_sn);
-  ok = raw >= 0 && raw < a.num_blocks;
-  blk = ok ? raw : 0;
-}
-
 // Workgroup barrier without a memory fence.  __syncthreads() adds a
 // workgroup-scope release that waits for every outstanding load-to-LDS,
 // including the prefetch of later tiles; the stream kernel instead waits for
@@ -667,11 +660,11 @@ __device__ __forceinline__ void stream_issue(const DecodeArgs& a, const StreamLa
       : "memory", "m0");
 }
 
+// Query operand of one wave: column c (0..15) holds one query vector.
 template <int QDT, bool QVEC>
-__device__ __forceinline__ void stream_load_q(const DecodeArgs& a, int b, int h, int g, int c, QOperand<QDT>& qop) {
-  const int G = a.groups;
-  const bool qvalid = c < G;
-  const int64_t qbase = static_cast<int64_t>(b) * a.q_sb + static_cast<int64_t>(h * G + (qvalid ? c : 0)) * a.q_sh;
+__device__ __forceinline__ void stream_load_q(const DecodeArgs& a, int qrow, int qhead, bool qvalid, int g,
+                                              QOperand<QDT>& qop) {
+  const int64_t qbase = static_cast<int64_t>(qrow) * a.q_sb + static_cast<int64_t>(qhead) * a.q_sh;
 #pragma unroll
   for (int cc = 0; cc < 4; ++cc) {
     float x[8];
@@ -725,72 +718,442 @@ __device__ __forceinline__ shortx4 fp8x4_to_bf16x4_bits(uint32_t w) {
   return __builtin_bit_cast(shortx4, r);
 }
 
+// ------------------------------------------------------------ shared pages
+//
+// Prefix sharing: sequences whose block tables start with the same physical
+// pages (a shared read-only prefix) would each stream those pages.  The plan
+// kernel finds, on the device, groups of sequences with the same first page
+// and, per member, how many leading whole pages it shares with the group's
+// leader (the lowest-numbered member).  Members are packed M = 16 / G at a
+// time into "virtual sequences": a virtual sequence walks the leader's shared
+// pages once with a query operand whose 16 columns are the G query heads of
+// each of its M members, so every shared page is read once per M members
+// instead of once per member, at the same MFMA cost per tile.  A member then
+// streams only its private tail (the tokens after the shared pages), and the
+// merge combines the partials of its tail with those of its virtual sequence.
+//
+// Plan layout (int32 at the start of the workspace):
+//   [0] V (virtual sequences), [1] total tiles
+//   tstart[NS + 1]      tile prefix sums over the stream order, NS = V + batch:
+//                       virtual sequences first, then the real ones
+//   skip[batch]         tokens a real sequence leaves to its virtual sequence
+//   vslot[batch]        v * 16 + member slot, or -1
+//   vsrc[kSMaxVirt]     block-table row (the leader) of virtual sequence v
+//   vmem[kSMaxVirt][16] members of v (-1 = unused slot)
+//   vrot[kSMaxVirt]     tile at which virtual sequence v starts its walk (it
+//                       wraps around): the virtual sequences of one group
+//                       start at different pages, so the workgroups reading
+//                       them at the same time do not all hit the same pages
+//
+// Work split: workgroup w streams tiles [w * total / nwg, (w+1) * total / nwg)
+// of the stream; ranges are contiguous and in stream order, so the pair
+// (workgroup, stream entry) indexes a partial uniquely as w + entry.
+
+constexpr int kSCols = 16;                 // query columns of the MFMA operand
+constexpr int kSMaxWg = 1024;              // grid size bound of the streaming kernel
+constexpr int kSMaxVirt = 128;             // virtual sequences (>= 2 members each)
+constexpr int kSShareMaxBatch = 256;       // batches above this are not analysed
+constexpr int kPlanMaxPages = 64;          // leading pages compared per sequence
+constexpr int kPlanTstart = 16;
+constexpr int kPlanSkip = kPlanTstart + kSMaxBatch + kSMaxVirt + 16;
+constexpr int kPlanVslot = kPlanSkip + kSMaxBatch;
+constexpr int kPlanVsrc = kPlanVslot + kSMaxBatch;
+constexpr int kPlanVmem = kPlanVsrc + kSMaxVirt;
+constexpr int kPlanVrot = kPlanVmem + kSMaxVirt * kSCols;  // first tile of each virtual walk
+constexpr int kPlanWgTime = kPlanVrot + kSMaxVirt;         // measurement aid: per-workgroup times
+// Key of the plan: everything the plan is computed from.  A call whose
+// inputs equal the key left by the previous call on the same workspace keeps
+// that plan (every layer of a decode step has the same metadata).
+constexpr int kPlanKey = kPlanWgTime + 2 * kSMaxWg;
+constexpr int kPlanKeyParams = 12;
+constexpr int kPlanKeyEff = kPlanKey + kPlanKeyParams;       // attended lengths
+constexpr int kPlanKeyBt = kPlanKeyEff + kSMaxBatch;         // compared block-table prefix
+constexpr int kPlanInts = kPlanKeyBt + kSShareMaxBatch * kPlanMaxPages;
+constexpr int kPlanMagic = 0x504C414E;
+constexpr int kPlanThreads = 1024;
+constexpr int kPlanHashBits = 10;
+constexpr int kPlanHash = 1 << kPlanHashBits;  // >= 2 * kSShareMaxBatch slots
+static_assert(2 * kSShareMaxBatch <= kPlanHash, "hash table load factor");
+static_assert(kSShareMaxBatch / 2 <= kSMaxVirt, "virtual sequences of a full batch fit");
+static_assert(kSMaxBatch <= kPlanThreads, "one thread per sequence in the plan kernel");
+
+// Work split: workgroup w streams tiles [floor(w * total / nwg),
+// floor((w + 1) * total / nwg)).  (Measured on MI355X: per-workgroup times
+// vary with stream position and with the order in which workgroups reach a
+// CU, but the kernel is bandwidth-bound in aggregate, so neither weighting the
+// split nor handing out the last tiles dynamically shortened it.)
+struct StreamSplit {
+  int64_t total, nwg;
+};
+
+__device__ __forceinline__ StreamSplit stream_split(const DecodeArgs& a, int64_t total) {
+  return StreamSplit{total, a.stream_nwg};
+}
+
+__device__ __forceinline__ int64_t split_begin(const StreamSplit& sp, int64_t w) { return w * sp.total / sp.nwg; }
+
+// The workgroup whose range holds tile t (0 <= t < total): the last w with
+// split_begin(w) <= t, i.e. ceil((t + 1) * nwg / total) - 1.
+__device__ __forceinline__ int64_t split_owner(const StreamSplit& sp, int64_t t) {
+  return ((t + 1) * sp.nwg + sp.total - 1) / sp.total - 1;
+}
+
+// Inclusive prefix sum over the workgroup (every thread calls it): shuffles
+// within each wave, one pass over the wave totals.
+__device__ __forceinline__ int plan_scan(int v, int* wsum_s, int& total) {
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  int x = v;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int y = __shfl_up(x, off);
+    if (lane >= off) x += y;
+  }
+  if (lane == 63) wsum_s[wave] = x;
+  __syncthreads();
+  int before = 0, tot = 0;
+#pragma unroll
+  for (int i = 0; i < kPlanThreads / 64; ++i) {
+    const int ws = wsum_s[i];
+    before += i < wave ? ws : 0;
+    tot += ws;
+  }
+  __syncthreads();
+  total = tot;
+  return x + before;
+}
+
+__global__ void __launch_bounds__(kPlanThreads) paged_decode_stream_plan_kernel(const DecodeArgs a) {
+  __shared__ int eff_s[kSMaxBatch];
+  __shared__ int cap_s[kSMaxBatch];    // whole pages covered by the attended length (<= kPlanMaxPages)
+  __shared__ int full_s[kSMaxBatch];   // leading whole pages with valid block ids
+  __shared__ int lead_s[kSMaxBatch];   // group leader
+  __shared__ int sh_s[kSMaxBatch];     // leading pages equal to the leader's
+  __shared__ int cnt_s[kSMaxBatch];    // at a leader: members besides itself
+  __shared__ int smax_s[kSMaxBatch];   // at a leader: longest member share
+  __shared__ int vb_s[kSMaxBatch];     // at a leader: first virtual sequence
+  __shared__ int skip_s[kSMaxBatch];
+  __shared__ int vslot_s[kSMaxBatch];
+  __shared__ int vlen_s[kSMaxVirt];    // pages of virtual sequence v
+  __shared__ int vk_s[kSMaxVirt];      // chunk index of v in its group
+  __shared__ int vn_s[kSMaxVirt];      // virtual sequences of v's group
+  __shared__ int vsrc_s[kSMaxVirt];
+  __shared__ int vmem_s[kSMaxVirt * kSCols];
+  __shared__ int hkey[kPlanHash];
+  __shared__ int hmin[kPlanHash];
+  __shared__ int bt_s[kSShareMaxBatch * kPlanMaxPages];  // compared part of the block tables
+  __shared__ int tst_s[kSMaxBatch + kSMaxVirt + 1];
+  __shared__ int wsum_s[kPlanThreads / 64];
+  __shared__ __attribute__((aligned(16))) int cnt_rank_s[kSShareMaxBatch];  // group of each member or -1
+  int* plan = a.plan;
+  const int tid = threadIdx.x;
+  const int B = a.batch;
+  const int P = a.page_size;
+  const int Wc = min(a.width, kPlanMaxPages);
+  const int M = kSCols / a.groups;  // members per virtual sequence
+  const bool share = a.share && B <= kSShareMaxBatch && M >= 2 && Wc >= 1;
+  const uint64_t t_start = __builtin_amdgcn_s_memtime();
+  auto stamp = [&](int k) {  // measurement aid: cycles since start of each phase (debug bit 4)
+    if ((a.debug & 4) && tid == 0) plan[4 + k] = static_cast<int>(__builtin_amdgcn_s_memtime() - t_start);
+  };
+
+  // Global memory is only read until the final write-out: a barrier after
+  // global stores would wait for them to complete.
+  const int* key = plan + kPlanKey;
+  const int key_params[kPlanKeyParams] = {kPlanMagic, B, a.width, P, a.groups,
+                                          static_cast<int>(a.num_blocks & 0x7FFFFFFF),
+                                          static_cast<int>(a.num_blocks >> 31), share ? 1 : 0, a.stream_nwg,
+                                          0, 0, 0};
+  bool same = true;
+  if (tid < kPlanKeyParams - 3) same = key[tid] == key_params[tid];
+  if (tid == 0) same = same && key[kPlanKeyParams - 2] == plan[0] && key[kPlanKeyParams - 1] == plan[1];
+  if (tid < B) {
+    const int n = effective_len(a, tid);
+    same = same && key[kPlanKeyEff - kPlanKey + tid] == n;
+    eff_s[tid] = n;
+    const int cap = min(n / P, Wc);
+    cap_s[tid] = cap;
+    full_s[tid] = cap;
+    sh_s[tid] = cap;
+    lead_s[tid] = tid;
+    cnt_s[tid] = 0;
+    smax_s[tid] = 0;
+    skip_s[tid] = 0;
+    vslot_s[tid] = -1;
+  }
+  int V = 0;
+  stamp(0);
+  const int items = share ? B * Wc : 0;
+  // stage the compared block-table prefix, eight loads in flight per thread
+  for (int base = 0; base < items; base += 8 * kPlanThreads) {
+    int val[8], old[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int idx = base + u * kPlanThreads + tid;
+      const int b = idx / Wc;
+      const int j = idx - b * Wc;
+      val[u] = idx < items ? a.bt[static_cast<int64_t>(b) * a.bt_sb + static_cast<int64_t>(j) * a.bt_sn] : -1;
+      old[u] = idx < items ? key[kPlanKeyBt - kPlanKey + idx] : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int idx = base + u * kPlanThreads + tid;
+      if (idx < items) bt_s[idx] = val[u];
+      same = same && old[u] == val[u];
+    }
+  }
+  if (__syncthreads_and(same ? 1 : 0)) return;  // the previous plan still holds
+  if (share) {
+    for (int i = tid; i < kPlanHash; i += kPlanThreads) {
+      hkey[i] = -1;
+      hmin[i] = INT_MAX;
+    }
+    for (int i = tid; i < kSMaxVirt * kSCols; i += kPlanThreads) vmem_s[i] = -1;
+    __syncthreads();
+    stamp(1);
+    // group by first page: open addressing, the lowest index wins the slot
+    int slot = -1;
+    if (tid < B && cap_s[tid] >= 1) {
+      const int raw = bt_s[tid * Wc];
+      if (raw >= 0 && raw < a.num_blocks) {
+        uint32_t hsh = (static_cast<uint32_t>(raw) * 2654435761u) >> (32 - kPlanHashBits);
+        for (;;) {
+          const int prev = atomicCAS(&hkey[hsh], -1, raw);
+          if (prev == -1 || prev == raw) {
+            atomicMin(&hmin[hsh], tid);
+            slot = static_cast<int>(hsh);
+            break;
+          }
+          hsh = (hsh + 1) & (kPlanHash - 1);
+        }
+      }
+    }
+    __syncthreads();
+    if (slot >= 0) lead_s[tid] = hmin[slot];
+    __syncthreads();
+    stamp(2);
+    // page by page: validity of each whole page, equality with the leader's
+    for (int idx = tid; idx < items; idx += kPlanThreads) {
+      const int b = idx / Wc;
+      const int j = idx - b * Wc;
+      if (j >= cap_s[b]) continue;
+      const int raw = bt_s[idx];
+      const bool valid = raw >= 0 && raw < a.num_blocks;
+      if (!valid) atomicMin(&full_s[b], j);
+      const int L = lead_s[b];
+      if (L != b) {
+        const int lraw = j < cap_s[L] ? bt_s[L * Wc + j] : -1;
+        if (!valid || lraw != raw) atomicMin(&sh_s[b], j);
+      }
+    }
+    __syncthreads();
+    stamp(3);
+    if (tid < B && lead_s[tid] != tid) {
+      const int sv = min(sh_s[tid], full_s[tid]);
+      sh_s[tid] = sv;
+      if (sv >= 1) {
+        atomicAdd(&cnt_s[lead_s[tid]], 1);
+        atomicMax(&smax_s[lead_s[tid]], sv);
+      }
+    }
+    __syncthreads();
+    // virtual sequences per group: chunks of M members in index order, kept
+    // only when a chunk has at least two members
+    int nv = 0;
+    if (tid < B && lead_s[tid] == tid && cnt_s[tid] >= 1) {
+      const int n = cnt_s[tid] + 1;
+      nv = n / M + ((n % M) >= 2 ? 1 : 0);
+    }
+    const int incl = plan_scan(nv, wsum_s, V);
+    if (tid < B) vb_s[tid] = incl - nv;
+    for (int i = tid; i < V; i += kPlanThreads) vlen_s[i] = INT_MAX;
+    // group of each member (-1 for non-members), for the rank count below
+    if (tid < kSShareMaxBatch) {
+      int ml = -1;
+      if (tid < B) {
+        const int L = lead_s[tid];
+        ml = ((L == tid) ? cnt_s[tid] >= 1 : sh_s[tid] >= 1) ? L : -1;
+      }
+      cnt_rank_s[tid] = ml;
+    }
+    __syncthreads();
+    stamp(4);
+    if (tid < B) {
+      const int L = lead_s[tid];
+      const bool member = cnt_rank_s[tid] >= 0;
+      if (member) {
+        // rank = members of the group with a lower index (the leader is rank 0);
+        // independent 16-byte LDS reads so the latencies overlap
+        int rank = 0;
+        const int4* ml4 = reinterpret_cast<const int4*>(cnt_rank_s);
+#pragma unroll 8
+        for (int q = 0; q < (tid + 3) / 4; ++q) {
+          const int4 x = ml4[q];
+          const int b0 = 4 * q;
+          rank += (b0 + 0 < tid && x.x == L) + (b0 + 1 < tid && x.y == L) + (b0 + 2 < tid && x.z == L) +
+                  (b0 + 3 < tid && x.w == L);
+        }
+        const int n = cnt_s[L] + 1;
+        const int k = rank / M;
+        const int chunk = min(M, n - k * M);
+        if (chunk >= 2) {
+          const int v = vb_s[L] + k;
+          const int m = rank - k * M;
+          vmem_s[v * kSCols + m] = tid;
+          vslot_s[tid] = v * kSCols + m;
+          atomicMin(&vlen_s[v], L == tid ? smax_s[tid] : sh_s[tid]);
+          if (m == 0) {
+            vsrc_s[v] = L;
+            vk_s[v] = k;
+            vn_s[v] = n / M + ((n % M) >= 2 ? 1 : 0);
+          }
+        }
+      }
+    }
+    __syncthreads();
+    stamp(5);
+    if (tid < B && vslot_s[tid] >= 0) skip_s[tid] = vlen_s[vslot_s[tid] / kSCols] * P;
+    __syncthreads();
+  }
+  stamp(6);
+  // tile prefix sums in stream order: virtual sequences, then real ones
+  const int NS = B + V;
+  int carry = 0;
+  if (tid == 0) tst_s[0] = 0;
+  for (int base = 0; base < NS; base += kPlanThreads) {
+    const int i = base + tid;
+    int n = 0;
+    if (i < V) n = vlen_s[i] * (P / kSTile);
+    else if (i < NS) n = (eff_s[i - V] - skip_s[i - V] + kSTile - 1) / kSTile;
+    int chunk_total;
+    const int incl = plan_scan(n, wsum_s, chunk_total);
+    if (i < NS) tst_s[i + 1] = carry + incl;
+    carry += chunk_total;
+  }
+  __syncthreads();
+  stamp(7);
+  // ---- write-out
+  for (int i = tid; i <= NS; i += kPlanThreads) plan[kPlanTstart + i] = tst_s[i];
+  if (tid < B) {
+    plan[kPlanSkip + tid] = skip_s[tid];
+    plan[kPlanVslot + tid] = vslot_s[tid];
+  }
+  for (int i = tid; i < V * kSCols; i += kPlanThreads) plan[kPlanVmem + i] = vmem_s[i];
+  if (tid < V) {
+    plan[kPlanVsrc + tid] = vsrc_s[tid];
+    plan[kPlanVrot + tid] = (vk_s[tid] * vlen_s[tid] / vn_s[tid]) * (P / kSTile);
+  }
+  if (tid < kPlanKeyParams - 3) plan[kPlanKey + tid] = key_params[tid];
+  if (tid == 0) {  // copies of the plan header, checked before the plan is reused
+    plan[kPlanKey + kPlanKeyParams - 2] = V;
+    plan[kPlanKey + kPlanKeyParams - 1] = carry;
+  }
+  if (tid < B) plan[kPlanKeyEff + tid] = eff_s[tid];
+  for (int i = tid; i < items; i += kPlanThreads) plan[kPlanKeyBt + i] = bt_s[i];
+  stamp(8);
+  if (tid == 0) {
+    plan[0] = V;
+    plan[1] = carry;
+  }
+}
+
+// Walk parameters of stream entry i (i < V: virtual sequence i, else real
+// sequence i - V): block-table row, first token, end token, and the tile at
+// which a virtual sequence starts its walk (it wraps around).
+__device__ __forceinline__ void stream_seq(const DecodeArgs& a, const int* tstart, int V, int i, int& bt_row,
+                                           int& tok0, int& n_end, int& rot) {
+  if (i >= V) {
+    const int b = i - V;
+    bt_row = b;
+    tok0 = ld_meta(a.plan + kPlanSkip + b);
+    n_end = effective_len(a, b);
+    rot = 0;
+  } else {
+    bt_row = ld_meta(a.plan + kPlanVsrc + i);
+    tok0 = 0;
+    n_end = (tstart[i + 1] - tstart[i]) * kSTile;
+    rot = ld_meta(a.plan + kPlanVrot + i);
+  }
+}
+
+// Query column c of wave h for stream entry i: real sequence b -> q head
+// h*G + c (c < G); virtual sequence -> q head h*G + qh of member m, c = m*G + qh.
+__device__ __forceinline__ void stream_column(const DecodeArgs& a, int V, int i, int h, int c, int& qrow,
+                                              int& qhead, bool& valid) {
+  const int G = a.groups;
+  if (i >= V) {
+    valid = c < G;
+    qrow = i - V;
+    qhead = h * G + (valid ? c : 0);
+    return;
+  }
+  const int m = c / G;
+  const int qh = c - m * G;
+  const int member = (m < kSCols / G) ? a.plan[kPlanVmem + i * kSCols + m] : -1;
+  valid = member >= 0;
+  qrow = valid ? member : 0;
+  qhead = h * G + (valid ? qh : 0);
+}
+
+// Two 8-wave workgroups per CU need 4 waves per SIMD: at most 128 VGPRs.
 template <int QDT, bool QVEC>
-__global__ void __launch_bounds__(kSThreads, kSWgPerCu)
+__global__ void __launch_bounds__(kSThreads) __attribute__((amdgpu_waves_per_eu(2 * kSWgPerCu)))
 paged_decode_stream_kernel(const DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t stages[kSStages * kSStage];
-  __shared__ int tstart[kSMaxBatch + 1];
-  __shared__ int scan[kSThreads];
+  __shared__ int tstart[kSMaxBatch + kSMaxVirt + 1];
   const int lane = threadIdx.x & 63;
   const int h = threadIdx.x >> 6;
   const int g = lane >> 4;
   const int c = lane & 15;
-  const int G = a.groups;
   const int B = a.batch;
 
-  // ---- prefix sums of per-sequence tile counts (every workgroup computes them)
-  if (threadIdx.x == 0) tstart[0] = 0;
-  for (int base = 0; base < B; base += kSThreads) {
-    __syncthreads();
-    const int bb = base + threadIdx.x;
-    const int n = bb < B ? (effective_len(a, bb) + kSTile - 1) / kSTile : 0;
-    scan[threadIdx.x] = n;  // inclusive Hillis-Steele scan through LDS
-    __syncthreads();
-    for (int off = 1; off < kSThreads; off <<= 1) {
-      const int v = threadIdx.x >= off ? scan[threadIdx.x - off] : 0;
-      __syncthreads();
-      scan[threadIdx.x] += v;
-      __syncthreads();
-    }
-    if (bb < B) tstart[bb + 1] = tstart[base] + scan[threadIdx.x];
-  }
-  __syncthreads();
-  const int64_t total = tstart[B];
-  const int64_t nwg = gridDim.x;
-  const int64_t s = static_cast<int64_t>(blockIdx.x) * total / nwg;
-  const int64_t e = static_cast<int64_t>(blockIdx.x + 1) * total / nwg;
+  // ---- the plan's tile prefix sums (virtual sequences, then real ones)
+  const int V = ld_meta(a.plan);
+  const int NS = B + V;
+  const int64_t total = ld_meta(a.plan + 1);
+  for (int i = threadIdx.x; i <= NS; i += kSThreads) tstart[i] = a.plan[kPlanTstart + i];
+  const StreamSplit sp = stream_split(a, total);
+  const int64_t s = split_begin(sp, blockIdx.x);
+  const int64_t e = split_begin(sp, blockIdx.x + 1);
   if (s >= e) return;  // uniform across the workgroup
+  __syncthreads();
+  const uint64_t t_begin = __builtin_amdgcn_s_memrealtime();
 
   const StreamLanePlan pl = stream_plan(h, lane);
   const uint32_t stage0 = lds_addr(stages);
   const int64_t count = e - s;
 
-  // ---- issue-side tile iterator: sequence ib, local tile ilt of int_ tiles;
-  // the block id is re-read only when the page changes.
+  // ---- issue-side tile iterator: stream entry ib, local tile ilt of intl
+  // tiles; the block id is re-read only when the page changes.
   int ib = 0;
-  advance_seq(tstart, B, s, ib);
+  advance_seq(tstart, NS, s, ib);
   int ilt = __builtin_amdgcn_readfirstlane(static_cast<int>(s - tstart[ib]));
   int intl = __builtin_amdgcn_readfirstlane(tstart[ib + 1] - tstart[ib]);
+  int ibt_row, itok0, iend, irot;
+  stream_seq(a, tstart, V, ib, ibt_row, itok0, iend, irot);
   int ipage = -1, iblk = 0;
   int64_t issued = 0;
   auto issue_next = [&]() {
-    const int t0 = ilt * kSTile;
+    const int lr = ilt + irot;
+    const int t0 = itok0 + (lr >= intl ? lr - intl : lr) * kSTile;
     const int page = __builtin_amdgcn_readfirstlane(t0 / a.page_size);
     if (page != ipage) {
       ipage = page;
-      const int32_t raw = ld_meta(a.bt + static_cast<int64_t>(ib) * a.bt_sb + static_cast<int64_t>(page) * a.bt_sn);
+      const int32_t raw =
+          ld_meta(a.bt + static_cast<int64_t>(ibt_row) * a.bt_sb + static_cast<int64_t>(page) * a.bt_sn);
       iblk = (raw >= 0 && raw < a.num_blocks) ? raw : 0;
     }
     if (!(a.debug & 2)) stream_issue(a, pl, t0, iblk, stage0 + static_cast<uint32_t>(issued % kSStages) * kSStage);
     ++issued;
-    if (++ilt == intl && issued < count) {  // next sequence with tiles
+    if (++ilt == intl && issued < count) {  // next stream entry with tiles
       do {
         ++ib;
         intl = __builtin_amdgcn_readfirstlane(tstart[ib + 1] - tstart[ib]);
-      } while (intl == 0 && ib + 1 < B);
+      } while (intl == 0 && ib + 1 < NS);
       ib = __builtin_amdgcn_readfirstlane(ib);
       ilt = 0;
       ipage = -1;
+      stream_seq(a, tstart, V, ib, ibt_row, itok0, iend, irot);
     }
   };
 #pragma unroll
@@ -799,18 +1162,24 @@ paged_decode_stream_kernel(const DecodeArgs a) {
 
   // ---- compute-side iterator (same walk, one tile behind)
   int b = 0;
-  advance_seq(tstart, B, s, b);
+  advance_seq(tstart, NS, s, b);
   int lt = __builtin_amdgcn_readfirstlane(static_cast<int>(s - tstart[b]));
   int ntl = __builtin_amdgcn_readfirstlane(tstart[b + 1] - tstart[b]);
+  int cbt_row, ctok0, n_eff, crot;
+  stream_seq(a, tstart, V, b, cbt_row, ctok0, n_eff, crot);
   int cpage = -1, cok = 0;
   QOperand<QDT> qop;
-  stream_load_q<QDT, QVEC>(a, b, h, g, c, qop);
-  int n_eff = effective_len(a, b);
+  bool colv;
+  {
+    int qrow, qhead;
+    stream_column(a, V, b, h, c, qrow, qhead, colv);
+    stream_load_q<QDT, QVEC>(a, qrow, qhead, colv, g, qop);
+  }
 
   floatx4 acc[8];
 #pragma unroll
   for (int j = 0; j < 8; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY;  // running max (log2 domain) of q head c
+  float m_run = -INFINITY;  // running max (log2 domain) of query column c
   float l_run = 0.f;        // this lane's share of the running sum
 
   // Per-lane LDS offsets inside a stage (loop invariant).
@@ -842,12 +1211,14 @@ paged_decode_stream_kernel(const DecodeArgs a) {
     stream_barrier();
     if (issued < count) issue_next();
 
-    const int t0 = lt * kSTile;
+    const int lr = lt + crot;
+    const int t0 = ctok0 + (lr >= ntl ? lr - ntl : lr) * kSTile;
     {
       const int page = __builtin_amdgcn_readfirstlane(t0 / a.page_size);
       if (page != cpage) {
         cpage = page;
-        const int32_t raw = ld_meta(a.bt + static_cast<int64_t>(b) * a.bt_sb + static_cast<int64_t>(page) * a.bt_sn);
+        const int32_t raw =
+            ld_meta(a.bt + static_cast<int64_t>(cbt_row) * a.bt_sb + static_cast<int64_t>(page) * a.bt_sn);
         cok = raw >= 0 && raw < a.num_blocks;
       }
     }
@@ -889,7 +1260,7 @@ paged_decode_stream_kernel(const DecodeArgs a) {
       for (int i = 0; i < 4; ++i) {
         const bool tv = t0 + 4 * g + i < n_eff;
         valid |= tv ? (1u << i) : 0u;
-        x[i] = (tv && c < G) ? (sca[i] + scb[i]) * (ks[i] * a.scale_log2) : -INFINITY;
+        x[i] = (tv && colv) ? (sca[i] + scb[i]) * (ks[i] * a.scale_log2) : -INFINITY;
         tmax = fmaxf(tmax, x[i]);
       }
       tmax = wave_max_across_groups(tmax);
@@ -934,20 +1305,25 @@ paged_decode_stream_kernel(const DecodeArgs a) {
       }
     }
 
-    // ---- advance the compute iterator; flush at the end of a sequence
+    // ---- advance the compute iterator; flush at the end of a stream entry
     const bool more = done + 1 < count;
     const bool seq_ends = !more || lt + 1 == ntl;
     if (seq_ends) {
       float l_tot = l_run + __shfl_xor(l_run, 16);
       l_tot += __shfl_xor(l_tot, 32);
-      const int64_t pidx = static_cast<int64_t>(blockIdx.x) + b;
+      // partial rows: real entry b at (wg + b) * Hq + q head; virtual entry v
+      // at vrow0 + ((wg + v) * 8 + h) * 16 + column
+      const bool virt = b < V;
+      const int ncols = virt ? kSCols : a.groups;
+      const int64_t row0 = virt ? a.vrow0 + ((static_cast<int64_t>(blockIdx.x) + b) * kSKv + h) * kSCols
+                                : (static_cast<int64_t>(blockIdx.x) + b) * a.num_heads + h * a.groups;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int qr = 4 * g + i;
         const float li = __shfl(l_tot, qr);
         const float mi = __shfl(m_run, qr);
-        if (qr < G) {
-          const int64_t row = pidx * a.num_heads + h * G + qr;
+        if (qr < ncols) {
+          const int64_t row = row0 + qr;
           float* dst = a.part_acc + row * kHeadDim + c;
 #pragma unroll
           for (int j = 0; j < 8; ++j) dst[16 * j] = acc[j][i];
@@ -965,94 +1341,102 @@ paged_decode_stream_kernel(const DecodeArgs a) {
         do {
           ++b;
           ntl = __builtin_amdgcn_readfirstlane(tstart[b + 1] - tstart[b]);
-        } while (ntl == 0 && b + 1 < B);
+        } while (ntl == 0 && b + 1 < NS);
         b = __builtin_amdgcn_readfirstlane(b);
         lt = 0;
         cpage = -1;
-        n_eff = effective_len(a, b);
-        stream_load_q<QDT, QVEC>(a, b, h, g, c, qop);
+        stream_seq(a, tstart, V, b, cbt_row, ctok0, n_eff, crot);
+        int qrow, qhead;
+        stream_column(a, V, b, h, c, qrow, qhead, colv);
+        stream_load_q<QDT, QVEC>(a, qrow, qhead, colv, g, qop);
       }
     } else {
       ++lt;
     }
   }
+  if ((a.debug & 8) && threadIdx.x == 0) {  // measurement aid: start and end (100 MHz clock)
+    const uint64_t t_end = __builtin_amdgcn_s_memrealtime();
+    a.plan[kPlanWgTime + 2 * blockIdx.x] = static_cast<int>(t_begin & 0x7FFFFFFF);
+    a.plan[kPlanWgTime + 2 * blockIdx.x + 1] = static_cast<int>(t_end & 0x7FFFFFFF);
+  }
 }
 
 // Merge the streaming partials: grid (batch, num_heads), one wave each.
-// The contributing workgroups are handled lane-parallel: lane i reads the
-// (m, l) of workgroup w_lo + i (+64k), the weights go through LDS, then each
-// lane accumulates two output dims over the workgroups.
-constexpr int kSMaxWg = 1024;
-
+// A sequence's partials come from the workgroups whose tile ranges meet its
+// own tiles (its private tail) and, when it belongs to a virtual sequence,
+// from those that walked its shared pages.  Lane i reads the (m, l) of
+// candidate i (+64k); candidates that wrote a partial are compacted into
+// LDS, then every lane accumulates two output dims.
 template <int QDT>
-__global__ void __launch_bounds__(64) paged_decode_stream_combine_kernel(const DecodeArgs a, int nwg) {
-  __shared__ float wts[kSMaxWg];
+__global__ void __launch_bounds__(64) paged_decode_stream_combine_kernel(const DecodeArgs a) {
+  // the tail's and the virtual sequence's tile ranges are disjoint, so at
+  // most one workgroup meets both: at most nwg + 1 candidates
+  __shared__ float m_s[kSMaxWg + 1];
+  __shared__ float l_s[kSMaxWg + 1];
+  __shared__ int rows[kSMaxWg + 1];
   const int b = blockIdx.x;
   const int hq = blockIdx.y;
   const int lane = threadIdx.x;
-  int64_t before = 0, total = 0;
-  for (int bb = lane; bb < a.batch; bb += 64) {
-    const int64_t n = (effective_len(a, bb) + kSTile - 1) / kSTile;
-    total += n;
-    if (bb < b) before += n;
+  const int V = ld_meta(a.plan);
+  const StreamSplit sp = stream_split(a, ld_meta(a.plan + 1));
+  const int first = ld_meta(a.plan + kPlanTstart + V + b);
+  const int end = ld_meta(a.plan + kPlanTstart + V + b + 1);
+  const int vslot = ld_meta(a.plan + kPlanVslot + b);
+  int lo0 = 0, cnt0 = 0, lo1 = 0, cnt1 = 0;
+  if (end > first) {
+    lo0 = static_cast<int>(split_owner(sp, first));
+    cnt0 = static_cast<int>(split_owner(sp, end - 1)) - lo0 + 1;
   }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) {
-    total += __shfl_xor(total, off);
-    before += __shfl_xor(before, off);
+  // row of workgroup w: real (w + V + b) * Hq + hq; virtual vrow0 + ((w + v) * 8 + hk) * 16 + col
+  const int64_t rbase0 = static_cast<int64_t>(V + b) * a.num_heads + hq;
+  int64_t rbase1 = 0;
+  if (vslot >= 0) {
+    const int v = vslot / kSCols;
+    const int m = vslot - v * kSCols;
+    const int hk = hq / a.groups;
+    rbase1 = a.vrow0 + (static_cast<int64_t>(v) * kSKv + hk) * kSCols + m * a.groups + (hq - hk * a.groups);
+    const int vfirst = ld_meta(a.plan + kPlanTstart + v);
+    const int vend = ld_meta(a.plan + kPlanTstart + v + 1);
+    lo1 = static_cast<int>(split_owner(sp, vfirst));
+    cnt1 = static_cast<int>(split_owner(sp, vend - 1)) - lo1 + 1;
   }
-  const int64_t n_b = (effective_len(a, b) + kSTile - 1) / kSTile;
-  const int64_t base = static_cast<int64_t>(b) * a.o_sb + static_cast<int64_t>(hq) * a.o_sh;
-  if (n_b == 0) {
-    store_out<QDT>(a.out, base + lane * a.o_sd, 0.f);
-    store_out<QDT>(a.out, base + (lane + 64) * a.o_sd, 0.f);
-    return;
-  }
-  // workgroups whose range [w*total/nwg, (w+1)*total/nwg) meets [before, before + n_b)
-  const int64_t first_tile = before, last_tile = before + n_b - 1;
-  auto owner = [&](int64_t tile) {  // the workgroup whose range holds `tile`
-    int64_t w = (tile * nwg) / total;
-    while (w > 0 && (w * total) / nwg > tile) --w;
-    while (((w + 1) * total) / nwg <= tile) ++w;
-    return w;
-  };
-  const int64_t w_lo = owner(first_tile);
-  const int64_t w_hi = owner(last_tile);
-  const int cnt = static_cast<int>(w_hi - w_lo + 1);
-  // pass 1: (m, l) lane-parallel; workgroups with an empty range wrote nothing
+  const int cnt = cnt0 + cnt1;
+  int nvalid = 0;
   float m_max = -INFINITY;
-  for (int i = lane; i < cnt; i += 64) {
-    const int64_t w = w_lo + i;
-    const bool has = (w * total) / nwg < ((w + 1) * total) / nwg;
-    const float m = has ? a.part_ml[((w + b) * a.num_heads + hq) * 2] : -INFINITY;
-    wts[i] = m;
-    m_max = fmaxf(m_max, m);
+  for (int base = 0; base < cnt; base += 64) {
+    const int i = base + lane;
+    const bool second = i >= cnt0;
+    const int64_t w = second ? lo1 + (i - cnt0) : lo0 + i;
+    bool ok = i < cnt && split_begin(sp, w) < split_begin(sp, w + 1);
+    const int64_t row = second ? rbase1 + w * (kSKv * kSCols) : rbase0 + w * a.num_heads;
+    float2 ml = {-INFINITY, 0.f};
+    if (ok) ml = *reinterpret_cast<const float2*>(a.part_ml + row * 2);
+    ok = ok && ml.x != -INFINITY;  // a partial with nothing attended weighs 0
+    const uint64_t mask = __builtin_amdgcn_ballot_w64(ok);
+    const int pos = nvalid + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                                       __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0));
+    if (ok) {
+      m_s[pos] = ml.x;
+      l_s[pos] = ml.y;
+      rows[pos] = static_cast<int>(row);
+      m_max = fmaxf(m_max, ml.x);
+    }
+    nvalid += __builtin_popcountll(mask);
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) m_max = fmaxf(m_max, __shfl_xor(m_max, off));
-  const float m_use = (m_max == -INFINITY) ? 0.f : m_max;
-  float l_sum = 0.f;
-  for (int i = lane; i < cnt; i += 64) {
-    const int64_t w = w_lo + i;
-    const float m = wts[i];
-    const float wgt = (m == -INFINITY) ? 0.f : exp2f(m - m_use);
-    if (wgt > 0.f) l_sum += wgt * a.part_ml[((w + b) * a.num_heads + hq) * 2 + 1];
-    wts[i] = wgt;
-  }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) l_sum += __shfl_xor(l_sum, off);
   __syncthreads();
-  // pass 2: weighted sum of the accumulators
-  float o0 = 0.f, o1 = 0.f;
+  float l_sum = 0.f, o0 = 0.f, o1 = 0.f;
 #pragma unroll 4
-  for (int i = 0; i < cnt; ++i) {
-    const float wgt = wts[i];
-    if (wgt == 0.f) continue;
-    const float* src = a.part_acc + ((w_lo + i + b) * a.num_heads + hq) * kHeadDim;
+  for (int i = 0; i < nvalid; ++i) {
+    const float wgt = exp2f(m_s[i] - m_max);
+    const float* src = a.part_acc + static_cast<int64_t>(rows[i]) * kHeadDim;
+    l_sum += wgt * l_s[i];
     o0 += wgt * src[lane];
     o1 += wgt * src[lane + 64];
   }
   const float inv = l_sum > 0.f ? 1.f / l_sum : 0.f;
+  const int64_t base = static_cast<int64_t>(b) * a.o_sb + static_cast<int64_t>(hq) * a.o_sh;
   store_out<QDT>(a.out, base + lane * a.o_sd, o0 * inv);
   store_out<QDT>(a.out, base + (lane + 64) * a.o_sd, o1 * inv);
 }
@@ -1169,7 +1553,7 @@ struct Geometry {
   // streaming path (canonical layout only; chosen per call from the strides)
   bool stream_shape;
   int stream_nwg;
-  int64_t stream_acc_off, stream_ml_off;
+  int64_t stream_acc_off, stream_ml_off, stream_vrow0;
 };
 
 // PRISM_DECODE_PATH=split|stream forces a kernel family (tests, A/B runs);
@@ -1219,12 +1603,16 @@ Geometry geometry(int batch, int num_heads, int num_kv_heads, int head_dim, int 
   geo.split = choose_split(batch, num_kv_heads, page_size, width);
   const int64_t cap = static_cast<int64_t>(width) * page_size;
   geo.max_splits = static_cast<int>(cap > 0 ? ceil_div(cap, geo.split) : 1);
+  // Every fast-path workspace starts with the streaming kernel's plan region,
+  // which only the plan kernel writes (a workspace shared by calls of
+  // different geometries never has its plan overwritten by split partials).
+  const int64_t plan_bytes = align_up(static_cast<int64_t>(kPlanInts) * 4, 256);
   if (geo.max_splits <= 1) {
     geo.ws_bytes = 0;
   } else {
     const int64_t rows = static_cast<int64_t>(batch) * geo.max_splits * num_heads;
-    geo.acc_off = 0;
-    geo.ml_off = align_up(rows * head_dim * 4, 256);
+    geo.acc_off = plan_bytes;
+    geo.ml_off = geo.acc_off + align_up(rows * head_dim * 4, 256);
     geo.ws_bytes = geo.ml_off + align_up(rows * 2 * 4, 256);
   }
   geo.stream_shape = num_kv_heads == kSKv && page_size % kSTile == 0 && batch <= kSMaxBatch && !stream_disabled() &&
@@ -1234,10 +1622,17 @@ Geometry geometry(int batch, int num_heads, int num_kv_heads, int head_dim, int 
     if (cap_tiles < 8LL * device_cu_count() * kSWgPerCu) geo.stream_shape = false;
   }
   if (geo.stream_shape) {
+    // workspace: shared-page plan, then partial rows of the real sequences
+    // and of the virtual ones
     geo.stream_nwg = device_cu_count() * kSWgPerCu;
-    const int64_t rows = (static_cast<int64_t>(geo.stream_nwg) + batch) * num_heads;
-    geo.stream_acc_off = 0;
-    geo.stream_ml_off = align_up(rows * head_dim * 4, 256);
+    const int members = kSCols / (num_heads / num_kv_heads);
+    const int64_t vmax = (batch <= kSShareMaxBatch && members >= 2) ? std::min(kSMaxVirt, batch / 2) : 0;
+    // real rows: (wg + V + b); virtual rows: (wg + v)
+    geo.stream_vrow0 = (static_cast<int64_t>(geo.stream_nwg) + vmax + batch) * num_heads;
+    const int64_t rows =
+        geo.stream_vrow0 + (vmax > 0 ? (static_cast<int64_t>(geo.stream_nwg) + vmax) * kSKv * kSCols : 0);
+    geo.stream_acc_off = plan_bytes;
+    geo.stream_ml_off = geo.stream_acc_off + align_up(rows * head_dim * 4, 256);
     const int64_t need = geo.stream_ml_off + align_up(rows * 2 * 4, 256);
     if (need > geo.ws_bytes) geo.ws_bytes = need;
   }
@@ -1246,18 +1641,24 @@ Geometry geometry(int batch, int num_heads, int num_kv_heads, int head_dim, int 
 
 template <int QDT>
 int launch_stream(int stage, const DecodeArgs& args, const Geometry& geo, hipStream_t stream) {
-  if (stage != 2) {
+  if (stage == 0 || stage == 3) {
+    hipLaunchKernelGGL(paged_decode_stream_plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, args);
+    int rc = check_launch("paged_decode_stream_plan_kernel launch");
+    if (rc || stage == 3) return rc;
+  }
+  if (stage == 0 || stage == 1) {
+    int rc;
     if (args.q_vec)
       hipLaunchKernelGGL((paged_decode_stream_kernel<QDT, true>), dim3(geo.stream_nwg), dim3(kSThreads), 0, stream, args);
     else
       hipLaunchKernelGGL((paged_decode_stream_kernel<QDT, false>), dim3(geo.stream_nwg), dim3(kSThreads), 0, stream,
                          args);
-    int rc = check_launch("paged_decode_stream_kernel launch");
+    rc = check_launch("paged_decode_stream_kernel launch");
     if (rc) return rc;
   }
   if (stage != 1) {
     hipLaunchKernelGGL(paged_decode_stream_combine_kernel<QDT>, dim3(args.batch, args.num_heads), dim3(64), 0, stream,
-                       args, geo.stream_nwg);
+                       args);
     return check_launch("paged_decode_stream_combine_kernel launch");
   }
   return PRISM_OK;
@@ -1267,6 +1668,7 @@ template <int QDT>
 int launch_all(int stage, const DecodeArgs& args, const Geometry& geo, bool page_aligned, bool use_stream,
                hipStream_t stream) {
   if (use_stream) return launch_stream<QDT>(stage, args, geo, stream);
+  if (stage == 3) return PRISM_OK;  // no plan outside the streaming kernel
   const bool scaled = args.ks != nullptr;
   if (!geo.fast) {
     if (stage == 2) return PRISM_OK;
@@ -1340,8 +1742,8 @@ extern "C" int prism_paged_decode_stage(
     void* stream_ptr) {
   using namespace prism;
   clear_error();
-  if (stage < 0 || stage > 2) {
-    set_error("prism_paged_decode: stage must be 0, 1 or 2");
+  if (stage < 0 || stage > 3) {
+    set_error("prism_paged_decode: stage must be 0, 1, 2 or 3");
     return PRISM_ERR_INVALID;
   }
   if (batch < 0 || num_heads <= 0 || num_kv_heads <= 0 || head_dim <= 0 || page_size <= 0 ||
@@ -1471,8 +1873,13 @@ extern "C" int prism_paged_decode_stage(
                           ks_strides[0] == vs_strides[0] && aligned(k_scale, 16) && aligned(v_scale, 16) &&
                           ks_strides[0] % 4 == 0;
   if (use_stream) {
+    args.plan = static_cast<int*>(workspace);
     args.part_acc = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + geo.stream_acc_off);
     args.part_ml = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + geo.stream_ml_off);
+    args.vrow0 = geo.stream_vrow0;
+    const char* share = getenv("PRISM_DECODE_SHARE");  // "0" turns the shared-page analysis off
+    args.share = !(share && share[0] == '0');
+    args.stream_nwg = geo.stream_nwg;
   }
   hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
   switch (q_dtype) {

@@ -172,6 +172,29 @@ def decode_workspace_bytes(q: torch.Tensor, k_cache: torch.Tensor, block_tables:
         _native.dtype_code(k_cache.dtype)))
 
 
+# One decode workspace per (device, stream), reused across calls: besides the
+# split-K partials it holds the streaming kernel's work plan together with
+# the inputs the plan was computed from, so consecutive calls with the same
+# metadata (every layer of a decode step) skip recomputing it.  Calls on one
+# stream are ordered, so they may share it; other streams get their own.
+# Under graph capture a fresh buffer from the graph's pool is used instead.
+_WORKSPACES: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def decode_workspace(device: torch.device, nbytes: int) -> torch.Tensor:
+    """The reused decode workspace of the current stream (at least ``nbytes``)."""
+
+    if torch.cuda.is_current_stream_capturing():
+        return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+    index = device.index if device.index is not None else torch.cuda.current_device()
+    key = (index, torch.cuda.current_stream(device).cuda_stream)
+    ws = _WORKSPACES.get(key)
+    if ws is None or ws.numel() < nbytes:
+        ws = torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+        _WORKSPACES[key] = ws
+    return ws
+
+
 def _launch_paged_decode_attention(q, k_cache, v_cache, block_tables, context_lens, scale, max_context_len, *,
                                    k_scale_cache, v_scale_cache, scaled_kv, stage: int = 0,
                                    output: torch.Tensor | None = None,
@@ -183,7 +206,7 @@ def _launch_paged_decode_attention(q, k_cache, v_cache, block_tables, context_le
         output = torch.empty_like(q)
     ws_bytes = decode_workspace_bytes(q, k_cache, block_tables)
     if ws_bytes > 0 and (workspace is None or workspace.numel() < ws_bytes):
-        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=q.device)
+        workspace = decode_workspace(q.device, ws_bytes)
     zero3 = _native.int64s(0, 0, 0)
     with torch.cuda.device(q.device):
         status = lib.prism_paged_decode_stage(
@@ -239,6 +262,7 @@ __all__ = [
     "DEFAULT_PAGED_DECODE_BLOCK_N",
     "HAS_HIP_KERNELS",
     "HAS_TRITON",
+    "decode_workspace",
     "decode_workspace_bytes",
     "paged_decode_attention",
 ]

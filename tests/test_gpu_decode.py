@@ -253,3 +253,130 @@ def test_graph_replay_follows_device_metadata(decode_path):
         want = _oracle(q.cpu(), k, v, ks, vs, tables.cpu(), lens.cpu(), 0.09)
         assert_decode_close(captured, want, label=f"replay len {new_len}")
         assert torch.equal(captured.cpu(), eager.cpu())
+
+
+def test_shared_prefix_groups(decode_path, monkeypatch):
+    """Prefix groups in every shape the shared-page analysis must handle.
+
+    Group A (7 members, not contiguous in the batch: virtual sequences of 4 and
+    3) shares 6 pages, but one member covers only 3 whole pages, one diverges
+    at page 4 and one shares only the first page; group B (3 members) shares 3
+    pages; a member of B has a hole at page 1; a ctx = 0 row starts with A's
+    first page; the rest are private.  Also with max_context_len cutting into
+    the shared pages, and with the analysis switched off.
+    """
+
+    require_gpu()
+    g = torch.Generator().manual_seed(20260811)
+    pool, width, batch = 260, 12, 24
+    q = torch.randn(batch, 32, 128, generator=g).to(torch.bfloat16)
+    k, ks = _quantize_cpu(torch.randn(pool, 256, 8, 128, generator=g).to(torch.bfloat16))
+    v, vs = _quantize_cpu(torch.randn(pool, 256, 8, 128, generator=g).to(torch.bfloat16))
+    perm = torch.randperm(pool, generator=g).to(torch.int32)
+    cursor = 0
+
+    def take(n):
+        nonlocal cursor
+        cursor += n
+        return perm[cursor - n:cursor]
+
+    pre_a, pre_b = take(6), take(3)
+    tables = torch.full((batch, width), -1, dtype=torch.int32)
+    lens = torch.zeros(batch, dtype=torch.int32)
+    group_a, group_b = [0, 3, 5, 8, 11, 15, 19], [2, 9, 20]
+    for b in range(batch):
+        if b in group_a:
+            tables[b, :6] = pre_a
+            tables[b, 6:] = take(width - 6)
+            lens[b] = 6 * 256 + int(torch.randint(1, 1400, (1,), generator=g))
+        elif b in group_b:
+            tables[b, :3] = pre_b
+            tables[b, 3:] = take(width - 3)
+            lens[b] = 3 * 256 + int(torch.randint(1, 2000, (1,), generator=g))
+        else:
+            tables[b] = take(width)
+            lens[b] = int(torch.randint(1, width * 256, (1,), generator=g))
+    lens[5] = 3 * 256 + 100                 # covers 3 whole shared pages
+    tables[11, 4] = take(1)[0]              # diverges at page 4
+    tables[13, 0] = pre_a[0]                # shares only A's first page
+    lens[13] = 2000
+    tables[22, 0] = pre_a[0]                # ctx = 0 row with A's first page
+    lens[22] = 0
+    tables[9, 1] = -1                       # B member with a hole at page 1
+    assert cursor <= pool
+    want = _oracle(q, k, v, ks, vs, tables, lens, 0.0883)
+    got = _decode_gpu(q, k, v, ks, vs, tables, lens, 0.0883)
+    assert_decode_close(got, want, label="shared groups")
+    assert torch.all(got[22] == 0)
+    got_cap = _decode_gpu(q, k, v, ks, vs, tables, lens, 0.0883, max_ctx=700)
+    assert_decode_close(got_cap, _oracle(q, k, v, ks, vs, tables, lens, 0.0883, max_ctx=700), label="max_ctx 700")
+    monkeypatch.setenv("PRISM_DECODE_SHARE", "0")
+    plain = _decode_gpu(q, k, v, ks, vs, tables, lens, 0.0883)
+    assert_decode_close(plain, want, label="sharing analysis off")
+
+
+def test_large_batch_prefix_groups_deterministic(monkeypatch):
+    """128 sequences of ~2k-5k tokens with two prefix groups (14 members sharing
+    5 pages, 21 sharing 2) on the streaming kernel: oracle parity, and
+    bit-identical results across runs."""
+
+    require_gpu()
+    from prism_infer.ops.paged_decode import paged_decode_attention
+
+    monkeypatch.setenv("PRISM_DECODE_PATH", "stream")
+    g = torch.Generator().manual_seed(20260812)
+    batch, width, pool = 128, 20, 2600
+    dev = torch.device("cuda")
+    q = torch.randn(batch, 32, 128, generator=g).to(torch.bfloat16)
+    k, ks = _quantize_cpu(torch.randn(pool, 256, 8, 128, generator=g).to(torch.bfloat16))
+    v, vs = _quantize_cpu(torch.randn(pool, 256, 8, 128, generator=g).to(torch.bfloat16))
+    tables = torch.randperm(pool, generator=g)[: batch * width].to(torch.int32).view(batch, width).clone()
+    tables[1:40:3, :5] = tables[0, :5]       # group of 14 sharing 5 pages
+    tables[70:90, :2] = tables[60, :2]       # group of 21 sharing 2 pages
+    lens = torch.randint(2000, width * 256, (batch,), generator=g, dtype=torch.int32)
+    to = lambda t: t.view(torch.uint8).to(dev).view(FP8) if t.dtype == FP8 else t.to(dev)
+    args = (to(q), to(k), to(v), to(tables), to(lens), 0.0883)
+    kw = dict(k_scale_cache=to(ks), v_scale_cache=to(vs))
+    first = paged_decode_attention(*args, **kw)
+    second = paged_decode_attention(*args, **kw)
+    torch.cuda.synchronize()
+    assert torch.equal(first, second)
+    want = oracle.decode_kernel_semantics(q, k, v, tables, lens, 0.0883, k_scale_cache=ks, v_scale_cache=vs,
+                                          compute_dtype=torch.float32)
+    assert_decode_close(first, want, label="large batch")
+
+
+def test_plan_reuse_across_calls_and_geometries():
+    """The streaming kernel's plan is kept in the per-stream workspace and reused
+    while the metadata is unchanged: a call of another geometry in between (the
+    per-split path, same workspace) must not disturb it, and a change of the
+    metadata in place must be picked up."""
+
+    require_gpu()
+    from prism_infer.ops.paged_decode import paged_decode_attention
+    from prism_infer.workloads import decode_mixed
+
+    dev = torch.device("cuda")
+    w = decode_mixed(dev)
+    run = lambda: paged_decode_attention(w.q, w.k_cache, w.v_cache, w.block_tables, w.context_lens, w.scale,
+                                         k_scale_cache=w.k_scale, v_scale_cache=w.v_scale,
+                                         max_context_len=w.max_context_len)
+    first = run()
+    small = paged_decode_attention(w.q[:2], w.k_cache, w.v_cache, w.block_tables[:2], w.context_lens[:2], w.scale,
+                                   k_scale_cache=w.k_scale, v_scale_cache=w.v_scale)
+    again = run()
+    torch.cuda.synchronize()
+    assert torch.equal(first, again)
+    q, k, v, ks, vs, tables, lens, mx = compact_to_cpu(w)
+    want_small = oracle.decode_kernel_semantics(q[:2], k, v, tables[:2], lens[:2], w.scale, k_scale_cache=ks,
+                                                v_scale_cache=vs, compute_dtype=torch.float32)
+    assert_decode_close(small, want_small, label="small call in between")
+    # shrink one sharing sequence below the shared prefix and another one a little
+    sharing = w.meta["sharing"]
+    w.context_lens[sharing[0]] = 1000
+    w.context_lens[sharing[1]] -= 300
+    changed = run()
+    lens2 = w.context_lens.cpu()
+    want = oracle.decode_kernel_semantics(q, k, v, tables, lens2, w.scale, k_scale_cache=ks, v_scale_cache=vs,
+                                          max_context_len=mx, compute_dtype=torch.float32)
+    assert_decode_close(changed, want, label="metadata changed in place")
