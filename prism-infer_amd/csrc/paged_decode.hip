@@ -506,22 +506,29 @@ __global__ void __launch_bounds__(64) paged_decode_combine_kernel(const DecodeAr
 // Persistent, tile-balanced kernel for the canonical page layout
 // ([num_blocks][P % 16 == 0][8 kv heads][128] FP8, scales [num_blocks][P][8]):
 //
+// * Three kernels: a one-workgroup plan kernel (prefix-sharing groups and the
+//   tile prefix sums, see "shared pages" below), the streaming kernel, and
+//   the merge of its partials.
 // * Two workgroups (8 waves each, wave = kv head) per CU.  The 16-token tiles
-//   of all sequences, concatenated in batch order, are split into gridDim.x
-//   equal contiguous ranges, so every CU streams the same number of bytes
-//   whatever the context-length mix.  A range spanning several sequences emits one
-//   (m, l, acc) partial per (workgroup, sequence) pair; as ranges are
-//   contiguous and monotone the pairs form a staircase and `wg + seq` indexes
-//   them uniquely.  The combine kernel merges them.
+//   of the stream (virtual sequences over shared pages first, then every
+//   sequence's own tiles) are split into gridDim.x equal contiguous ranges, so
+//   every CU streams the same number of bytes whatever the context-length
+//   mix.  A range spanning several stream entries emits one (m, l, acc)
+//   partial per (workgroup, entry) pair; as ranges are contiguous and
+//   monotone the pairs form a staircase and `wg + entry` indexes them
+//   uniquely.  The merge kernel combines them.
 // * A tile is one contiguous slab per tensor (K [16 tok][8 h][128 B], V
 //   likewise, and the fp32 scales).  The workgroup copies tiles straight into
 //   LDS with global_load_lds (16 B per lane), two stages per workgroup, so
 //   while one workgroup computes a tile the CU has up to three more (about
-//   100 KB) in flight and no VGPRs hold prefetched data.  16-byte chunks of a head row are XOR-swizzled by token
-//   so row-parallel K reads and transposed V reads spread over the banks.
+//   100 KB) in flight and no VGPRs hold prefetched data.  16-byte chunks of a
+//   head row are XOR-swizzled by token so row-parallel K reads and transposed
+//   V reads spread over the banks.
 //   Scales are stored [head][token] so a lane's four tokens are one 16-byte read.
 // * QK: 4 MFMA f32_16x16x32_bf16 per tile (A = K rows fp8 -> bf16, exact;
-//   B = Q^T).  Lane (g, c) gets the scores of q head c for tokens 4g..4g+3.
+//   B = Q^T, 16 query columns: the G heads of one sequence, or of up to 16/G
+//   sequences for a virtual sequence).  Lane (g, c) gets the scores of query
+//   column c for tokens 4g..4g+3.
 // * PV: MFMA f32_16x16x16_bf16, whose four k slots per lane are exactly those
 //   four tokens, so P needs no data movement; P * v_scale is split into a
 //   bf16 hi/lo pair (two MFMAs) for fp32-like accuracy.  The V operand comes
