@@ -57,6 +57,35 @@ def _time_loop(fn, steps: int, torch) -> float:
     return start.elapsed_time(end) / 1e3 / steps
 
 
+def _time_graph(fn, calls: int, torch, *, reps: int = 5, flush=None) -> float:
+    """Median seconds per call of ``fn`` with ``calls`` calls captured in one
+    HIP graph (GPU time, no host launch overhead), replayed ``reps`` times;
+    ``flush()`` runs before each replay, outside the timed region."""
+
+    for i in range(calls):  # eager warm-up (allocations, plans)
+        fn(i)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for i in range(calls):
+            fn(i)
+    graph.replay()
+    torch.cuda.synchronize()
+    times = []
+    for _ in range(reps):
+        if flush is not None:
+            flush()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record()
+        graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        times.append(start.elapsed_time(end) / 1e3 / calls)
+    times.sort()
+    return times[len(times) // 2]
+
+
 def _cpu_baseline(w, budget_s: float, torch) -> dict:
     """Time the CPU restatement of the reference decode path on a bounded sample."""
 
@@ -239,25 +268,29 @@ def main() -> int:
 
 
 def _extras(torch, dev, workloads) -> dict:
-    """Store (prefill chunk), compaction and single-sequence decode timings."""
+    """GPU time of the other configurations: store (config 2), compaction
+    (config 5), B = 1 decode over 36 layers (config 3) and a batch of
+    copy-on-write block copies.  Each is captured in a HIP graph and replayed
+    after a 1 GiB write that evicts the MALL and L2 ("cold")."""
 
+    from prism_infer.engine.kv_block_ops import copy_kv_blocks  # noqa: PLC0415
     from prism_infer.ops.kv_cache_store import store_kvcache  # noqa: PLC0415
     from prism_infer.ops.kv_compaction import compact_kv_slots  # noqa: PLC0415
     from prism_infer.ops.paged_decode import paged_decode_attention  # noqa: PLC0415
 
+    scratch = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    flush = lambda: scratch.fill_(1)
     out = {}
-    reps = 20
     # store: 8192 tokens into a 512-page pool
     sw = workloads.store_prefill(dev)
     kc = torch.empty(sw.num_pages, 256, 8, 128, dtype=torch.float8_e4m3fn, device=dev)
     vc = torch.empty_like(kc)
     ks = torch.empty(sw.num_pages, 256, 8, dtype=torch.float32, device=dev)
     vs = torch.empty_like(ks)
-    run = lambda i: store_kvcache(sw.key, sw.value, kc, vc, sw.slot_mapping, ks, vs)
-    run(0)
-    s = _time_loop(run, reps, torch)
+    s = _time_graph(lambda i: store_kvcache(sw.key, sw.value, kc, vc, sw.slot_mapping, ks, vs), 1, torch,
+                    flush=flush)
     out["store_prefill"] = {"us": round(s * 1e6, 2), "GBps": round(sw.algorithmic_bytes() / s / 1e9, 1),
-                            "bytes": sw.algorithmic_bytes()}
+                            "bytes": sw.algorithmic_bytes(), "timing": "graph replay, cold"}
     del kc, vc, ks, vs
     # compaction: 64 x 8192-token prefixes, ~30% dropped, out of place, payload + scales (L=1)
     cw = workloads.compaction_plans()
@@ -271,20 +304,37 @@ def _extras(torch, dev, workloads) -> dict:
         compact_kv_slots(payload, src, dst)
         compact_kv_slots(scales, src, dst)
 
-    compact(0)
-    s = _time_loop(compact, reps, torch)
+    s = _time_graph(compact, 1, torch, flush=flush)
     out["compaction_out_of_place"] = {"us": round(s * 1e6, 2), "GBps": round(cw.algorithmic_bytes() / s / 1e9, 1),
-                                      "bytes": cw.algorithmic_bytes(), "kept_tokens": cw.kept}
-    del payload, scales
-    # single-sequence decode (latency bound): Qwen3-VL-shaped, B=1, 1800 tokens
-    qw = workloads.decode_qwen_vl(dev)
-    run = lambda i: paged_decode_attention(qw.q, qw.k_cache, qw.v_cache, qw.block_tables, qw.context_lens, qw.scale,
-                                           k_scale_cache=qw.k_scale, v_scale_cache=qw.v_scale,
-                                           max_context_len=qw.max_context_len)
-    run(0)
-    s = _time_loop(run, 50, torch)
+                                      "bytes": cw.algorithmic_bytes(), "kept_tokens": cw.kept,
+                                      "timing": "graph replay, cold"}
+    del payload, scales, src, dst
+    # single-sequence decode (latency bound): Qwen3-VL-shaped, B=1, 1800 tokens, 36 layers with their own pools
+    layers = [workloads.decode_qwen_vl(dev, seed=20260803 + li) for li in range(36)]
+    s = _time_graph(lambda i: paged_decode_attention(
+        layers[i].q, layers[i].k_cache, layers[i].v_cache, layers[i].block_tables, layers[i].context_lens,
+        layers[i].scale, k_scale_cache=layers[i].k_scale, v_scale_cache=layers[i].v_scale,
+        max_context_len=layers[i].max_context_len), 36, torch, flush=flush)
     out["decode_qwen_vl_b1"] = {"us_per_layer": round(s * 1e6, 2),
-                                "GBps": round(qw.algorithmic_bytes() / s / 1e9, 1)}
+                                "GBps": round(layers[0].algorithmic_bytes() / s / 1e9, 1),
+                                "timing": "graph of 36 layers, replayed cold"}
+    del layers
+    # copy-on-write: 128 block pairs of a [2, 4, 1024, 256, 8, 128] cache, payload and scales
+    cache = torch.zeros(2, 4, 1024, 256, 8, 128, dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
+    scache = torch.zeros(2, 4, 1024, 256, 8, dtype=torch.float32, device=dev)
+    pairs = [(i, 512 + i) for i in range(128)]
+    nbytes = 2 * len(pairs) * 2 * 4 * 256 * 8 * (128 + 4)
+    copy_kv_blocks(cache, pairs, scache)  # the API once; the graph holds the device work it launches
+    bsrc = torch.tensor([p[0] for p in pairs], dtype=torch.long, device=dev)
+    bdst = torch.tensor([p[1] for p in pairs], dtype=torch.long, device=dev)
+
+    def cow(i):
+        compact_kv_slots(cache.view(2, 4, 1024, -1), bsrc, bdst)
+        compact_kv_slots(scache.view(2, 4, 1024, -1), bsrc, bdst)
+
+    s = _time_graph(cow, 1, torch, flush=flush)
+    out["copy_on_write_blocks"] = {"us": round(s * 1e6, 2), "GBps": round(nbytes / s / 1e9, 1), "bytes": nbytes,
+                                   "pairs": len(pairs), "layers": 4, "timing": "graph replay, cold"}
     return out
 
 

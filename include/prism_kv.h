@@ -175,6 +175,25 @@ int prism_compact_slots(void* cache, int64_t rows, int64_t num_slots, int64_t ve
                         int64_t workspace_bytes, void* stream);
 
 /*
+ * Whole-block moves between two caches of the same layout, either of which may
+ * be pinned host memory.  Replaces the per-block copies of
+ *   ModelRunner.swap_blocks(swap_map, direction)
+ *   (prism_infer/engine/model_runner.py:1001-1031).
+ *
+ * dst, src    : caches viewed as [rows][row_pitch bytes]; block i of a row is
+ *               the block_bytes bytes at i * block_bytes (a [kv, layers,
+ *               blocks, ...] cache has rows = kv * layers and row_pitch =
+ *               blocks * block_bytes).
+ * dst_ids, src_ids : HOST int64 [n] block ids, each in [0, dst_blocks) or
+ *               [0, src_blocks); entry i copies block src_ids[i] of every row
+ *               to block dst_ids[i] (one strided async DMA copy per entry, in
+ *               entry order).  Host memory must be pinned (page-locked).
+ */
+int prism_copy_blocks(void* dst, const void* src, int64_t rows, int64_t dst_row_pitch, int64_t src_row_pitch,
+                      int64_t block_bytes, int64_t dst_blocks, int64_t src_blocks, const int64_t* dst_ids,
+                      const int64_t* src_ids, int64_t n, void* stream);
+
+/*
  * Test hook with no counterpart in the reference: converts n fp32 values to
  * E4M3FN bytes with the exact device routine the scaled store uses (native
  * gfx950 conversion plus the NaN rule), so the rounding can be checked

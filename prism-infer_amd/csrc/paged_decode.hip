@@ -509,7 +509,7 @@ __global__ void __launch_bounds__(64) paged_decode_combine_kernel(const DecodeAr
 // * Three kernels: a one-workgroup plan kernel (prefix-sharing groups and the
 //   tile prefix sums, see "shared pages" below), the streaming kernel, and
 //   the merge of its partials.
-// * Two workgroups (8 waves each, wave = kv head) per CU.  The 16-token tiles
+// * One workgroup (8 waves, wave = kv head) per CU.  The 16-token tiles
 //   of the stream (virtual sequences over shared pages first, then every
 //   sequence's own tiles) are split into gridDim.x equal contiguous ranges, so
 //   every CU streams the same number of bytes whatever the context-length
@@ -519,9 +519,10 @@ __global__ void __launch_bounds__(64) paged_decode_combine_kernel(const DecodeAr
 //   uniquely.  The merge kernel combines them.
 // * A tile is one contiguous slab per tensor (K [16 tok][8 h][128 B], V
 //   likewise, and the fp32 scales).  The workgroup copies tiles straight into
-//   LDS with global_load_lds (16 B per lane), two stages per workgroup, so
-//   while one workgroup computes a tile the CU has up to three more (about
-//   100 KB) in flight and no VGPRs hold prefetched data.  16-byte chunks of a
+//   LDS with global_load_lds (16 B per lane), four stages, so while the
+//   workgroup computes a tile three more (about 100 KB) are in flight and no
+//   VGPRs hold prefetched data.  (Measured: two workgroups per CU with two
+//   stages each keep only two tiles in flight per CU and stream ~5% slower.)  16-byte chunks of a
 //   head row are XOR-swizzled by token so row-parallel K reads and transposed
 //   V reads spread over the banks.
 //   Scales are stored [head][token] so a lane's four tokens are one 16-byte read.
@@ -529,9 +530,9 @@ __global__ void __launch_bounds__(64) paged_decode_combine_kernel(const DecodeAr
 //   B = Q^T, 16 query columns: the G heads of one sequence, or of up to 16/G
 //   sequences for a virtual sequence).  Lane (g, c) gets the scores of query
 //   column c for tokens 4g..4g+3.
-// * PV: MFMA f32_16x16x16_bf16, whose four k slots per lane are exactly those
-//   four tokens, so P needs no data movement; P * v_scale is split into a
-//   bf16 hi/lo pair (two MFMAs) for fp32-like accuracy.  The V operand comes
+// * PV: MFMA f32_16x16x16_f16, whose four k slots per lane are exactly those
+//   four tokens, so P needs no data movement; P * v_scale goes in as f16
+//   (2^-11 relative; V bytes convert to f16 exactly), one MFMA per N-tile.  The V operand comes
 //   from ds_read_b64_tr_b8, which hands lane i of each 16-lane group byte i of
 //   eight 16-byte rows: rows 0-3 = tokens 4g..4g+3 at dims 16j.., rows 4-7 =
 //   the same tokens at dims 16(j+1).., i.e. two N-tiles per read.
@@ -540,8 +541,8 @@ __global__ void __launch_bounds__(64) paged_decode_combine_kernel(const DecodeAr
 
 constexpr int kSKv = 8;                                 // kv heads on this path
 constexpr int kSTile = 16;                              // tokens per tile
-constexpr int kSStages = 2;                             // pipeline depth per workgroup
-constexpr int kSWgPerCu = 2;                            // independent workgroups per CU
+constexpr int kSStages = 4;                             // pipeline depth per workgroup
+constexpr int kSWgPerCu = 1;                            // workgroups per CU
 constexpr int kSRow = kSKv * kHeadDim;                  // 1024 bytes per token row
 constexpr int kSKBytes = kSTile * kSRow;                // 16 KB of K per tile
 constexpr int kSScaleBytes = kSTile * kSKv * 4;         // 512 B of k scales per tile
@@ -550,6 +551,12 @@ constexpr int kSMaxBatch = 1024;
 constexpr int kSThreads = 64 * kSKv;
 constexpr int kSLoadsPerStage = 5;                      // per lane: 2 K, 2 V, 1 scale
 constexpr float kSRescaleThreshold = 8.0f;              // log2 domain
+// PV is one f16 MFMA per N-tile, with P * v_scale as f16 (2^-11 relative).
+// P <= 2^8 with the lazy rescaling, so P * v_scale fits f16 while every v
+// scale is <= kSF16MaxVScale; a tile with a larger one (|V| > 1.1e5) scales
+// P * v_scale by 2^-k and the accumulators by 2^-k before its MFMAs and by
+// 2^k after them, exact powers of two.
+constexpr float kSF16MaxVScale = 255.0f;
 
 __device__ __forceinline__ int stream_swz(int t) { return ((2 * t) + (t >> 2)) & 7; }
 
@@ -714,6 +721,16 @@ __device__ __forceinline__ void stream_load_q(const DecodeArgs& a, int qrow, int
 }
 
 typedef short shortx4 __attribute__((ext_vector_type(4)));
+
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+
+// 4 fp8 bytes (one dword) -> 4 f16, exact; assembled from whole dwords like
+// fp8x4_to_bf16x4_bits below.
+__device__ __forceinline__ f16x4 fp8x4_to_f16x4(uint32_t w) {
+  const u32x2 r = {__builtin_bit_cast(uint32_t, fp8x2_to_f16x2<false>(w)),
+                   __builtin_bit_cast(uint32_t, fp8x2_to_f16x2<true>(w))};
+  return __builtin_bit_cast(f16x4, r);
+}
 
 // 4 fp8 bytes (one dword) -> 4 bf16 bit patterns, exact.  Built from whole
 // dwords: extracting single bf16 lanes of the converted pairs (bit_cast of
@@ -1102,7 +1119,7 @@ __device__ __forceinline__ void stream_column(const DecodeArgs& a, int V, int i,
   qhead = h * G + (valid ? qh : 0);
 }
 
-// Two 8-wave workgroups per CU need 4 waves per SIMD: at most 128 VGPRs.
+// kSWgPerCu 8-wave workgroups per CU need 2 * kSWgPerCu waves per SIMD.
 template <int QDT, bool QVEC>
 __global__ void __launch_bounds__(kSThreads) __attribute__((amdgpu_waves_per_eu(2 * kSWgPerCu)))
 paged_decode_stream_kernel(const DecodeArgs a) {
@@ -1285,15 +1302,12 @@ paged_decode_stream_kernel(const DecodeArgs a) {
         }
       }
       const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
-      shortx4 pa, pa_lo;
+      float pv[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float p = exp2f(x[i] - m_use);  // 0 for masked slots
         l_run += p;
-        const float pv = ((valid >> i) & 1u) ? p * vs[i] : 0.f;
-        const __bf16 hi = static_cast<__bf16>(pv);
-        pa[i] = __builtin_bit_cast(short, hi);
-        pa_lo[i] = __builtin_bit_cast(short, static_cast<__bf16>(pv - static_cast<float>(hi)));
+        pv[i] = ((valid >> i) & 1u) ? p * vs[i] : 0.f;
       }
       // ---- PV: one transposed read feeds N-tiles 2jp and 2jp+1.  Bytes of
       // tokens past the end of the sequence are zeroed (rows there may hold
@@ -1301,14 +1315,32 @@ paged_decode_stream_kernel(const DecodeArgs a) {
       uint32_t keep = 0;
 #pragma unroll
       for (int i = 0; i < 4; ++i) keep |= ((valid >> i) & 1u) ? (0xFFu << (8 * i)) : 0u;
+      const bool big_v = fmaxf(fmaxf(vs[0], vs[1]), fmaxf(vs[2], vs[3])) > kSF16MaxVScale;
+      int vexp = 0;  // wave-uniform power-of-two shift of this tile's P * v_scale
+      if (__builtin_amdgcn_ballot_w64(big_v) != 0) {
+        float vmax = fmaxf(fmaxf(vs[0], vs[1]), fmaxf(vs[2], vs[3]));
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) vmax = fmaxf(vmax, __shfl_xor(vmax, off));
+        vexp = __builtin_amdgcn_readfirstlane(ilogbf(vmax / kSF16MaxVScale) + 1);
+        const float down = ldexpf(1.f, -vexp);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] *= down;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) pv[i] *= down;
+      }
+      const f16x4 pa = {static_cast<_Float16>(pv[0]), static_cast<_Float16>(pv[1]), static_cast<_Float16>(pv[2]),
+                        static_cast<_Float16>(pv[3])};
 #pragma unroll
       for (int jp = 0; jp < 4; ++jp) {
-        const shortx4 b0 = fp8x4_to_bf16x4_bits(static_cast<uint32_t>(vt[jp]) & keep);
-        const shortx4 b1 = fp8x4_to_bf16x4_bits(static_cast<uint32_t>(vt[jp] >> 32) & keep);
-        acc[2 * jp] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, b0, acc[2 * jp], 0, 0, 0);
-        acc[2 * jp + 1] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, b1, acc[2 * jp + 1], 0, 0, 0);
-        acc[2 * jp] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa_lo, b0, acc[2 * jp], 0, 0, 0);
-        acc[2 * jp + 1] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa_lo, b1, acc[2 * jp + 1], 0, 0, 0);
+        const f16x4 b0 = fp8x4_to_f16x4(static_cast<uint32_t>(vt[jp]) & keep);
+        const f16x4 b1 = fp8x4_to_f16x4(static_cast<uint32_t>(vt[jp] >> 32) & keep);
+        acc[2 * jp] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, b0, acc[2 * jp], 0, 0, 0);
+        acc[2 * jp + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, b1, acc[2 * jp + 1], 0, 0, 0);
+      }
+      if (vexp != 0) {
+        const float up = ldexpf(1.f, vexp);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j] *= up;
       }
     }
 

@@ -58,6 +58,7 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "prism_compact_slots_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64]),
     "prism_compact_slots": (_I, [_VP, _I64, _I64, _I64, _VP, _VP, _I64, _VP, _I64, _VP]),
+    "prism_copy_blocks": (_I, [_VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _I64P, _I64P, _I64, _VP]),
     "prism_debug_fp8_encode": (_I, [_VP, _VP, _I64, _VP]),
 }
 
