@@ -17,7 +17,7 @@ launched on.  ``cpu_baseline`` times the CPU restatement of the reference's
 decode path (per-sequence page gather, bf16 dequant, GQA expand, SDPA) on a
 bounded sample of the same workload's sequences.
 
-    python bench.py [--gpus 1] [--steps 50] [--warmup 10]
+    python bench.py [--gpus 1] [--steps 50] [--warmup 100]
 """
 
 from __future__ import annotations
@@ -57,30 +57,38 @@ def _time_loop(fn, steps: int, torch) -> float:
     return start.elapsed_time(end) / 1e3 / steps
 
 
-def _time_graph(fn, calls: int, torch, *, reps: int = 5, flush=None) -> float:
-    """Median seconds per call of ``fn`` with ``calls`` calls captured in one
-    HIP graph (GPU time, no host launch overhead), replayed ``reps`` times;
-    ``flush()`` runs before each replay, outside the timed region."""
+def _time_queued(fn, calls: int, torch, *, reps: int = 5, flush=None) -> float:
+    """Median GPU seconds per call of ``fn`` launched eagerly behind a GPU spin.
 
-    for i in range(calls):  # eager warm-up (allocations, plans)
+    Each repetition runs ``flush()``, then a spin kernel long enough for the
+    host to enqueue all ``calls`` calls before the start event is reached, so
+    the timed span is the calls' own GPU time back to back (no host launch
+    overhead and no graph-launch latency).  If the start event has already
+    completed when the host finishes enqueueing, the spin was too short: it
+    is doubled and the repetition is repeated."""
+
+    for i in range(calls):  # warm-up (allocations, plans)
         fn(i)
     torch.cuda.synchronize()
-    graph = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(graph):
-        for i in range(calls):
-            fn(i)
-    graph.replay()
-    torch.cuda.synchronize()
+    spin = 2_000_000 + calls * 200_000
     times = []
-    for _ in range(reps):
+    while len(times) < reps:
         if flush is not None:
             flush()
+        torch.cuda._sleep(spin)
         start = torch.cuda.Event(enable_timing=True)
         end = torch.cuda.Event(enable_timing=True)
         start.record()
-        graph.replay()
+        for i in range(calls):
+            fn(i)
         end.record()
+        late = start.query()
         torch.cuda.synchronize()
+        if late:
+            spin *= 2
+            if spin > 1 << 32:
+                raise RuntimeError("host cannot enqueue the timed calls ahead of the GPU")
+            continue
         times.append(start.elapsed_time(end) / 1e3 / calls)
     times.sort()
     return times[len(times) // 2]
@@ -131,7 +139,7 @@ def main() -> int:
     parser = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     parser.add_argument("--gpus", type=int, default=1)
     parser.add_argument("--steps", type=int, default=50)
-    parser.add_argument("--warmup", type=int, default=10)
+    parser.add_argument("--warmup", type=int, default=100)
     parser.add_argument("--layers", type=int, default=4, help="independent KV pools the steps rotate over")
     parser.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
     parser.add_argument("--no-cpu-baseline", action="store_true")
@@ -270,8 +278,9 @@ def main() -> int:
 def _extras(torch, dev, workloads) -> dict:
     """GPU time of the other configurations: store (config 2), compaction
     (config 5), B = 1 decode over 36 layers (config 3) and a batch of
-    copy-on-write block copies.  Each is captured in a HIP graph and replayed
-    after a 1 GiB write that evicts the MALL and L2 ("cold")."""
+    copy-on-write block copies.  Each runs after a 1 GiB write that evicts the
+    MALL and L2 ("cold"), queued behind a GPU spin so that only GPU time is
+    measured (``_time_queued``)."""
 
     from prism_infer.engine.kv_block_ops import copy_kv_blocks  # noqa: PLC0415
     from prism_infer.ops.kv_cache_store import store_kvcache  # noqa: PLC0415
@@ -287,10 +296,9 @@ def _extras(torch, dev, workloads) -> dict:
     vc = torch.empty_like(kc)
     ks = torch.empty(sw.num_pages, 256, 8, dtype=torch.float32, device=dev)
     vs = torch.empty_like(ks)
-    s = _time_graph(lambda i: store_kvcache(sw.key, sw.value, kc, vc, sw.slot_mapping, ks, vs), 1, torch,
-                    flush=flush)
+    s = _time_queued(lambda i: store_kvcache(sw.key, sw.value, kc, vc, sw.slot_mapping, ks, vs), 1, torch, flush=flush)
     out["store_prefill"] = {"us": round(s * 1e6, 2), "GBps": round(sw.algorithmic_bytes() / s / 1e9, 1),
-                            "bytes": sw.algorithmic_bytes(), "timing": "graph replay, cold"}
+                            "bytes": sw.algorithmic_bytes(), "timing": "queued behind a spin, cold"}
     del kc, vc, ks, vs
     # compaction: 64 x 8192-token prefixes, ~30% dropped, out of place, payload + scales (L=1)
     cw = workloads.compaction_plans()
@@ -304,27 +312,27 @@ def _extras(torch, dev, workloads) -> dict:
         compact_kv_slots(payload, src, dst)
         compact_kv_slots(scales, src, dst)
 
-    s = _time_graph(compact, 1, torch, flush=flush)
+    s = _time_queued(compact, 1, torch, flush=flush)
     out["compaction_out_of_place"] = {"us": round(s * 1e6, 2), "GBps": round(cw.algorithmic_bytes() / s / 1e9, 1),
                                       "bytes": cw.algorithmic_bytes(), "kept_tokens": cw.kept,
-                                      "timing": "graph replay, cold"}
+                                      "timing": "queued behind a spin, cold"}
     del payload, scales, src, dst
     # single-sequence decode (latency bound): Qwen3-VL-shaped, B=1, 1800 tokens, 36 layers with their own pools
     layers = [workloads.decode_qwen_vl(dev, seed=20260803 + li) for li in range(36)]
-    s = _time_graph(lambda i: paged_decode_attention(
+    s = _time_queued(lambda i: paged_decode_attention(
         layers[i].q, layers[i].k_cache, layers[i].v_cache, layers[i].block_tables, layers[i].context_lens,
         layers[i].scale, k_scale_cache=layers[i].k_scale, v_scale_cache=layers[i].v_scale,
         max_context_len=layers[i].max_context_len), 36, torch, flush=flush)
     out["decode_qwen_vl_b1"] = {"us_per_layer": round(s * 1e6, 2),
                                 "GBps": round(layers[0].algorithmic_bytes() / s / 1e9, 1),
-                                "timing": "graph of 36 layers, replayed cold"}
+                                "timing": "36 layers back to back, queued behind a spin, cold"}
     del layers
     # copy-on-write: 128 block pairs of a [2, 4, 1024, 256, 8, 128] cache, payload and scales
     cache = torch.zeros(2, 4, 1024, 256, 8, 128, dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
     scache = torch.zeros(2, 4, 1024, 256, 8, dtype=torch.float32, device=dev)
     pairs = [(i, 512 + i) for i in range(128)]
     nbytes = 2 * len(pairs) * 2 * 4 * 256 * 8 * (128 + 4)
-    copy_kv_blocks(cache, pairs, scache)  # the API once; the graph holds the device work it launches
+    copy_kv_blocks(cache, pairs, scache)  # the API once; the timed calls reuse its device index tensors
     bsrc = torch.tensor([p[0] for p in pairs], dtype=torch.long, device=dev)
     bdst = torch.tensor([p[1] for p in pairs], dtype=torch.long, device=dev)
 
@@ -332,9 +340,9 @@ def _extras(torch, dev, workloads) -> dict:
         compact_kv_slots(cache.view(2, 4, 1024, -1), bsrc, bdst)
         compact_kv_slots(scache.view(2, 4, 1024, -1), bsrc, bdst)
 
-    s = _time_graph(cow, 1, torch, flush=flush)
+    s = _time_queued(cow, 1, torch, flush=flush)
     out["copy_on_write_blocks"] = {"us": round(s * 1e6, 2), "GBps": round(nbytes / s / 1e9, 1), "bytes": nbytes,
-                                   "pairs": len(pairs), "layers": 4, "timing": "graph replay, cold"}
+                                   "pairs": len(pairs), "layers": 4, "timing": "queued behind a spin, cold"}
     return out
 
 

@@ -174,3 +174,54 @@ def test_dense_bf16_cache_store():
         if s >= 0:
             assert torch.equal(flat_k[s], key[t]) and torch.equal(flat_v[s], value[t])
     assert torch.all(flat_k[4] == 0)
+
+
+def _every_bf16_below(amax: float) -> torch.Tensor:
+    """All positive finite bf16 values <= amax (bf16 bit patterns 0x0001..)."""
+
+    bits = torch.arange(1, 0x7F80, dtype=torch.int32).to(torch.int16).view(torch.bfloat16)
+    vals = bits[bits.float() <= amax]
+    return vals
+
+
+@pytest.mark.parametrize("amax", [1.0, 3.0, 448.0, 0.0625, 1.7e-5, 2.9e-38, 5.3e11, 2.0 ** 120, 2.0 ** 125,
+                                  2.0 ** 126, 3.3e38])
+def test_scaled_store_every_bf16_quotient(amax):
+    """Each row holds ±amax and a run of bf16 values below it, so every bf16
+    quotient x / s of that scale (including the ones next to fp8 rounding
+    midpoints, subnormal results and scales near the fp32 range limit) goes
+    through the store and must match the oracle's IEEE division bit for bit."""
+
+    require_gpu()
+    amax_bf16 = torch.tensor(amax, dtype=torch.bfloat16)
+    vals = _every_bf16_below(amax_bf16.item())
+    heads, dim = 8, 128
+    per_row = dim - 1
+    rows = -(-vals.numel() // per_row)
+    rows = -(-rows // (2 * heads)) * 2 * heads  # whole tokens, K and V rows
+    body = vals.repeat(-(-rows * per_row // vals.numel()))[:rows * per_row].view(rows, per_row)
+    sign = torch.where(torch.arange(rows) % 3 == 0, -1.0, 1.0).to(torch.bfloat16)[:, None]
+    full = torch.cat([amax_bf16.expand(rows, 1), body * sign], dim=1)
+    tokens = rows // (2 * heads)
+    kv = full.view(tokens, 2, heads, dim)
+    key, value = kv[:, 0].contiguous(), kv[:, 1].contiguous()
+    num_pages = -(-tokens // 256) + 1
+    gen = torch.Generator().manual_seed(20260801)
+    slots = torch.randperm(num_pages * 256, generator=gen)[:tokens].to(torch.int32)
+    got, want = _run_store(key, value, (num_pages, 256, heads, dim), slots)
+    _assert_bit_exact(got, want, f"every bf16 below amax={amax}")
+
+
+def test_scaled_store_large_fp32_sample_bit_exact():
+    """16.7M fp32 elements with per-row scales spread over 2^-30..2^30: near-
+    midpoint quotients, which take the exact-division branch, occur a few
+    hundred times, and every byte and scale must match the oracle."""
+
+    require_gpu()
+    gen = torch.Generator().manual_seed(20260802)
+    tokens, heads, dim = 4096, 8, 128
+    key = torch.randn(tokens, heads, dim, generator=gen) * torch.exp2(torch.randint(-30, 31, (tokens, heads, 1), generator=gen).float())
+    value = torch.rand(tokens, heads, dim, generator=gen) * 1000.0 - 500.0
+    slots = torch.randperm(20 * 256, generator=gen)[:tokens].to(torch.int32)
+    got, want = _run_store(key, value, (20, 256, heads, dim), slots)
+    _assert_bit_exact(got, want, "fp32 sample")
