@@ -36,6 +36,7 @@ for _p in (REPO_ROOT, REPO_ROOT / "prism-infer_amd"):
 
 METRIC = "paged-decode achieved HBM GB/s (% of peak) + µs/layer, batch 64 mixed ctx"
 HBM_PEAK_GBPS = 8000.0
+MFMA_BF16_PEAK = 2.5e15  # dense bf16/fp16 MFMA, FLOP/s
 TRAFFIC_FILE = REPO_ROOT / "profiles" / "decode_mixed_traffic.json"
 
 
@@ -327,6 +328,21 @@ def _extras(torch, dev, workloads) -> dict:
                                 "GBps": round(layers[0].algorithmic_bytes() / s / 1e9, 1),
                                 "timing": "36 layers back to back, queued behind a spin, cold"}
     del layers
+    # paged prefill: 4 sequences x (8192 cached + 2048 new tokens), causal
+    from types import SimpleNamespace  # noqa: PLC0415
+
+    from prism_infer.ops.paged_prefill import _launch_paged_prefill  # noqa: PLC0415
+
+    pw = workloads.prefill_chunked(dev)
+    pctx = SimpleNamespace(block_tables=pw.block_tables, context_lens=pw.context_lens, cu_seqlens_q=pw.cu_seqlens_q)
+    s = _time_queued(lambda i: _launch_paged_prefill(
+        pw.q, pw.k_cache, pw.v_cache, pctx, num_heads=pw.num_heads, num_kv_heads=pw.num_kv_heads, scale=pw.scale,
+        k_scale_cache=pw.k_scale, v_scale_cache=pw.v_scale), 1, torch, flush=flush)
+    out["prefill_chunked"] = {"us": round(s * 1e6, 2), "TFLOPs": round(pw.flops() / s / 1e12, 1),
+                              "mfma_frac": round(pw.flops() / s / MFMA_BF16_PEAK, 4), "flops": pw.flops(),
+                              "GBps": round(pw.algorithmic_bytes() / s / 1e9, 1),
+                              "timing": "queued behind a spin, cold (status fill + kernel; the host check is not timed)"}
+    del pw
     # copy-on-write: 128 block pairs of a [2, 4, 1024, 256, 8, 128] cache, payload and scales
     cache = torch.zeros(2, 4, 1024, 256, 8, 128, dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
     scache = torch.zeros(2, 4, 1024, 256, 8, dtype=torch.float32, device=dev)

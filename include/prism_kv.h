@@ -194,6 +194,45 @@ int prism_copy_blocks(void* dst, const void* src, int64_t rows, int64_t dst_row_
                       const int64_t* src_ids, int64_t n, void* stream);
 
 /*
+ * Paged prefill attention (chunked / prefix-hit prefill) over paged FP8
+ * K/V.  Replaces
+ *   paged_prefill_attention_reference(q, k_cache, v_cache, context, *,
+ *       num_heads, num_kv_heads, scale, k_scale_cache=None, v_scale_cache=None)
+ *   (prism_infer/ops/paged_attention_reference.py:185-246).
+ *
+ * q          : [total_q, num_heads, head_dim] of q_dtype (BF16/F16), strides
+ *              q_strides {token, head, dim}; dim stride 1, rows 16-byte aligned.
+ *              Sequence i owns rows [cu_seqlens_q[i], cu_seqlens_q[i + 1]).
+ * k/v_cache  : [num_blocks, page_size, num_kv_heads, head_dim] FP8_E4M3FN,
+ *              strides k_strides / v_strides {block, token, head, dim}; dim
+ *              stride 1.  head_dim 128; page_size a multiple of 16; GQA group
+ *              num_heads / num_kv_heads of 1, 2, 4 or 8.
+ * k/v_scale  : [num_blocks, page_size, num_kv_heads] fp32 or both NULL (unit
+ *              scale); strides ks_strides / vs_strides.
+ * block_tables, context_lens, cu_seqlens_q : int32 device arrays ([>= batch,
+ *              width], [>= batch], [>= batch + 1]).  context_lens[i] counts the
+ *              sequence's whole history including its query tokens, which are
+ *              already stored in the cache; query token j of sequence i sits
+ *              at position context_lens[i] - query_len_i + j and attends to
+ *              keys 0 .. that position.
+ * out        : [total_q, num_heads, head_dim] of q_dtype, strides out_strides.
+ * status     : device int32[1], set by the caller to INT32_MAX.  A sequence
+ *              whose lengths are invalid (query_len <= 0, context_len <
+ *              query_len, context_len > width * page_size) or whose needed
+ *              block ids are negative or >= num_blocks records its index
+ *              there (atomic min); its output rows are unspecified.
+ */
+int prism_paged_prefill(const void* q, int q_dtype, const int64_t q_strides[3], const void* k_cache,
+                        const void* v_cache, int cache_dtype, const int64_t k_strides[4],
+                        const int64_t v_strides[4], const float* k_scale, const float* v_scale,
+                        const int64_t ks_strides[3], const int64_t vs_strides[3],
+                        const int32_t* block_tables, const int64_t bt_strides[2],
+                        const int32_t* context_lens, const int32_t* cu_seqlens_q, void* out,
+                        const int64_t out_strides[3], int batch, int total_q, int num_heads,
+                        int num_kv_heads, int head_dim, int page_size, int num_blocks, int width,
+                        float scale, int32_t* status, void* stream);
+
+/*
  * Test hook with no counterpart in the reference: converts n fp32 values to
  * E4M3FN bytes with the exact device routine the scaled store uses (native
  * gfx950 conversion plus the NaN rule), so the rounding can be checked

@@ -42,6 +42,9 @@ __all__ = [
     "decode_bruteforce_f64",
     "dequantize",
     "decode_token_mask",
+    "prefill_reference_qdtype",
+    "prefill_reference_fp32",
+    "prefill_bruteforce_f64",
 ]
 
 
@@ -389,6 +392,108 @@ def decode_bruteforce_f64(q, keys, values, scale) -> torch.Tensor:
         total = sum(weights)
         for d in range(head_dim):
             out[h, d] = sum(w * float(values[t, kh, d]) for t, w in enumerate(weights)) / total
+    return out
+
+
+# --------------------------------------------------------------------------- prefill
+
+
+def _prefill_lengths(cu_seqlens_q, context_lens, i: int) -> tuple[int, int, int]:
+    query_start = int(cu_seqlens_q[i])
+    query_len = int(cu_seqlens_q[i + 1]) - query_start
+    context_len = int(context_lens[i])
+    if query_len <= 0 or context_len < query_len:
+        raise RuntimeError(f"invalid paged prefill lengths: query={query_len} context={context_len}")
+    return query_start, query_len, context_len
+
+
+def prefill_reference_qdtype(q, k_cache, v_cache, block_tables, context_lens, cu_seqlens_q, *, num_heads,
+                             num_kv_heads, scale, k_scale_cache=None, v_scale_cache=None) -> torch.Tensor:
+    """``paged_prefill_attention_reference`` (ops/paged_attention_reference.py:185-246).
+
+    Per sequence i: query rows ``cu[i]:cu[i+1]``; ``prefix = context_len -
+    query_len``; gather the pages up to ``context_len`` (:22-63), dequantize
+    in ``q.dtype`` (:102-122), expand GQA (:125-145), and run SDPA with the
+    causal mask ``key_pos <= prefix + j`` (:228-240).  Outputs are
+    concatenated in sequence order.
+    """
+
+    outputs = []
+    groups = num_heads // num_kv_heads
+    for i in range(context_lens.numel()):
+        start, query_len, context_len = _prefill_lengths(cu_seqlens_q, context_lens, i)
+        prefix = context_len - query_len
+        keys = _gather_sequence(k_cache, block_tables[i], context_len)
+        values = _gather_sequence(v_cache, block_tables[i], context_len)
+        ks = vs = None
+        if k_scale_cache is not None:
+            ks = _gather_sequence(k_scale_cache, block_tables[i], context_len)
+            vs = _gather_sequence(v_scale_cache, block_tables[i], context_len)
+        keys = dequantize(keys, ks, q.dtype)
+        values = dequantize(values, vs, q.dtype)
+        if groups != 1:
+            keys = keys.repeat_interleave(groups, dim=1)
+            values = values.repeat_interleave(groups, dim=1)
+        queries = q[start:start + query_len].transpose(0, 1).unsqueeze(0)
+        mask = (torch.arange(context_len).unsqueeze(0) <= torch.arange(prefix, context_len).unsqueeze(1))
+        output = F.scaled_dot_product_attention(
+            queries, keys.transpose(0, 1).unsqueeze(0), values.transpose(0, 1).unsqueeze(0),
+            attn_mask=mask.unsqueeze(0).unsqueeze(0), is_causal=False, scale=scale,
+        )
+        outputs.append(output.squeeze(0).transpose(0, 1))
+    return torch.cat(outputs, dim=0)
+
+
+def prefill_reference_fp32(q, k_cache, v_cache, block_tables, context_lens, cu_seqlens_q, *, num_heads,
+                           num_kv_heads, scale, k_scale_cache=None, v_scale_cache=None,
+                           compute_dtype=torch.float64) -> torch.Tensor:
+    """The same attention with fp32 dequantization (``fp8 -> fp32 * scale``, as
+    the reference's decode test oracle dequantizes, tests/test_scaled_fp8_kv_cache.py:71-102)
+    and the softmax evaluated in ``compute_dtype`` (float64 by default): the
+    exact causal attention of the dequantized cache.  Result in ``q.dtype``.
+    """
+
+    outputs = []
+    groups = num_heads // num_kv_heads
+    for i in range(context_lens.numel()):
+        start, query_len, context_len = _prefill_lengths(cu_seqlens_q, context_lens, i)
+        prefix = context_len - query_len
+        keys = _gather_sequence(k_cache, block_tables[i], context_len).to(torch.float32)
+        values = _gather_sequence(v_cache, block_tables[i], context_len).to(torch.float32)
+        if k_scale_cache is not None:
+            keys = keys * _gather_sequence(k_scale_cache, block_tables[i], context_len).float().unsqueeze(-1)
+            values = values * _gather_sequence(v_scale_cache, block_tables[i], context_len).float().unsqueeze(-1)
+        keys = keys.to(compute_dtype).repeat_interleave(groups, dim=1)        # [ctx, Hq, D]
+        values = values.to(compute_dtype).repeat_interleave(groups, dim=1)
+        queries = q[start:start + query_len].to(compute_dtype)               # [n, Hq, D]
+        scores = torch.einsum("nhd,khd->hnk", queries, keys) * scale
+        visible = torch.arange(context_len).unsqueeze(0) <= torch.arange(prefix, context_len).unsqueeze(1)
+        scores = scores.masked_fill(~visible.unsqueeze(0), float("-inf"))
+        probs = torch.softmax(scores, dim=-1)
+        outputs.append(torch.einsum("hnk,khd->nhd", probs, values))
+    return torch.cat(outputs, dim=0).to(q.dtype)
+
+
+def prefill_bruteforce_f64(queries, keys, values, prefix: int, scale: float) -> torch.Tensor:
+    """Causal attention of ONE sequence in float64 with explicit loops.
+
+    ``queries``: [n, Hq, D]; ``keys``/``values``: [prefix + n, Hkv, D] already
+    dequantized; query j attends to keys ``0 .. prefix + j``.
+    """
+
+    n, num_heads, head_dim = queries.shape
+    groups = num_heads // keys.shape[1]
+    out = torch.zeros(n, num_heads, head_dim, dtype=torch.float64)
+    for j in range(n):
+        for h in range(num_heads):
+            kh = h // groups
+            logits = [sum(float(queries[j, h, d]) * float(keys[t, kh, d]) for d in range(head_dim)) * scale
+                      for t in range(prefix + j + 1)]
+            m = max(logits)
+            weights = [math.exp(x - m) for x in logits]
+            total = sum(weights)
+            for d in range(head_dim):
+                out[j, h, d] = sum(w * float(values[t, kh, d]) for t, w in enumerate(weights)) / total
     return out
 
 

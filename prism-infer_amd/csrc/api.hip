@@ -48,7 +48,7 @@ __global__ void __launch_bounds__(256) fp8_encode_kernel(const float* __restrict
 
 extern "C" {
 
-int prism_abi_version(void) { return 1; }
+int prism_abi_version(void) { return 2; }
 
 const char* prism_last_error(void) { return prism::g_last_error.c_str(); }
 

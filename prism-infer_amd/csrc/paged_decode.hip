@@ -28,6 +28,7 @@
 // Generic path (any other supported shape): one wave per (sequence, q head),
 //   lane-per-token scores, lane-per-dim accumulation, no split-K.
 #include "common.h"
+#include "fp8_mfma.h"
 
 namespace prism {
 namespace {
@@ -99,34 +100,6 @@ __device__ __forceinline__ void store_out(void* out, int64_t idx, float v) {
   else static_cast<uint16_t*>(out)[idx] = f32_to_f16_bits(v);
 }
 
-// Two fp8 bytes (the selected 16-bit half of `w`) -> bf16x2, exact.
-template <bool HI>
-__device__ __forceinline__ bf16x2 fp8x2_to_bf16x2(uint32_t w) {
-  return __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(w, 1.0f, HI);
-}
-
-template <bool HI>
-__device__ __forceinline__ f16x2 fp8x2_to_f16x2(uint32_t w) {
-  return __builtin_amdgcn_cvt_scalef32_pk_f16_fp8(w, 1.0f, HI);
-}
-
-// 8 fp8 bytes (two dwords) -> 8 bf16 in order.  Assembled from whole dwords
-// (see fp8x4_to_bf16x4_bits for why lanes are not extracted one by one).
-__device__ __forceinline__ bf16x8 fp8x8_to_bf16x8(uint32_t w0, uint32_t w1) {
-  const u32x4 r = {__builtin_bit_cast(uint32_t, fp8x2_to_bf16x2<false>(w0)),
-                   __builtin_bit_cast(uint32_t, fp8x2_to_bf16x2<true>(w0)),
-                   __builtin_bit_cast(uint32_t, fp8x2_to_bf16x2<false>(w1)),
-                   __builtin_bit_cast(uint32_t, fp8x2_to_bf16x2<true>(w1))};
-  return __builtin_bit_cast(bf16x8, r);
-}
-
-__device__ __forceinline__ f16x8 fp8x8_to_f16x8(uint32_t w0, uint32_t w1) {
-  const u32x4 r = {__builtin_bit_cast(uint32_t, fp8x2_to_f16x2<false>(w0)),
-                   __builtin_bit_cast(uint32_t, fp8x2_to_f16x2<true>(w0)),
-                   __builtin_bit_cast(uint32_t, fp8x2_to_f16x2<false>(w1)),
-                   __builtin_bit_cast(uint32_t, fp8x2_to_f16x2<true>(w1))};
-  return __builtin_bit_cast(f16x8, r);
-}
 
 struct TileRegs {
   u32x4 k[2][2];   // [half][part]: 32 bytes of K row (c + 16 * half), dims 32g..32g+31
@@ -560,37 +533,8 @@ constexpr float kSF16MaxVScale = 255.0f;
 
 __device__ __forceinline__ int stream_swz(int t) { return ((2 * t) + (t >> 2)) & 7; }
 
-typedef __attribute__((address_space(3))) void lds_void;
-
-__device__ __forceinline__ uint32_t lds_addr(const void* p) {
-  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>((const lds_void*)p));
-}
-
-// Four ds_read_b64_tr_b8 issued back to back with one lgkmcnt wait.  Written
-// as asm because the compiler's waitcnt pass cannot tell this LDS read from
-// the in-flight load-to-LDS of other stages and would drain the whole
-// prefetch (vmcnt(0)) before it.
-__device__ __forceinline__ void lds_read_tr8_x4(const uint32_t (&ad)[4], uint64_t (&out)[4]) {
-  asm volatile(
-      "ds_read_b64_tr_b8 %0, %4\n\t"
-      "ds_read_b64_tr_b8 %1, %5\n\t"
-      "ds_read_b64_tr_b8 %2, %6\n\t"
-      "ds_read_b64_tr_b8 %3, %7\n\t"
-      "s_waitcnt lgkmcnt(0)"
-      : "=&v"(out[0]), "=&v"(out[1]), "=&v"(out[2]), "=&v"(out[3])
-      : "v"(ad[0]), "v"(ad[1]), "v"(ad[2]), "v"(ad[3])
-      : "memory");
-}
 
 
-// Max over the four 16-lane groups (lanes l, l^16, l^32, l^48) with the
-// gfx950 lane-swap instructions (VALU, no LDS round trip).
-__device__ __forceinline__ float wave_max_across_groups(float v) {
-  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  v = fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
-  const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
-}
 
 // Global tile index -> sequence, by walking the prefix sums.
 __device__ __forceinline__ void advance_seq(const int* tstart, int batch, int64_t tile, int& b) {
@@ -720,27 +664,7 @@ __device__ __forceinline__ void stream_load_q(const DecodeArgs& a, int qrow, int
   }
 }
 
-typedef short shortx4 __attribute__((ext_vector_type(4)));
 
-typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
-
-// 4 fp8 bytes (one dword) -> 4 f16, exact; assembled from whole dwords like
-// fp8x4_to_bf16x4_bits below.
-__device__ __forceinline__ f16x4 fp8x4_to_f16x4(uint32_t w) {
-  const u32x2 r = {__builtin_bit_cast(uint32_t, fp8x2_to_f16x2<false>(w)),
-                   __builtin_bit_cast(uint32_t, fp8x2_to_f16x2<true>(w))};
-  return __builtin_bit_cast(f16x4, r);
-}
-
-// 4 fp8 bytes (one dword) -> 4 bf16 bit patterns, exact.  Built from whole
-// dwords: extracting single bf16 lanes of the converted pairs (bit_cast of
-// element [1] to short) was lowered by this compiler (ROCm 7.2 clang) to a
-// v_perm that duplicates element [0].
-__device__ __forceinline__ shortx4 fp8x4_to_bf16x4_bits(uint32_t w) {
-  const u32x2 r = {__builtin_bit_cast(uint32_t, fp8x2_to_bf16x2<false>(w)),
-                   __builtin_bit_cast(uint32_t, fp8x2_to_bf16x2<true>(w))};
-  return __builtin_bit_cast(shortx4, r);
-}
 
 // ------------------------------------------------------------ shared pages
 //

@@ -1,0 +1,531 @@
+// Paged prefill attention over scaled-FP8 pages (chunked / prefix-hit
+// prefill): for every sequence i, query token j of its chunk sits at
+// position prefix_i + j (prefix_i = context_len_i - query_len_i) and attends
+// to keys 0..prefix_i + j of its paged history, which already holds the
+// chunk's own K/V.  Restates prism_infer/ops/paged_attention_reference.py:
+// 185-246 (gather :22-63, dequantisation :102-122, GQA :125-145): causal
+// SDPA over the dequantised pages, output in q's dtype.  Dequantisation here
+// is fp32 (payload * scale applied to the fp32 scores and to P), as the
+// decode kernels do; the reference multiplies in q's dtype.
+//
+// Work layout.  A workgroup owns one kv head and one block of 32 query
+// tokens of one sequence; its G waves are the G query heads of the kv head,
+// so each K/V tile is read once into LDS for all of them.  Tiles of KT keys
+// (one page holds whole tiles) are double buffered through LDS: the next
+// tile's loads are in flight while the current one is computed.  Per
+// 16-key sub-block, a wave computes S^T = K Q^T with
+// v_mfma_f32_16x16x32_{bf16,f16} (fp8 -> bf16/f16 is exact; the key scale
+// multiplies the rows of S^T), runs the online softmax per query column
+// (log2 domain, lazy rescaling), and accumulates O^T += V^T P^T with
+// v_mfma_f32_16x16x16_f16, V^T coming from ds_read_b64_tr_b8 and P * v_scale
+// entering as f16 (a tile whose v scales exceed 255 is shifted by a power of
+// two, exactly).  Only tiles on the diagonal apply the causal mask.
+//
+// Metadata stays on the device: each workgroup finds its sequence and query
+// block from cu_seqlens_q with a wave scan.  Invalid lengths or block ids
+// record the lowest offending sequence in status[0] (atomicMin); the host
+// raises the reference's error for it.
+#include "common.h"
+#include "fp8_mfma.h"
+
+namespace prism {
+namespace {
+
+constexpr int kPfD = 128;                      // head dim
+constexpr int kPfCols = 16;                    // query tokens per MFMA column block
+constexpr int kPfColBlocks = 2;                // column blocks per wave
+constexpr int kPfQTile = kPfCols * kPfColBlocks;  // query tokens per workgroup
+constexpr int kPfMaxWaves = 8;                 // GQA group size limit
+constexpr float kPfRescaleThreshold = 8.0f;    // log2 units
+constexpr float kPfF16MaxVScale = 255.0f;      // P <= 2^8, so P * v_scale < 65504
+
+struct PrefillArgs {
+  const void* q;
+  int64_t q_st, q_sh;  // elements (dim stride 1)
+  const uint8_t* k;
+  const uint8_t* v;
+  int64_t k_sn, k_sp, k_sh, v_sn, v_sp, v_sh;  // bytes (dim stride 1)
+  const float* ks;
+  const float* vs;
+  int64_t ks_sn, ks_sp, ks_sh, vs_sn, vs_sp, vs_sh;  // elements
+  const int32_t* bt;
+  int64_t bt_sb, bt_sn;
+  const int32_t* ctx;
+  const int32_t* cu_q;
+  void* out;
+  int64_t o_st, o_sh;
+  int batch, num_heads, groups, page, num_blocks, width;
+  float scale_log2;
+  int* status;
+};
+
+// 16-byte chunk swizzle of a key row in LDS, by the key's index inside its
+// 16-key sub-block (spreads the column reads of a sub-block over the banks).
+__device__ __forceinline__ int pf_swz(int t) { return ((2 * t) + ((t & 15) >> 2)) & 7; }
+
+__device__ __forceinline__ void flag_sequence(const PrefillArgs& a, int seq) {
+  atomicMin(a.status, seq);
+}
+
+// Inclusive wave scan of v (64 lanes).
+__device__ __forceinline__ int wave_scan(int v) {
+  const int lane = __lane_id();
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int u = __shfl_up(v, off);
+    if (lane >= off) v += u;
+  }
+  return v;
+}
+
+// Query blocks of sequence i (0 for a sequence with invalid lengths, which
+// is flagged).
+__device__ __forceinline__ int seq_blocks(const PrefillArgs& a, int i, bool flag) {
+  const int q0 = a.cu_q[i];
+  const int qlen = a.cu_q[i + 1] - q0;
+  const int ctx = a.ctx[i];
+  if (qlen <= 0 || ctx < qlen || ctx > a.width * a.page) {
+    if (flag) flag_sequence(a, i);
+    return 0;
+  }
+  return (qlen + kPfQTile - 1) / kPfQTile;
+}
+
+// Workgroup -> (sequence, query block).  Blocks are numbered in reverse so
+// that the last (longest) query blocks start first.  Returns false for a
+// workgroup beyond the real blocks.
+__device__ bool locate(const PrefillArgs& a, int& seq, int& qblock) {
+  const int lane = __lane_id();
+  int total = 0;
+  for (int base = 0; base < a.batch; base += 64) {
+    const int i = base + lane;
+    const int n = i < a.batch ? seq_blocks(a, i, blockIdx.y == 0 && blockIdx.x == 0 && threadIdx.x < 64) : 0;
+    total += __shfl(wave_scan(n), 63);
+  }
+  const int target = total - 1 - static_cast<int>(blockIdx.x);
+  if (target < 0) return false;
+  int before = 0;
+  for (int base = 0; base < a.batch; base += 64) {
+    const int i = base + lane;
+    const int n = i < a.batch ? seq_blocks(a, i, false) : 0;
+    const int incl = wave_scan(n) + before;
+    const uint64_t hit = __builtin_amdgcn_ballot_w64(i < a.batch && target < incl && target >= incl - n);
+    if (hit != 0) {
+      const int l = __builtin_ctzll(hit);
+      seq = __builtin_amdgcn_readfirstlane(base + l);
+      qblock = __builtin_amdgcn_readfirstlane(target - (__shfl(incl, l) - __shfl(n, l)));
+      return true;
+    }
+    before = __shfl(incl, 63);
+  }
+  return false;
+}
+
+template <int QDT>
+struct PfQOperand {
+  using T = typename std::conditional<QDT == PRISM_DTYPE_F16, f16x8, bf16x8>::type;
+  T op[4];
+};
+
+// Two waves per SIMD: at most 256 VGPRs + AGPRs per lane.
+template <int QDT, int KT, int NW, bool SCALED>
+__global__ void __launch_bounds__(64 * NW) __attribute__((amdgpu_waves_per_eu(2)))
+paged_prefill_kernel(const PrefillArgs a) {
+  constexpr int kRow = kPfD;                  // one key's payload row in LDS (bytes)
+  constexpr int kPayload = KT * kRow;         // K or V payload of a tile
+  constexpr int kStage = 2 * kPayload + 2 * KT * 4;
+  constexpr int kChunks = 2 * KT * (kRow / 16);  // 16-byte payload chunks per tile (K then V)
+  __shared__ __attribute__((aligned(16))) uint8_t stages[2 * kStage];
+
+  int seq, qblock;
+  if (!locate(a, seq, qblock)) return;
+  const int h = blockIdx.y;
+  constexpr int nthreads = 64 * NW;
+  const int tid = threadIdx.x;
+  const int wave = tid / 64;
+  const int lane = tid % 64;
+  const int c = lane % 16;
+  const int g = lane / 16;
+  const int qhead = h * a.groups + wave;
+
+  const int qs = a.cu_q[seq];
+  const int qlen = a.cu_q[seq + 1] - qs;
+  const int ctx = a.ctx[seq];
+  const int prefix = ctx - qlen;
+  const int qb0 = qblock * kPfQTile;                       // first query token of the block
+  const int qcount = min(kPfQTile, qlen - qb0);
+  const int kend = prefix + qb0 + qcount;                  // keys [0, kend) are needed
+  const int ntiles = (kend + KT - 1) / KT;
+  const int32_t* bt_row = a.bt + static_cast<int64_t>(seq) * a.bt_sb;
+
+  // ---- query operand (B of S^T = K Q^T): column c of block cb is query
+  // token qb0 + 16 cb + c; lane group g holds dims 32g .. 32g + 31.
+  PfQOperand<QDT> qop[kPfColBlocks];
+  bool colv[kPfColBlocks];
+#pragma unroll
+  for (int cb = 0; cb < kPfColBlocks; ++cb) {
+    const int j = qb0 + cb * kPfCols + c;
+    colv[cb] = j < qlen;
+    const uint16_t* src = static_cast<const uint16_t*>(a.q) + static_cast<int64_t>(qs + (colv[cb] ? j : 0)) * a.q_st +
+                          static_cast<int64_t>(qhead) * a.q_sh + 32 * g;
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+      u32x4 w = colv[cb] ? *reinterpret_cast<const u32x4*>(src + 8 * cc) : u32x4{0u, 0u, 0u, 0u};
+      qop[cb].op[cc] = __builtin_bit_cast(typename PfQOperand<QDT>::T, w);
+    }
+  }
+
+  // ---- tile loads: thread chunk ids tid, tid + nthreads, ... of kChunks;
+  // scales by threads < 2 * KT (one float each)
+  constexpr int kMaxPer = (kChunks + nthreads - 1) / nthreads;  // chunks per thread
+  u32x4 pre[kMaxPer];
+  float pre_s = 0.f;
+  bool tile_ok = true;
+  auto load_tile = [&](int t) {
+    const int tok0 = t * KT;
+    const int page = tok0 / a.page;
+    const int32_t blk = bt_row[static_cast<int64_t>(page) * a.bt_sn];
+    tile_ok = blk >= 0 && blk < a.num_blocks;
+    if (!tile_ok) {
+      if (tid == 0) flag_sequence(a, seq);
+      return;
+    }
+    const int row0 = tok0 - page * a.page;
+#pragma unroll
+    for (int k = 0; k < kMaxPer; ++k) {
+      const int ch = tid + k * nthreads;
+      if (ch < kChunks) {
+        const int isv = ch >= kChunks / 2;
+        const int cw = ch - isv * (kChunks / 2);
+        const int tok = cw / (kRow / 16);
+        const int part = cw % (kRow / 16);
+        const uint8_t* base = isv ? a.v + blk * a.v_sn + static_cast<int64_t>(row0 + tok) * a.v_sp + h * a.v_sh
+                                  : a.k + blk * a.k_sn + static_cast<int64_t>(row0 + tok) * a.k_sp + h * a.k_sh;
+        pre[k] = *reinterpret_cast<const u32x4*>(base + part * 16);
+      }
+    }
+    if constexpr (SCALED) {
+      if (tid < 2 * KT) {
+        const int isv = tid >= KT;
+        const int tok = tid - isv * KT;
+        pre_s = isv ? a.vs[blk * a.vs_sn + static_cast<int64_t>(row0 + tok) * a.vs_sp + h * a.vs_sh]
+                    : a.ks[blk * a.ks_sn + static_cast<int64_t>(row0 + tok) * a.ks_sp + h * a.ks_sh];
+      }
+    } else {
+      pre_s = 1.f;
+    }
+  };
+  auto store_tile = [&](uint8_t* st) {
+    if (!tile_ok) return;
+#pragma unroll
+    for (int k = 0; k < kMaxPer; ++k) {
+      const int ch = tid + k * nthreads;
+      if (ch < kChunks) {
+        const int isv = ch >= kChunks / 2;
+        const int cw = ch - isv * (kChunks / 2);
+        const int tok = cw / (kRow / 16);
+        const int part = cw % (kRow / 16);
+        *reinterpret_cast<u32x4*>(st + isv * kPayload + tok * kRow + ((part ^ pf_swz(tok)) << 4)) = pre[k];
+      }
+    }
+    if (tid < 2 * KT) reinterpret_cast<float*>(st + 2 * kPayload)[tid] = pre_s;
+  };
+
+  floatx4 acc[kPfColBlocks][8];
+  float m_run[kPfColBlocks], l_run[kPfColBlocks];
+#pragma unroll
+  for (int cb = 0; cb < kPfColBlocks; ++cb) {
+#pragma unroll
+    for (int j = 0; j < 8; ++j) acc[cb][j] = floatx4{0.f, 0.f, 0.f, 0.f};
+    m_run[cb] = -INFINITY;
+    l_run[cb] = 0.f;
+  }
+
+  // per-lane LDS offsets inside a stage for sub-block 0 (add 16 rows per sub-block)
+  const uint32_t k_off0 = c * kRow + (((2 * g) ^ pf_swz(c)) << 4);
+  const uint32_t k_off1 = c * kRow + (((2 * g + 1) ^ pf_swz(c)) << 4);
+  uint32_t v_off[4];
+  {
+    const int r = c >> 1;
+    const int t = 4 * g + (r & 3);
+    const int half = c & 1;
+#pragma unroll
+    for (int jp = 0; jp < 4; ++jp) {
+      const int chunk = 2 * jp + (r >> 2);
+      v_off[jp] = kPayload + t * kRow + ((chunk ^ pf_swz(t)) << 4) + half * 8;
+    }
+  }
+  const uint32_t stage_base = lds_addr(stages);
+  const int qpos0 = prefix + qb0;  // position of query column 0 of block 0
+
+  load_tile(0);
+  store_tile(stages);
+  bool cur_ok = tile_ok;
+  __syncthreads();
+  for (int t = 0; t < ntiles; ++t) {
+    const bool more = t + 1 < ntiles;
+    if (more) load_tile(t + 1);
+    const uint32_t soff = static_cast<uint32_t>(t & 1) * kStage;
+    const uint8_t* st = stages + soff;
+    if (cur_ok) {
+#pragma unroll 1
+      for (int sb = 0; sb < KT / 16; ++sb) {
+        const int key0 = t * KT + sb * 16;                   // first key of the sub-block
+        if (key0 > qpos0 + kPfQTile - 1) break;              // above the diagonal for every column
+        const uint8_t* sbp = st + sb * 16 * kRow;
+        const u32x4 k0 = *reinterpret_cast<const u32x4*>(sbp + k_off0);
+        const u32x4 k1 = *reinterpret_cast<const u32x4*>(sbp + k_off1);
+        const float* scl = reinterpret_cast<const float*>(st + 2 * kPayload) + sb * 16 + 4 * g;
+        const floatx4 ksv = *reinterpret_cast<const floatx4*>(scl);
+        const floatx4 vsv = *reinterpret_cast<const floatx4*>(scl + KT);
+        uint32_t ad[4];
+#pragma unroll
+        for (int jp = 0; jp < 4; ++jp) ad[jp] = stage_base + soff + sb * 16 * kRow + v_off[jp];
+        uint64_t vt[4];
+        lds_read_tr8_x4(ad, vt);
+        // K operand (A of S^T), shared by the column blocks
+        typename PfQOperand<QDT>::T kop[4];
+#pragma unroll
+        for (int cc = 0; cc < 4; ++cc) {
+          const u32x4& kw = (cc < 2) ? k0 : k1;
+          if constexpr (QDT == PRISM_DTYPE_F16) kop[cc] = fp8x8_to_f16x8(kw[(cc & 1) * 2], kw[(cc & 1) * 2 + 1]);
+          else kop[cc] = fp8x8_to_bf16x8(kw[(cc & 1) * 2], kw[(cc & 1) * 2 + 1]);
+        }
+        // keys past the context end may hold any bytes: zero them in V
+        uint32_t keep = 0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) keep |= (key0 + 4 * g + i < ctx) ? (0xFFu << (8 * i)) : 0u;
+        const float vmax4 = fmaxf(fmaxf(vsv[0], vsv[1]), fmaxf(vsv[2], vsv[3]));
+        int vexp = 0;  // wave-uniform power-of-two shift of P * v_scale
+        if (__builtin_amdgcn_ballot_w64(vmax4 > kPfF16MaxVScale) != 0) {
+          float vmax = vmax4;
+#pragma unroll
+          for (int off = 32; off >= 1; off >>= 1) vmax = fmaxf(vmax, __shfl_xor(vmax, off));
+          vexp = __builtin_amdgcn_readfirstlane(ilogbf(vmax / kPfF16MaxVScale) + 1);
+        }
+        f16x4 vb[8];
+#pragma unroll
+        for (int jp = 0; jp < 4; ++jp) {
+          vb[2 * jp] = fp8x4_to_f16x4(static_cast<uint32_t>(vt[jp]) & keep);
+          vb[2 * jp + 1] = fp8x4_to_f16x4(static_cast<uint32_t>(vt[jp] >> 32) & keep);
+        }
+#pragma unroll
+        for (int cb = 0; cb < kPfColBlocks; ++cb) {
+          floatx4 sca = {0.f, 0.f, 0.f, 0.f}, scb = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int cc = 0; cc < 4; ++cc) {
+            floatx4& sc = (cc & 1) ? scb : sca;
+            if constexpr (QDT == PRISM_DTYPE_F16)
+              sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[cc], qop[cb].op[cc], sc, 0, 0, 0);
+            else
+              sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[cc], qop[cb].op[cc], sc, 0, 0, 0);
+          }
+          // causal mask: key key0 + 4g + i is visible to column c iff it is
+          // at or before the query's position
+          const int qpos = qpos0 + cb * kPfCols + c;
+          float x[4];
+          float tmax = -INFINITY;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const bool vis = colv[cb] && key0 + 4 * g + i <= qpos;
+            x[i] = vis ? (sca[i] + scb[i]) * (ksv[i] * a.scale_log2) : -INFINITY;
+            tmax = fmaxf(tmax, x[i]);
+          }
+          tmax = wave_max_across_groups(tmax);
+          const bool raise = tmax > m_run[cb] + kPfRescaleThreshold;
+          if (__builtin_amdgcn_ballot_w64(raise) != 0) {
+            const float m_new = raise ? tmax : m_run[cb];
+            const float alpha = raise ? exp2f(m_run[cb] - m_new) : 1.f;
+            m_run[cb] = m_new;
+            l_run[cb] *= alpha;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const float ai = __shfl(alpha, 4 * g + i);
+#pragma unroll
+              for (int j = 0; j < 8; ++j) acc[cb][j][i] *= ai;
+            }
+          }
+          const float m_use = (m_run[cb] == -INFINITY) ? 0.f : m_run[cb];
+          float pv[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float p = exp2f(x[i] - m_use);  // 0 where masked
+            l_run[cb] += p;
+            pv[i] = p * vsv[i];
+          }
+          if (vexp != 0) {
+            const float down = ldexpf(1.f, -vexp);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[cb][j] *= down;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) pv[i] *= down;
+          }
+          const f16x4 pa = {static_cast<_Float16>(pv[0]), static_cast<_Float16>(pv[1]),
+                            static_cast<_Float16>(pv[2]), static_cast<_Float16>(pv[3])};
+#pragma unroll
+          for (int j = 0; j < 8; ++j) acc[cb][j] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, vb[j], acc[cb][j], 0, 0, 0);
+          if (vexp != 0) {
+            const float up = ldexpf(1.f, vexp);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[cb][j] *= up;
+          }
+        }
+      }
+    }
+    if (more) {
+      // the other stage was last read while computing tile t - 1, which every
+      // wave finished before the barrier that ended that iteration
+      store_tile(stages + ((t + 1) & 1) * kStage);
+      cur_ok = tile_ok;
+    }
+    __syncthreads();
+  }
+
+  // ---- epilogue: acc[cb][j][i] is query column 4g + i of block cb, dim 16j + c
+#pragma unroll
+  for (int cb = 0; cb < kPfColBlocks; ++cb) {
+    float l_tot = l_run[cb] + __shfl_xor(l_run[cb], 16);
+    l_tot += __shfl_xor(l_tot, 32);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int qr = 4 * g + i;
+      const float li = __shfl(l_tot, qr);
+      const int j = qb0 + cb * kPfCols + qr;
+      if (j < qlen) {
+        const float inv = li > 0.f ? 1.f / li : 0.f;
+        uint16_t* dst = static_cast<uint16_t*>(a.out) + static_cast<int64_t>(qs + j) * a.o_st +
+                        static_cast<int64_t>(qhead) * a.o_sh + c;
+#pragma unroll
+        for (int jd = 0; jd < 8; ++jd) {
+          const float o = acc[cb][jd][i] * inv;
+          dst[16 * jd] = (QDT == PRISM_DTYPE_F16) ? f32_to_f16_bits(o) : f32_to_bf16_bits(o);
+        }
+      }
+    }
+  }
+}
+
+template <int QDT, int KT, int NW>
+int launch_prefill(const PrefillArgs& a, bool scaled, int total_q, hipStream_t stream) {
+  const dim3 grid(static_cast<unsigned>(ceil_div(total_q, kPfQTile) + a.batch),
+                  static_cast<unsigned>(a.num_heads / a.groups));
+  const dim3 block(64 * NW);
+  if (scaled) hipLaunchKernelGGL((paged_prefill_kernel<QDT, KT, NW, true>), grid, block, 0, stream, a);
+  else hipLaunchKernelGGL((paged_prefill_kernel<QDT, KT, NW, false>), grid, block, 0, stream, a);
+  return check_launch("paged_prefill_kernel launch");
+}
+
+// Key tiles of 64 (pages of a multiple of 64 tokens) or 16; one wave per
+// query head of the GQA group (1, 2, 4 or 8).
+template <int QDT, int KT>
+int dispatch_waves(const PrefillArgs& a, bool scaled, int total_q, hipStream_t stream) {
+  switch (a.groups) {
+    case 1: return launch_prefill<QDT, 16, 1>(a, scaled, total_q, stream);
+    case 2: return launch_prefill<QDT, KT, 2>(a, scaled, total_q, stream);
+    case 4: return launch_prefill<QDT, KT, 4>(a, scaled, total_q, stream);
+    case 8: return launch_prefill<QDT, KT, 8>(a, scaled, total_q, stream);
+    default:
+      set_error("prism_paged_prefill: GQA group size %d is not 1, 2, 4 or 8", a.groups);
+      return PRISM_ERR_LAYOUT;
+  }
+}
+
+template <int QDT>
+int dispatch_tile(const PrefillArgs& a, bool scaled, int total_q, hipStream_t stream) {
+  // one wave would hold 16 chunks of a 64-key tile in flight: too many VGPRs
+  if (a.page % 64 == 0 && a.groups > 1) return dispatch_waves<QDT, 64>(a, scaled, total_q, stream);
+  return dispatch_waves<QDT, 16>(a, scaled, total_q, stream);
+}
+
+}  // namespace
+}  // namespace prism
+
+extern "C" int prism_paged_prefill(const void* q, int q_dtype, const int64_t q_strides[3], const void* k_cache,
+                                   const void* v_cache, int cache_dtype, const int64_t k_strides[4],
+                                   const int64_t v_strides[4], const float* k_scale, const float* v_scale,
+                                   const int64_t k_scale_strides[3], const int64_t v_scale_strides[3],
+                                   const int32_t* block_tables, const int64_t bt_strides[2],
+                                   const int32_t* context_lens, const int32_t* cu_seqlens_q, void* out,
+                                   const int64_t out_strides[3], int batch, int total_q, int num_heads,
+                                   int num_kv_heads, int head_dim, int page_size, int num_blocks, int width,
+                                   float scale, int32_t* status, void* stream_ptr) {
+  using namespace prism;
+  clear_error();
+  if (batch < 0 || total_q < 0 || num_heads <= 0 || num_kv_heads <= 0 || page_size <= 0 || num_blocks < 0 ||
+      width < 0) {
+    set_error("prism_paged_prefill: invalid geometry");
+    return PRISM_ERR_INVALID;
+  }
+  if (num_heads % num_kv_heads != 0 || num_heads / num_kv_heads > kPfMaxWaves) {
+    set_error("prism_paged_prefill: num_heads=%d / num_kv_heads=%d must be an integer group of at most %d",
+              num_heads, num_kv_heads, kPfMaxWaves);
+    return PRISM_ERR_LAYOUT;
+  }
+  if (head_dim != kPfD) {
+    set_error("prism_paged_prefill: head_dim must be %d, got %d", kPfD, head_dim);
+    return PRISM_ERR_LAYOUT;
+  }
+  if (cache_dtype != PRISM_DTYPE_FP8_E4M3FN) {
+    set_error("prism_paged_prefill: the cache must be FP8 E4M3FN (dtype code %d)", cache_dtype);
+    return PRISM_ERR_LAYOUT;
+  }
+  if (q_dtype != PRISM_DTYPE_BF16 && q_dtype != PRISM_DTYPE_F16) {
+    set_error("prism_paged_prefill: q must be bf16 or float16 (dtype code %d)", q_dtype);
+    return PRISM_ERR_LAYOUT;
+  }
+  if (page_size % 16 != 0) {
+    set_error("prism_paged_prefill: page size must be a multiple of 16, got %d", page_size);
+    return PRISM_ERR_LAYOUT;
+  }
+  if ((k_scale == nullptr) != (v_scale == nullptr)) {
+    set_error("prism_paged_prefill: K/V scale caches must be provided together");
+    return PRISM_ERR_INVALID;
+  }
+  if (!q_strides || !k_strides || !v_strides || !bt_strides || !out_strides || !status ||
+      (k_scale && (!k_scale_strides || !v_scale_strides))) {
+    set_error("prism_paged_prefill: null argument");
+    return PRISM_ERR_INVALID;
+  }
+  if (q_strides[2] != 1 || k_strides[3] != 1 || v_strides[3] != 1 || out_strides[2] != 1 ||
+      !aligned(q, 16) || !aligned(k_cache, 16) || !aligned(v_cache, 16) || q_strides[0] % 8 || q_strides[1] % 8 ||
+      k_strides[0] % 16 || k_strides[1] % 16 || k_strides[2] % 16 || v_strides[0] % 16 || v_strides[1] % 16 ||
+      v_strides[2] % 16) {
+    set_error("prism_paged_prefill: q, K/V and out need unit-stride head dims and 16-byte aligned rows");
+    return PRISM_ERR_LAYOUT;
+  }
+  if (batch == 0 || total_q == 0) return PRISM_OK;
+  PrefillArgs a{};
+  a.q = q;
+  a.q_st = q_strides[0];
+  a.q_sh = q_strides[1];
+  a.k = static_cast<const uint8_t*>(k_cache);
+  a.v = static_cast<const uint8_t*>(v_cache);
+  a.k_sn = k_strides[0], a.k_sp = k_strides[1], a.k_sh = k_strides[2];
+  a.v_sn = v_strides[0], a.v_sp = v_strides[1], a.v_sh = v_strides[2];
+  a.ks = k_scale;
+  a.vs = v_scale;
+  if (k_scale) {
+    a.ks_sn = k_scale_strides[0], a.ks_sp = k_scale_strides[1], a.ks_sh = k_scale_strides[2];
+    a.vs_sn = v_scale_strides[0], a.vs_sp = v_scale_strides[1], a.vs_sh = v_scale_strides[2];
+  }
+  a.bt = block_tables;
+  a.bt_sb = bt_strides[0];
+  a.bt_sn = bt_strides[1];
+  a.ctx = context_lens;
+  a.cu_q = cu_seqlens_q;
+  a.out = out;
+  a.o_st = out_strides[0];
+  a.o_sh = out_strides[1];
+  a.batch = batch;
+  a.num_heads = num_heads;
+  a.groups = num_heads / num_kv_heads;
+  a.page = page_size;
+  a.num_blocks = num_blocks;
+  a.width = width;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  a.status = status;
+  hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
+  const bool scaled = k_scale != nullptr;
+  if (q_dtype == PRISM_DTYPE_F16) return dispatch_tile<PRISM_DTYPE_F16>(a, scaled, total_q, stream);
+  return dispatch_tile<PRISM_DTYPE_BF16>(a, scaled, total_q, stream);
+}

@@ -59,10 +59,15 @@ SIGNATURES: dict[str, tuple] = {
     "prism_compact_slots_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64]),
     "prism_compact_slots": (_I, [_VP, _I64, _I64, _I64, _VP, _VP, _I64, _VP, _I64, _VP]),
     "prism_copy_blocks": (_I, [_VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _I64P, _I64P, _I64, _VP]),
+    "prism_paged_prefill": (
+        _I,
+        [_VP, _I, _I64P, _VP, _VP, _I, _I64P, _I64P, _VP, _VP, _I64P, _I64P, _VP, _I64P, _VP, _VP, _VP,
+         _I64P, _I, _I, _I, _I, _I, _I, _I, _I, _F, _VP, _VP],
+    ),
     "prism_debug_fp8_encode": (_I, [_VP, _VP, _I64, _VP]),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _LIB: ctypes.CDLL | None = None
 

@@ -16,6 +16,10 @@ heads over 8 KV heads, head_dim 128, 256-token pages unless stated):
 * ``compaction``      -- 64 prefixes x 8192 tokens, seeded keep-mask dropping
                          ~30% of visual positions [64, 8192), >= 768 kept.
 * ``decode_long``     -- B=256, 32k context each, pages scattered in a pool.
+* ``prefill_chunked`` -- paged prefill: B=4 sequences, each an 8192-token
+                         cached prefix plus a 2048-token chunk (already
+                         stored), 40 pages per sequence drawn without
+                         replacement from a 512-page pool.
 
 Index metadata is drawn on the CPU with ``torch.Generator`` so it is identical
 on every machine.  K/V values are drawn as bf16 N(0,1) on the target device
@@ -192,6 +196,72 @@ def decode_long(device, seed: int = 20260805, *, batch: int = 256, context_len: 
     pool = _alloc_pool(pool_pages, device)
     return _finish("decode_long", q, pool, tables, [context_len] * batch, seed, perm.clone(),
                    batch * context_len, fill=fill)
+
+
+@dataclass
+class PrefillWorkload:
+    q: torch.Tensor                     # [total_q, Hq, D] bf16
+    k_cache: torch.Tensor
+    v_cache: torch.Tensor
+    k_scale: torch.Tensor
+    v_scale: torch.Tensor
+    block_tables: torch.Tensor          # int32 [B, W]
+    context_lens: torch.Tensor          # int32 [B]
+    cu_seqlens_q: torch.Tensor          # int32 [B + 1]
+    scale: float
+    query_lens: list
+    ctx_lens: list
+
+    @property
+    def num_heads(self) -> int:
+        return self.q.shape[1]
+
+    @property
+    def num_kv_heads(self) -> int:
+        return self.k_cache.shape[2]
+
+    def attended_pairs(self) -> int:
+        """Sum over sequences of (query, key) pairs the causal mask admits."""
+
+        total = 0
+        for n, ctx in zip(self.query_lens, self.ctx_lens):
+            prefix = ctx - n
+            total += n * prefix + n * (n + 1) // 2
+        return total
+
+    def flops(self) -> int:
+        """2 * D multiply-adds per (query head, visible key) for QK^T and again for PV."""
+
+        return 4 * self.q.shape[2] * self.num_heads * self.attended_pairs()
+
+    def algorithmic_bytes(self) -> int:
+        kv_heads, dim = self.k_cache.shape[2], self.k_cache.shape[3]
+        per_token = 2 * kv_heads * dim + 2 * kv_heads * 4
+        q_out = 2 * self.q.numel() * self.q.element_size()
+        meta = self.block_tables.numel() * 4 + len(self.ctx_lens) * 8 + 4
+        return sum(self.ctx_lens) * per_token + q_out + meta
+
+
+def prefill_chunked(device, seed: int = 20260807, *, batch: int = 4, prefix: int = 8192, chunk: int = 2048,
+                    pool_pages: int = 512, fill: bool = True) -> PrefillWorkload:
+    g = _gen(seed)
+    ctx = prefix + chunk
+    pages_per = math.ceil(ctx / PAGE_SIZE)
+    if batch * pages_per > pool_pages:
+        raise ValueError("pool too small for the prefill workload")
+    perm = torch.randperm(pool_pages, generator=g)[:batch * pages_per].view(batch, pages_per)
+    q = torch.randn(batch * chunk, NUM_HEADS, HEAD_DIM, generator=g, dtype=torch.float32).to(torch.bfloat16)
+    pool = _alloc_pool(pool_pages, device)
+    if fill:
+        fill_pages(*pool, perm.reshape(-1), seed + 1)
+    cu = torch.arange(batch + 1, dtype=torch.int32) * chunk
+    return PrefillWorkload(
+        q=q.to(device), k_cache=pool[0], v_cache=pool[1], k_scale=pool[2], v_scale=pool[3],
+        block_tables=perm.to(torch.int32).to(device),
+        context_lens=torch.full((batch,), ctx, dtype=torch.int32).to(device),
+        cu_seqlens_q=cu.to(device), scale=HEAD_DIM ** -0.5,
+        query_lens=[chunk] * batch, ctx_lens=[ctx] * batch,
+    )
 
 
 @dataclass
