@@ -43,6 +43,7 @@ inline int dtype_size(int dtype) {
 // ---------------------------------------------------------------- device side
 
 typedef float floatx2 __attribute__((ext_vector_type(2)));
+typedef int i32x8 __attribute__((ext_vector_type(8)));
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));

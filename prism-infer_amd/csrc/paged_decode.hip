@@ -684,6 +684,94 @@ __device__ __forceinline__ void stream_load_q(const DecodeArgs& a, int qrow, int
 
 
 
+// Query operand of the streaming kernel for the fp8 MFMA (16x16x128): lane
+// (g, c) holds column c's dims 32g..32g+31 as fp8 bytes, the same bytes of
+// the K rows it multiplies.  Each column is scaled by 2^e so that its
+// largest |q| lies in [128, 256), then split into three E4M3FN terms,
+// hi + mid + lo, each the round-to-nearest of what the previous terms left:
+// four significant bits per term, so a bf16 query (eight bits) is
+// represented exactly except for elements below 2^-9 after scaling (at most
+// 2^-17 of the column's largest), and f16/f32 queries to about 2^-12
+// relative.  The score is then (K . (hi + mid + lo)) * 2^-e, and 2^-e is
+// folded into the per-column score multiplier.
+struct QOperandF8 {
+  i32x8 t[3];      // hi, mid, lo
+  float colscale;  // scale_log2 * 2^-e of this lane's column
+};
+
+__device__ __forceinline__ void fp8_split3(const float (&y)[4], uint32_t (&out)[3]) {
+  float r[4] = {y[0], y[1], y[2], y[3]};
+#pragma unroll
+  for (int t = 0; t < 3; ++t) {
+    int w = __builtin_amdgcn_cvt_pk_fp8_f32(r[0], r[1], 0, false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(r[2], r[3], w, true);
+    out[t] = static_cast<uint32_t>(w);
+    if (t < 2) {
+      const floatx2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
+      const floatx2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(w, true);
+      r[0] -= lo[0];
+      r[1] -= lo[1];
+      r[2] -= hi[0];
+      r[3] -= hi[1];
+    }
+  }
+}
+
+template <int QDT, bool QVEC>
+__device__ __forceinline__ void stream_load_q8(const DecodeArgs& a, int qrow, int qhead, bool qvalid, int g,
+                                               QOperandF8& qop) {
+  const int64_t qbase = static_cast<int64_t>(qrow) * a.q_sb + static_cast<int64_t>(qhead) * a.q_sh;
+  float x[32];
+#pragma unroll
+  for (int cc = 0; cc < 4; ++cc) {
+    const int64_t d0 = 32 * g + 8 * cc;
+    float* xc = x + 8 * cc;
+    if constexpr (QVEC) {
+      if constexpr (QDT == PRISM_DTYPE_F32) {
+        const floatx4* p = reinterpret_cast<const floatx4*>(static_cast<const float*>(a.q) + qbase + d0);
+        const floatx4 lo = p[0], hi = p[1];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) xc[e] = lo[e], xc[4 + e] = hi[e];
+      } else {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.q) + qbase + d0);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          if constexpr (QDT == PRISM_DTYPE_BF16) {
+            xc[2 * e] = bf16_bits_to_f32(w[e] & 0xFFFFu);
+            xc[2 * e + 1] = bf16_bits_to_f32(w[e] >> 16);
+          } else {
+            xc[2 * e] = f16_bits_to_f32(w[e] & 0xFFFFu);
+            xc[2 * e + 1] = f16_bits_to_f32(w[e] >> 16);
+          }
+        }
+      }
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xc[e] = load_q<QDT>(a.q, qbase + (d0 + e) * a.q_sd);
+    }
+  }
+  float mx = 0.f;
+#pragma unroll
+  for (int e = 0; e < 32; ++e) {
+    x[e] = qvalid ? x[e] : 0.f;
+    mx = fmaxf(mx, fabsf(x[e]));
+  }
+  mx = wave_max_across_groups(mx);
+  // 2^e puts the column's largest |q| in [128, 256); clamped so that 2^-e
+  // stays a normal fp32 number (columns of zeros keep e = 0).
+  const int e = (mx > 0.f && mx <= 3.0e38f) ? min(max(7 - ilogbf(mx), -120), 120) : 0;
+  qop.colscale = ldexpf(a.scale_log2, -e);
+#pragma unroll
+  for (int w = 0; w < 8; ++w) {
+    const float y[4] = {ldexpf(x[4 * w], e), ldexpf(x[4 * w + 1], e), ldexpf(x[4 * w + 2], e),
+                        ldexpf(x[4 * w + 3], e)};
+    uint32_t parts[3];
+    fp8_split3(y, parts);
+#pragma unroll
+    for (int t = 0; t < 3; ++t) qop.t[t][w] = static_cast<int>(parts[t]);
+  }
+}
+
 // ------------------------------------------------------------ shared pages
 //
 // Prefix sharing: sequences whose block tables start with the same physical
@@ -1136,12 +1224,12 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   int cbt_row, ctok0, n_eff, crot;
   stream_seq(a, tstart, V, b, cbt_row, ctok0, n_eff, crot);
   int cpage = -1, cok = 0;
-  QOperand<QDT> qop;
+  QOperandF8 qop;
   bool colv;
   {
     int qrow, qhead;
     stream_column(a, V, b, h, c, qrow, qhead, colv);
-    stream_load_q<QDT, QVEC>(a, qrow, qhead, colv, g, qop);
+    stream_load_q8<QDT, QVEC>(a, qrow, qhead, colv, g, qop);
   }
 
   floatx4 acc[8];
@@ -1203,30 +1291,22 @@ paged_decode_stream_kernel(const DecodeArgs a) {
       for (int jp = 0; jp < 4; ++jp) ad[jp] = stage0 + slot + v_off[jp];
       uint64_t vt[4];
       lds_read_tr8_x4(ad, vt);
-      // ---- QK over 16 tokens: two independent MFMA chains
-      floatx4 sca = {0.f, 0.f, 0.f, 0.f}, scb = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int cc = 0; cc < 4; ++cc) {
-        const u32x4& kw = (cc < 2) ? k0 : k1;
-        const uint32_t w0 = kw[(cc & 1) * 2];
-        const uint32_t w1 = kw[(cc & 1) * 2 + 1];
-        floatx4& sc = (cc & 1) ? scb : sca;
-        if constexpr (QDT == PRISM_DTYPE_F16) {
-          sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(fp8x8_to_f16x8(w0, w1), qop.hi[cc], sc, 0, 0, 0);
-        } else {
-          const bf16x8 kb = fp8x8_to_bf16x8(w0, w1);
-          sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qop.hi[cc], sc, 0, 0, 0);
-          if constexpr (QDT == PRISM_DTYPE_F32)
-            sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qop.lo[cc], sc, 0, 0, 0);
-        }
-      }
+      // ---- QK over 16 tokens: the K bytes are the fp8 MFMA's A operand as
+      // they are (row = token c, k = dims 32g..32g+31); smallest term first.
+      const i32x8 ka = {static_cast<int>(k0[0]), static_cast<int>(k0[1]), static_cast<int>(k0[2]),
+                        static_cast<int>(k0[3]), static_cast<int>(k1[0]), static_cast<int>(k1[1]),
+                        static_cast<int>(k1[2]), static_cast<int>(k1[3])};
+      floatx4 sc = {0.f, 0.f, 0.f, 0.f};
+      sc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, qop.t[2], sc, 0, 0, 0, 0, 0, 0);
+      sc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, qop.t[1], sc, 0, 0, 0, 0, 0, 0);
+      sc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, qop.t[0], sc, 0, 0, 0, 0, 0, 0);
       // ---- scores in the log2 domain.  Query columns without a query hold
       // q = 0, so their scores are finite and their rows are never written.
       float x[4];
       float vsm[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        x[i] = (sca[i] + scb[i]) * (ks[i] * a.scale_log2);
+        x[i] = sc[i] * (ks[i] * qop.colscale);
         vsm[i] = vs[i];
       }
       // Only a sequence's last tile can reach past its end (uniform branch).
@@ -1346,7 +1426,7 @@ paged_decode_stream_kernel(const DecodeArgs a) {
         stream_seq(a, tstart, V, b, cbt_row, ctok0, n_eff, crot);
         int qrow, qhead;
         stream_column(a, V, b, h, c, qrow, qhead, colv);
-        stream_load_q<QDT, QVEC>(a, qrow, qhead, colv, g, qop);
+        stream_load_q8<QDT, QVEC>(a, qrow, qhead, colv, g, qop);
       }
     } else {
       ++lt;

@@ -129,6 +129,30 @@ def test_query_dtypes_and_strided_query(qdtype, decode_path):
     assert_decode_close(got, _oracle(q, k, v, ks, vs, tables, lens, 128 ** -0.5), label=str(qdtype))
 
 
+@pytest.mark.parametrize("qdtype,lo_exp,hi_exp", [(torch.bfloat16, -6.0, 4.0), (torch.float32, -3.0, 1.5)])
+def test_query_magnitudes_per_head(qdtype, lo_exp, hi_exp, decode_path):
+    """Query heads spanning many orders of magnitude, plus an all-zero head.
+
+    The streaming kernel scales each query column by a power of two and splits
+    it into three fp8 terms for the QK MFMA: tiny heads (near-uniform softmax),
+    huge heads (near one-hot) and a zero head exercise that scaling.
+    """
+
+    require_gpu()
+    g = torch.Generator().manual_seed(31)
+    pool, batch = 48, 4
+    mags = torch.logspace(lo_exp, hi_exp, 32)
+    q = torch.randn(batch, 32, 128, generator=g) * mags[None, :, None]
+    q[:, 5] = 0.0
+    q = q.to(qdtype)
+    k, ks = _quantize_cpu(torch.randn(pool, 256, 8, 128, generator=g).to(torch.bfloat16))
+    v, vs = _quantize_cpu(torch.randn(pool, 256, 8, 128, generator=g).to(torch.bfloat16))
+    tables = torch.randperm(pool, generator=g)[:48].to(torch.int32).view(batch, 12)
+    lens = torch.tensor([3000, 2049, 1024, 2900], dtype=torch.int32)
+    got = _decode_gpu(q, k, v, ks, vs, tables, lens, 128 ** -0.5)
+    assert_decode_close(got, _oracle(q, k, v, ks, vs, tables, lens, 128 ** -0.5), label=f"mags {qdtype}")
+
+
 def test_small_gqa_generic_path_and_unscaled_caches():
     """head_dim 16 / page 4 (generic kernel), unit-scale FP8 and bf16 caches."""
 
