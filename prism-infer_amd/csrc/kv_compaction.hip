@@ -16,6 +16,8 @@
 // bytes per lane when the row width allows it, 4 or 1 bytes otherwise.
 #include "common.h"
 
+#include <algorithm>
+
 namespace prism {
 namespace {
 
@@ -81,39 +83,64 @@ struct Chunk<1> { using T = uint8_t; };
 // MODE 0: direct copy (skip when the hazard flag is set)
 // MODE 1: gather into temp (only when the flag is set)
 // MODE 2: scatter from temp (only when the flag is set)
+//
+// Grid (x: chunk ranges, y: rows).  Chunk c of a row is part c & (U - 1) of
+// entry c >> USHIFT when a row vector holds U = 2^USHIFT chunks (every
+// canonical shape: token rows of 1024 or 32 bytes, whole blocks), else
+// c / U and c % U (USHIFT < 0).  Each thread moves four chunks per trip with
+// the four loads issued before the stores, and every byte is read and
+// written once, so both go through the non-temporal cache policy.
 template <int BYTES, int MODE>
 __global__ void __launch_bounds__(kThreads)
-compact_move_kernel(uint8_t* __restrict__ cache, int64_t rows, int64_t num_slots, int64_t vec_bytes,
+compact_move_kernel(uint8_t* __restrict__ cache, int64_t num_slots, int64_t vec_bytes, int ushift,
                     const int64_t* __restrict__ src, const int64_t* __restrict__ dst, int64_t retained,
                     uint8_t* __restrict__ temp, const uint32_t* __restrict__ flag) {
   using T = typename Chunk<BYTES>::T;
   const bool staged = *flag != 0u;
   if ((MODE == 0) == staged) return;
   const int64_t chunks_per_vec = vec_bytes / BYTES;
-  const int64_t total = rows * retained * chunks_per_vec;
-  for (int64_t c = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; c < total;
-       c += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int64_t item = c / chunks_per_vec;
-    const int64_t part = c - item * chunks_per_vec;
-    const int64_t row = item / retained;
-    const int64_t i = item - row * retained;
-    const int64_t s = src[i];
-    const int64_t d = dst[i];
-    if (s < 0 || s >= num_slots || d < 0 || d >= num_slots) continue;
-    const int64_t row_base = row * num_slots;
-    const T* from;
-    T* to;
-    if (MODE == 0) {
-      from = reinterpret_cast<const T*>(cache + (row_base + s) * vec_bytes) + part;
-      to = reinterpret_cast<T*>(cache + (row_base + d) * vec_bytes) + part;
-    } else if (MODE == 1) {
-      from = reinterpret_cast<const T*>(cache + (row_base + s) * vec_bytes) + part;
-      to = reinterpret_cast<T*>(temp + item * vec_bytes) + part;
-    } else {
-      from = reinterpret_cast<const T*>(temp + item * vec_bytes) + part;
-      to = reinterpret_cast<T*>(cache + (row_base + d) * vec_bytes) + part;
+  const int64_t per_row = retained * chunks_per_vec;
+  const int64_t row = blockIdx.y;
+  const int64_t row_base = row * num_slots;
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+  constexpr int kUnroll = 4;
+  for (int64_t base = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; base < per_row;
+       base += kUnroll * stride) {
+    T val[kUnroll];
+    T* to[kUnroll];
+    bool ok[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int64_t c = base + u * stride;
+      int64_t i, part;
+      if (ushift >= 0) {
+        i = c >> ushift;
+        part = c & (chunks_per_vec - 1);
+      } else {
+        i = c / chunks_per_vec;
+        part = c - i * chunks_per_vec;
+      }
+      ok[u] = c < per_row;
+      const int64_t s = ok[u] ? src[i] : -1;
+      const int64_t d = ok[u] ? dst[i] : -1;
+      ok[u] = ok[u] && s >= 0 && s < num_slots && d >= 0 && d < num_slots;
+      const int64_t item = row * retained + i;
+      const T* from;
+      if (MODE == 0) {
+        from = reinterpret_cast<const T*>(cache + (row_base + s) * vec_bytes) + part;
+        to[u] = reinterpret_cast<T*>(cache + (row_base + d) * vec_bytes) + part;
+      } else if (MODE == 1) {
+        from = reinterpret_cast<const T*>(cache + (row_base + s) * vec_bytes) + part;
+        to[u] = reinterpret_cast<T*>(temp + item * vec_bytes) + part;
+      } else {
+        from = reinterpret_cast<const T*>(temp + item * vec_bytes) + part;
+        to[u] = reinterpret_cast<T*>(cache + (row_base + d) * vec_bytes) + part;
+      }
+      if (ok[u]) val[u] = __builtin_nontemporal_load(from);
     }
-    *to = *from;
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u)
+      if (ok[u]) __builtin_nontemporal_store(val[u], to[u]);
   }
 }
 
@@ -128,20 +155,47 @@ template <int BYTES>
 int launch_moves(uint8_t* cache, int64_t rows, int64_t num_slots, int64_t vec_bytes, const int64_t* src,
                  const int64_t* dst, int64_t retained, uint8_t* temp, const uint32_t* flag,
                  hipStream_t stream) {
-  const int64_t total = rows * retained * (vec_bytes / BYTES);
-  const int cap = device_cu_count() * 16;
-  const int grid = grid_for(total, cap);
-  hipLaunchKernelGGL((compact_move_kernel<BYTES, 0>), dim3(grid), dim3(kThreads), 0, stream, cache, rows,
-                     num_slots, vec_bytes, src, dst, retained, temp, flag);
-  int rc = check_launch("compact direct copy launch");
-  if (rc) return rc;
-  hipLaunchKernelGGL((compact_move_kernel<BYTES, 1>), dim3(grid), dim3(kThreads), 0, stream, cache, rows,
-                     num_slots, vec_bytes, src, dst, retained, temp, flag);
-  rc = check_launch("compact gather launch");
-  if (rc) return rc;
-  hipLaunchKernelGGL((compact_move_kernel<BYTES, 2>), dim3(grid), dim3(kThreads), 0, stream, cache, rows,
-                     num_slots, vec_bytes, src, dst, retained, temp, flag);
-  return check_launch("compact scatter launch");
+  const int64_t chunks_per_vec = vec_bytes / BYTES;
+  int ushift = -1;
+  if ((chunks_per_vec & (chunks_per_vec - 1)) == 0) {
+    ushift = 0;
+    while ((int64_t{1} << ushift) < chunks_per_vec) ++ushift;
+  }
+  const int64_t per_row = retained * chunks_per_vec;
+  // about 8 workgroups per CU in total, spread over the rows
+  const int64_t cap = std::max<int64_t>(1, device_cu_count() * 8 / std::max<int64_t>(rows, 1));
+  const int gx = grid_for(ceil_div(per_row, 4), cap);
+  for (int64_t r0 = 0; r0 < rows; r0 += 65535) {  // grid.y limit
+    const int64_t nr = std::min<int64_t>(rows - r0, 65535);
+    uint8_t* c = cache + r0 * num_slots * vec_bytes;
+    uint8_t* t = temp + r0 * retained * vec_bytes;
+    const dim3 grid(gx, static_cast<unsigned>(nr));
+    hipLaunchKernelGGL((compact_move_kernel<BYTES, 0>), grid, dim3(kThreads), 0, stream, c, num_slots, vec_bytes,
+                       ushift, src, dst, retained, t, flag);
+    int rc = check_launch("compact direct copy launch");
+    if (rc) return rc;
+  }
+  for (int64_t r0 = 0; r0 < rows; r0 += 65535) {
+    const int64_t nr = std::min<int64_t>(rows - r0, 65535);
+    uint8_t* c = cache + r0 * num_slots * vec_bytes;
+    uint8_t* t = temp + r0 * retained * vec_bytes;
+    const dim3 grid(gx, static_cast<unsigned>(nr));
+    hipLaunchKernelGGL((compact_move_kernel<BYTES, 1>), grid, dim3(kThreads), 0, stream, c, num_slots, vec_bytes,
+                       ushift, src, dst, retained, t, flag);
+    int rc = check_launch("compact gather launch");
+    if (rc) return rc;
+  }
+  for (int64_t r0 = 0; r0 < rows; r0 += 65535) {
+    const int64_t nr = std::min<int64_t>(rows - r0, 65535);
+    uint8_t* c = cache + r0 * num_slots * vec_bytes;
+    uint8_t* t = temp + r0 * retained * vec_bytes;
+    const dim3 grid(gx, static_cast<unsigned>(nr));
+    hipLaunchKernelGGL((compact_move_kernel<BYTES, 2>), grid, dim3(kThreads), 0, stream, c, num_slots, vec_bytes,
+                       ushift, src, dst, retained, t, flag);
+    int rc = check_launch("compact scatter launch");
+    if (rc) return rc;
+  }
+  return PRISM_OK;
 }
 
 }  // namespace

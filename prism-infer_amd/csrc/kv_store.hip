@@ -194,6 +194,12 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_over(void* base, uint32
   return __builtin_amdgcn_make_buffer_rsrc(base, 0, static_cast<int>(bytes), 0x00020000);
 }
 
+// Cache-policy operand of the token path's buffer stores: non-temporal.  The
+// cache rows are written once here and read back by a later decode, so
+// they need not occupy the caches on the way (the input rows are read with
+// non-temporal loads for the same reason).
+constexpr int kNtPolicy = 2;
+
 // Token path: one wave per token, no branches on the slot.  Every lane
 // issues all of its 2 * PASSES 16-byte input loads (K passes, then V passes)
 // together with the slot load, so a wave has the token's whole K and V rows
@@ -231,7 +237,7 @@ kv_store_token_kernel(const char* __restrict__ key, const char* __restrict__ val
     for (int p = 0; p < PASSES; ++p) {
       const u32x4* src = reinterpret_cast<const u32x4*>(row + p * 64 * 8 * IN_BYTES);
 #pragma unroll
-      for (int c = 0; c < IN_BYTES / 2; ++c) raw[which][p][c] = src[c];
+      for (int c = 0; c < IN_BYTES / 2; ++c) raw[which][p][c] = __builtin_nontemporal_load(src + c);
     }
   }
   const int32_t slot = __builtin_amdgcn_readfirstlane(slot_mapping[token]);
@@ -259,13 +265,13 @@ kv_store_token_kernel(const char* __restrict__ key, const char* __restrict__ val
         if (sub == 0) {
           const __amdgpu_buffer_rsrc_t scale_row =
               buffer_over((which ? v_scale : k_scale) + row_slot * H, valid ? kScaleBytes : 0u);
-          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(s), scale_row, head * 4, 0, 0);
+          __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(s), scale_row, head * 4, 0, kNtPolicy);
         }
       } else {
         packed[0] = fp8_encode4(x[0], x[1], x[2], x[3]);
         packed[1] = fp8_encode4(x[4], x[5], x[6], x[7]);
       }
-      __builtin_amdgcn_raw_buffer_store_b64(packed, out_row, (p * 64 + lane) * 8, 0, 0);
+      __builtin_amdgcn_raw_buffer_store_b64(packed, out_row, (p * 64 + lane) * 8, 0, kNtPolicy);
     }
   }
 }
