@@ -45,14 +45,31 @@ __global__ void __launch_bounds__(kThreads) clear_words_kernel(uint32_t* __restr
     words[i] = 0u;
 }
 
+// Sources of one wave that fall in the same bitmap word (plans list kept
+// slots in runs, so a wave usually touches two or three words) are OR-ed
+// together first: one atomic per distinct word instead of one per entry.
 __global__ void __launch_bounds__(kThreads)
 mark_sources_kernel(const int64_t* __restrict__ src, int64_t retained, int64_t num_slots,
                     uint32_t* __restrict__ bitmap) {
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < retained;
-       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int64_t s = src[i];
-    if (s < 0 || s >= num_slots) continue;
-    atomicOr(&bitmap[s >> 5], 1u << (s & 31));
+  const int lane = lane_id();
+  const int64_t wave0 = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) - lane;
+  for (int64_t base = wave0; base < retained; base += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t i = base + lane;
+    const int64_t sl = i < retained ? src[i] : -1;
+    const bool valid = sl >= 0 && sl < num_slots;
+    const int64_t w = valid ? (sl >> 5) : -1;
+    const uint32_t bit = valid ? (1u << (sl & 31)) : 0u;
+    uint64_t todo = __builtin_amdgcn_ballot_w64(valid);
+    while (todo != 0) {  // wave-uniform loop
+      const int leader = __builtin_ctzll(todo);
+      const int64_t lw = __shfl(w, leader);
+      const bool mine = valid && w == lw;
+      uint32_t v = mine ? bit : 0u;
+#pragma unroll
+      for (int off = 32; off >= 1; off >>= 1) v |= __shfl_xor(v, off);
+      if (lane == leader) atomicOr(&bitmap[lw], v);
+      todo &= ~__builtin_amdgcn_ballot_w64(mine);
+    }
   }
 }
 
@@ -80,9 +97,8 @@ struct Chunk<4> { using T = uint32_t; };
 template <>
 struct Chunk<1> { using T = uint8_t; };
 
-// MODE 0: direct copy (skip when the hazard flag is set)
-// MODE 1: gather into temp (only when the flag is set)
-// MODE 2: scatter from temp (only when the flag is set)
+// MODE 0: flag clear -> direct copy src -> dst; flag set -> gather src -> temp
+// MODE 2: scatter temp -> dst (only when the flag is set)
 //
 // Grid (x: chunk ranges, y: rows).  Chunk c of a row is part c & (U - 1) of
 // entry c >> USHIFT when a row vector holds U = 2^USHIFT chunks (every
@@ -97,7 +113,7 @@ compact_move_kernel(uint8_t* __restrict__ cache, int64_t num_slots, int64_t vec_
                     uint8_t* __restrict__ temp, const uint32_t* __restrict__ flag) {
   using T = typename Chunk<BYTES>::T;
   const bool staged = *flag != 0u;
-  if ((MODE == 0) == staged) return;
+  if (MODE == 2 && !staged) return;
   const int64_t chunks_per_vec = vec_bytes / BYTES;
   const int64_t per_row = retained * chunks_per_vec;
   const int64_t row = blockIdx.y;
@@ -128,10 +144,8 @@ compact_move_kernel(uint8_t* __restrict__ cache, int64_t num_slots, int64_t vec_
       const T* from;
       if (MODE == 0) {
         from = reinterpret_cast<const T*>(cache + (row_base + s) * vec_bytes) + part;
-        to[u] = reinterpret_cast<T*>(cache + (row_base + d) * vec_bytes) + part;
-      } else if (MODE == 1) {
-        from = reinterpret_cast<const T*>(cache + (row_base + s) * vec_bytes) + part;
-        to[u] = reinterpret_cast<T*>(temp + item * vec_bytes) + part;
+        to[u] = staged ? reinterpret_cast<T*>(temp + item * vec_bytes) + part
+                       : reinterpret_cast<T*>(cache + (row_base + d) * vec_bytes) + part;
       } else {
         from = reinterpret_cast<const T*>(temp + item * vec_bytes) + part;
         to[u] = reinterpret_cast<T*>(cache + (row_base + d) * vec_bytes) + part;
@@ -172,17 +186,7 @@ int launch_moves(uint8_t* cache, int64_t rows, int64_t num_slots, int64_t vec_by
     const dim3 grid(gx, static_cast<unsigned>(nr));
     hipLaunchKernelGGL((compact_move_kernel<BYTES, 0>), grid, dim3(kThreads), 0, stream, c, num_slots, vec_bytes,
                        ushift, src, dst, retained, t, flag);
-    int rc = check_launch("compact direct copy launch");
-    if (rc) return rc;
-  }
-  for (int64_t r0 = 0; r0 < rows; r0 += 65535) {
-    const int64_t nr = std::min<int64_t>(rows - r0, 65535);
-    uint8_t* c = cache + r0 * num_slots * vec_bytes;
-    uint8_t* t = temp + r0 * retained * vec_bytes;
-    const dim3 grid(gx, static_cast<unsigned>(nr));
-    hipLaunchKernelGGL((compact_move_kernel<BYTES, 1>), grid, dim3(kThreads), 0, stream, c, num_slots, vec_bytes,
-                       ushift, src, dst, retained, t, flag);
-    int rc = check_launch("compact gather launch");
+    int rc = check_launch("compact copy/gather launch");
     if (rc) return rc;
   }
   for (int64_t r0 = 0; r0 < rows; r0 += 65535) {
