@@ -460,13 +460,25 @@ __global__ void __launch_bounds__(64) paged_decode_combine_kernel(const DecodeAr
   }
 #pragma unroll
   for (int off = 32; off >= 1; off >>= 1) l_sum += __shfl_xor(l_sum, off);
+  // eight partials per trip, all their loads issued before the first use
   float o0 = 0.f, o1 = 0.f;
-  for (int s = 0; s < nsplit; ++s) {
-    const int64_t r = row0 + static_cast<int64_t>(s) * a.num_heads;
-    const float w = exp2f(a.part_ml[r * 2] - m_use);
-    const float* src = a.part_acc + r * kHeadDim;
-    o0 += w * src[lane];
-    o1 += w * src[lane + 64];
+  constexpr int kU = 8;
+  for (int s0 = 0; s0 < nsplit; s0 += kU) {
+    float mv[kU], v0[kU], v1[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int s = min(s0 + u, nsplit - 1);
+      const int64_t r = row0 + static_cast<int64_t>(s) * a.num_heads;
+      mv[u] = s0 + u < nsplit ? a.part_ml[r * 2] : -INFINITY;
+      v0[u] = a.part_acc[r * kHeadDim + lane];
+      v1[u] = a.part_acc[r * kHeadDim + lane + 64];
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const float w = exp2f(mv[u] - m_use);  // 0 past the last split
+      o0 += w * v0[u];
+      o1 += w * v1[u];
+    }
   }
   const float inv = l_sum > 0.f ? 1.f / l_sum : 0.f;
   const int64_t base = static_cast<int64_t>(b) * a.o_sb + static_cast<int64_t>(hq) * a.o_sh;
