@@ -291,10 +291,16 @@ paged_prefill_kernel(const PrefillArgs a) {
           if constexpr (QDT == PRISM_DTYPE_F16) kop[cc] = fp8x8_to_f16x8(kw[(cc & 1) * 2], kw[(cc & 1) * 2 + 1]);
           else kop[cc] = fp8x8_to_bf16x8(kw[(cc & 1) * 2], kw[(cc & 1) * 2 + 1]);
         }
-        // keys past the context end may hold any bytes: zero them in V
-        uint32_t keep = 0;
+        // keys past the context end may hold any bytes: zero them in V (only
+        // the context's last sub-block can hold such keys; uniform branch)
+        if (key0 + 16 > ctx) {
+          uint32_t keep = 0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) keep |= (key0 + 4 * g + i < ctx) ? (0xFFu << (8 * i)) : 0u;
+          for (int i = 0; i < 4; ++i) keep |= (key0 + 4 * g + i < ctx) ? (0xFFu << (8 * i)) : 0u;
+          const uint64_t keep2 = static_cast<uint64_t>(keep) | (static_cast<uint64_t>(keep) << 32);
+#pragma unroll
+          for (int jp = 0; jp < 4; ++jp) vt[jp] &= keep2;
+        }
         const float vmax4 = fmaxf(fmaxf(vsv[0], vsv[1]), fmaxf(vsv[2], vsv[3]));
         int vexp = 0;  // wave-uniform power-of-two shift of P * v_scale
         if (__builtin_amdgcn_ballot_w64(vmax4 > kPfF16MaxVScale) != 0) {
@@ -306,8 +312,8 @@ paged_prefill_kernel(const PrefillArgs a) {
         f16x4 vb[8];
 #pragma unroll
         for (int jp = 0; jp < 4; ++jp) {
-          vb[2 * jp] = fp8x4_to_f16x4(static_cast<uint32_t>(vt[jp]) & keep);
-          vb[2 * jp + 1] = fp8x4_to_f16x4(static_cast<uint32_t>(vt[jp] >> 32) & keep);
+          vb[2 * jp] = fp8x4_to_f16x4(static_cast<uint32_t>(vt[jp]));
+          vb[2 * jp + 1] = fp8x4_to_f16x4(static_cast<uint32_t>(vt[jp] >> 32));
         }
 #pragma unroll
         for (int cb = 0; cb < kPfColBlocks; ++cb) {
@@ -321,21 +327,24 @@ paged_prefill_kernel(const PrefillArgs a) {
               sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[cc], qop[cb].op[cc], sc, 0, 0, 0);
           }
           // causal mask: key key0 + 4g + i is visible to column c iff it is
-          // at or before the query's position
-          const int qpos = qpos0 + cb * kPfCols + c;
+          // at or before the query's position.  Sub-blocks wholly below the
+          // diagonal of the column block need no mask (uniform branch); columns
+          // without a query hold q = 0 there, so their scores stay finite and
+          // their rows are never written.
           float x[4];
-          float tmax = -INFINITY;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const bool vis = colv[cb] && key0 + 4 * g + i <= qpos;
-            x[i] = vis ? (sca[i] + scb[i]) * (ksv[i] * a.scale_log2) : -INFINITY;
-            tmax = fmaxf(tmax, x[i]);
+          for (int i = 0; i < 4; ++i) x[i] = (sca[i] + scb[i]) * (ksv[i] * a.scale_log2);
+          if (key0 + 15 > qpos0 + cb * kPfCols) {
+            const int qpos = qpos0 + cb * kPfCols + c;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[i] = (colv[cb] && key0 + 4 * g + i <= qpos) ? x[i] : -INFINITY;
           }
+          float tmax = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
           tmax = wave_max_across_groups(tmax);
           const bool raise = tmax > m_run[cb] + kPfRescaleThreshold;
           if (__builtin_amdgcn_ballot_w64(raise) != 0) {
             const float m_new = raise ? tmax : m_run[cb];
-            const float alpha = raise ? exp2f(m_run[cb] - m_new) : 1.f;
+            const float alpha = raise ? __builtin_amdgcn_exp2f(m_run[cb] - m_new) : 1.f;
             m_run[cb] = m_new;
             l_run[cb] *= alpha;
 #pragma unroll
@@ -349,7 +358,9 @@ paged_prefill_kernel(const PrefillArgs a) {
           float pv[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float p = exp2f(x[i] - m_use);  // 0 where masked
+            // v_exp_f32: arguments are at most 2^3 above the running max;
+            // results below 2^-126 (flushed to 0) weigh nothing next to it
+            const float p = __builtin_amdgcn_exp2f(x[i] - m_use);  // 0 where masked
             l_run[cb] += p;
             pv[i] = p * vsv[i];
           }
