@@ -38,6 +38,8 @@ METRIC = "paged-decode achieved HBM GB/s (% of peak) + µs/layer, batch 64 mixed
 HBM_PEAK_GBPS = 8000.0
 MFMA_BF16_PEAK = 2.5e15  # dense bf16/fp16 MFMA, FLOP/s
 TRAFFIC_FILE = REPO_ROOT / "profiles" / "decode_mixed_traffic.json"
+# config 5's decode pool: ~120 GB of scaled-FP8 pages (256 x 128 of them are used)
+LONG_POOL_PAGES = 221_946
 
 
 def _log(msg: str) -> None:
@@ -328,6 +330,17 @@ def _extras(torch, dev, workloads) -> dict:
                                 "GBps": round(layers[0].algorithmic_bytes() / s / 1e9, 1),
                                 "timing": "36 layers back to back, queued behind a spin, cold"}
     del layers
+    # long-context decode (config 5): B = 256 at 32k tokens each, pages scattered in a ~120 GB pool
+    lw = workloads.decode_long(dev, pool_pages=LONG_POOL_PAGES)
+    s = _time_queued(lambda i: paged_decode_attention(
+        lw.q, lw.k_cache, lw.v_cache, lw.block_tables, lw.context_lens, lw.scale, k_scale_cache=lw.k_scale,
+        v_scale_cache=lw.v_scale, max_context_len=lw.max_context_len), 3, torch, flush=flush)
+    pool_bytes = sum(t.numel() * t.element_size() for t in (lw.k_cache, lw.v_cache, lw.k_scale, lw.v_scale))
+    out["decode_long_b256"] = {"us": round(s * 1e6, 1), "GBps": round(lw.algorithmic_bytes() / s / 1e9, 1),
+                               "pct_of_hbm_peak": round(100.0 * lw.algorithmic_bytes() / s / 1e9 / HBM_PEAK_GBPS, 2),
+                               "bytes": lw.algorithmic_bytes(), "pool_GB": round(pool_bytes / 1e9, 1),
+                               "timing": "3 calls back to back, queued behind a spin, cold"}
+    del lw
     # paged prefill: 4 sequences x (8192 cached + 2048 new tokens), causal
     from types import SimpleNamespace  # noqa: PLC0415
 

@@ -222,6 +222,36 @@ def test_mixed_batch_north_star_config(decode_path):
     assert_decode_close(out, want, label="decode_mixed")
 
 
+def test_long_context_b256_config(monkeypatch):
+    """Config 5's decode at full shape: B=256, 32k tokens each, pages scattered in the pool.
+
+    Both kernel families on every sequence, agreeing within the decode
+    tolerance, and the CPU oracle on a sample of sequences (copied pages only).
+    """
+
+    require_gpu()
+    from prism_infer.ops.paged_decode import paged_decode_attention
+    from prism_infer.workloads import decode_long
+
+    w = decode_long(torch.device("cuda"))
+    run = lambda: paged_decode_attention(w.q, w.k_cache, w.v_cache, w.block_tables, w.context_lens, w.scale,
+                                         k_scale_cache=w.k_scale, v_scale_cache=w.v_scale,
+                                         max_context_len=w.max_context_len)
+    monkeypatch.setenv("PRISM_DECODE_PATH", "stream")
+    out_stream = run()
+    monkeypatch.setenv("PRISM_DECODE_PATH", "split")
+    out_split = run()
+    torch.cuda.synchronize()
+    assert_decode_close(out_stream, out_split, label="decode_long stream vs split")
+    rows = torch.tensor([0, 97, 255])
+    pages = torch.unique(w.block_tables[rows.to(w.block_tables.device)].cpu().to(torch.int64))
+    q, k, v, ks, vs, tables, lens, mx = compact_to_cpu(w, page_ids=pages)
+    want = oracle.decode_kernel_semantics(q[rows], k, v, tables[rows], lens[rows], w.scale, k_scale_cache=ks,
+                                          v_scale_cache=vs, max_context_len=mx, compute_dtype=torch.float32)
+    assert_decode_close(out_stream[rows.to(out_stream.device)], want, label="decode_long sample (stream)")
+    assert_decode_close(out_split[rows.to(out_split.device)], want, label="decode_long sample (split)")
+
+
 def test_page_permutation_invariance_on_gpu():
     """Same logical K/V in different physical pages gives the same output bit for bit."""
 
