@@ -830,7 +830,11 @@ constexpr int kPlanWgTime = kPlanVrot + kSMaxVirt;         // measurement aid: p
 // Key of the plan: everything the plan is computed from.  A call whose
 // inputs equal the key left by the previous call on the same workspace keeps
 // that plan (every layer of a decode step has the same metadata).
-constexpr int kPlanKey = kPlanWgTime + 2 * kSMaxWg;
+// Per real sequence b, 8 ints at kPlanRec + 8 b: first and end tile of its
+// own stream entry, its virtual slot (or -1), and first and end tile of its
+// virtual sequence: what the merge needs, at an offset independent of V.
+constexpr int kPlanRec = kPlanWgTime + 2 * kSMaxWg;
+constexpr int kPlanKey = kPlanRec + 8 * kSMaxBatch;
 constexpr int kPlanKeyParams = 12;
 constexpr int kPlanKeyEff = kPlanKey + kPlanKeyParams;       // attended lengths
 constexpr int kPlanKeyBt = kPlanKeyEff + kSMaxBatch;         // compared block-table prefix
@@ -1103,6 +1107,11 @@ __global__ void __launch_bounds__(kPlanThreads) paged_decode_stream_plan_kernel(
   if (tid < B) {
     plan[kPlanSkip + tid] = skip_s[tid];
     plan[kPlanVslot + tid] = vslot_s[tid];
+    const int vs = vslot_s[tid];
+    const int v = vs >= 0 ? vs / kSCols : 0;
+    int4* rec = reinterpret_cast<int4*>(plan + kPlanRec + 8 * tid);
+    rec[0] = int4{tst_s[V + tid], tst_s[V + tid + 1], vs, vs >= 0 ? tst_s[v] : 0};
+    rec[1] = int4{vs >= 0 ? tst_s[v + 1] : 0, 0, 0, 0};
   }
   for (int i = tid; i < V * kSCols; i += kPlanThreads) plan[kPlanVmem + i] = vmem_s[i];
   if (tid < V) {
@@ -1454,24 +1463,21 @@ paged_decode_stream_kernel(const DecodeArgs a) {
 // Merge the streaming partials: grid (batch, num_heads), one wave each.
 // A sequence's partials come from the workgroups whose tile ranges meet its
 // own tiles (its private tail) and, when it belongs to a virtual sequence,
-// from those that walked its shared pages.  Lane i reads the (m, l) of
-// candidate i (+64k); candidates that wrote a partial are compacted into
-// LDS, then every lane accumulates two output dims.
+// from those that walked its shared pages.  Every such (workgroup, entry)
+// pair wrote a partial (m = -inf when nothing was attended), so candidates
+// are enumerated by arithmetic and their (m, l) and accumulators are loaded
+// together, eight candidates per trip, with a running max: two rounds of
+// dependent loads (the sequence's plan record, then the partials).
 template <int QDT>
 __global__ void __launch_bounds__(64) paged_decode_stream_combine_kernel(const DecodeArgs a) {
-  // the tail's and the virtual sequence's tile ranges are disjoint, so at
-  // most one workgroup meets both: at most nwg + 1 candidates
-  __shared__ float m_s[kSMaxWg + 1];
-  __shared__ float l_s[kSMaxWg + 1];
-  __shared__ int rows[kSMaxWg + 1];
   const int b = blockIdx.x;
   const int hq = blockIdx.y;
   const int lane = threadIdx.x;
+  const int4 r0 = *reinterpret_cast<const int4*>(a.plan + kPlanRec + 8 * b);
+  const int vend = a.plan[kPlanRec + 8 * b + 4];
   const int V = ld_meta(a.plan);
   const StreamSplit sp = stream_split(a, ld_meta(a.plan + 1));
-  const int first = ld_meta(a.plan + kPlanTstart + V + b);
-  const int end = ld_meta(a.plan + kPlanTstart + V + b + 1);
-  const int vslot = ld_meta(a.plan + kPlanVslot + b);
+  const int first = r0.x, end = r0.y, vslot = r0.z, vfirst = r0.w;
   int lo0 = 0, cnt0 = 0, lo1 = 0, cnt1 = 0;
   if (end > first) {
     lo0 = static_cast<int>(split_owner(sp, first));
@@ -1485,50 +1491,52 @@ __global__ void __launch_bounds__(64) paged_decode_stream_combine_kernel(const D
     const int m = vslot - v * kSCols;
     const int hk = hq / a.groups;
     rbase1 = a.vrow0 + (static_cast<int64_t>(v) * kSKv + hk) * kSCols + m * a.groups + (hq - hk * a.groups);
-    const int vfirst = ld_meta(a.plan + kPlanTstart + v);
-    const int vend = ld_meta(a.plan + kPlanTstart + v + 1);
     lo1 = static_cast<int>(split_owner(sp, vfirst));
     cnt1 = static_cast<int>(split_owner(sp, vend - 1)) - lo1 + 1;
   }
   const int cnt = cnt0 + cnt1;
-  int nvalid = 0;
-  float m_max = -INFINITY;
-  for (int base = 0; base < cnt; base += 64) {
-    const int i = base + lane;
-    const bool second = i >= cnt0;
-    const int64_t w = second ? lo1 + (i - cnt0) : lo0 + i;
-    bool ok = i < cnt && split_begin(sp, w) < split_begin(sp, w + 1);
-    const int64_t row = second ? rbase1 + w * (kSKv * kSCols) : rbase0 + w * a.num_heads;
-    float2 ml = {-INFINITY, 0.f};
-    if (ok) ml = *reinterpret_cast<const float2*>(a.part_ml + row * 2);
-    ok = ok && ml.x != -INFINITY;  // a partial with nothing attended weighs 0
-    const uint64_t mask = __builtin_amdgcn_ballot_w64(ok);
-    const int pos = nvalid + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
-                                                       __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0));
-    if (ok) {
-      m_s[pos] = ml.x;
-      l_s[pos] = ml.y;
-      rows[pos] = static_cast<int>(row);
-      m_max = fmaxf(m_max, ml.x);
-    }
-    nvalid += __builtin_popcountll(mask);
-  }
+  constexpr int kU = 8;
+  float m_run = -INFINITY, l_sum = 0.f, o0 = 0.f, o1 = 0.f;
+  for (int base = 0; base < cnt; base += kU) {
+    float mv[kU], lv[kU], v0[kU], v1[kU];
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) m_max = fmaxf(m_max, __shfl_xor(m_max, off));
-  __syncthreads();
-  float l_sum = 0.f, o0 = 0.f, o1 = 0.f;
-#pragma unroll 4
-  for (int i = 0; i < nvalid; ++i) {
-    const float wgt = exp2f(m_s[i] - m_max);
-    const float* src = a.part_acc + static_cast<int64_t>(rows[i]) * kHeadDim;
-    l_sum += wgt * l_s[i];
-    o0 += wgt * src[lane];
-    o1 += wgt * src[lane + 64];
+    for (int u = 0; u < kU; ++u) {
+      const int i = min(base + u, cnt - 1);
+      const bool second = i >= cnt0;
+      const int64_t w = second ? lo1 + (i - cnt0) : lo0 + i;
+      const int64_t row = second ? rbase1 + w * (kSKv * kSCols) : rbase0 + w * a.num_heads;
+      // a workgroup with an empty range (fewer tiles than workgroups) wrote
+      // nothing: its row is never read into the sums
+      const bool ok = base + u < cnt && split_begin(sp, w) < split_begin(sp, w + 1);
+      const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + row * 2);
+      const float x0 = a.part_acc[row * kHeadDim + lane];
+      const float x1 = a.part_acc[row * kHeadDim + lane + 64];
+      mv[u] = ok ? ml.x : -INFINITY;  // -inf: weighs nothing
+      lv[u] = ok ? ml.y : 0.f;
+      v0[u] = ok ? x0 : 0.f;
+      v1[u] = ok ? x1 : 0.f;
+    }
+    float mx = m_run;
+#pragma unroll
+    for (int u = 0; u < kU; ++u) mx = fmaxf(mx, mv[u]);
+    if (mx == -INFINITY) continue;  // nothing attended so far (uniform)
+    const float alpha = exp2f(m_run - mx);  // 0 when m_run = -inf
+    l_sum *= alpha;
+    o0 *= alpha;
+    o1 *= alpha;
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const float wgt = mv[u] == -INFINITY ? 0.f : exp2f(mv[u] - mx);  // rows with m = -inf hold zeros
+      l_sum += wgt * lv[u];
+      o0 += wgt * v0[u];
+      o1 += wgt * v1[u];
+    }
+    m_run = mx;
   }
   const float inv = l_sum > 0.f ? 1.f / l_sum : 0.f;
-  const int64_t base = static_cast<int64_t>(b) * a.o_sb + static_cast<int64_t>(hq) * a.o_sh;
-  store_out<QDT>(a.out, base + lane * a.o_sd, o0 * inv);
-  store_out<QDT>(a.out, base + (lane + 64) * a.o_sd, o1 * inv);
+  const int64_t obase = static_cast<int64_t>(b) * a.o_sb + static_cast<int64_t>(hq) * a.o_sh;
+  store_out<QDT>(a.out, obase + lane * a.o_sd, o0 * inv);
+  store_out<QDT>(a.out, obase + (lane + 64) * a.o_sd, o1 * inv);
 }
 
 // ---------------------------------------------------------------- generic path
