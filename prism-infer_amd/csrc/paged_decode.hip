@@ -1465,11 +1465,17 @@ paged_decode_stream_kernel(const DecodeArgs a) {
 // own tiles (its private tail) and, when it belongs to a virtual sequence,
 // from those that walked its shared pages.  Every such (workgroup, entry)
 // pair wrote a partial (m = -inf when nothing was attended), so candidates
-// are enumerated by arithmetic and their (m, l) and accumulators are loaded
-// together, eight candidates per trip, with a running max: two rounds of
-// dependent loads (the sequence's plan record, then the partials).
+// are enumerated by arithmetic.  Up to eight candidates (the usual case) have
+// their (m, l) and accumulators loaded together: two rounds of dependent
+// loads (the sequence's plan record, then the partials).  More candidates
+// are read lane-parallel first.
 template <int QDT>
 __global__ void __launch_bounds__(64) paged_decode_stream_combine_kernel(const DecodeArgs a) {
+  // the tail's and the virtual sequence's tile ranges are disjoint, so at
+  // most one workgroup meets both: at most nwg + 1 candidates
+  __shared__ float m_s[kSMaxWg + 1];
+  __shared__ float l_s[kSMaxWg + 1];
+  __shared__ int rows[kSMaxWg + 1];
   const int b = blockIdx.x;
   const int hq = blockIdx.y;
   const int lane = threadIdx.x;
@@ -1495,43 +1501,86 @@ __global__ void __launch_bounds__(64) paged_decode_stream_combine_kernel(const D
     cnt1 = static_cast<int>(split_owner(sp, vend - 1)) - lo1 + 1;
   }
   const int cnt = cnt0 + cnt1;
-  constexpr int kU = 8;
-  float m_run = -INFINITY, l_sum = 0.f, o0 = 0.f, o1 = 0.f;
-  for (int base = 0; base < cnt; base += kU) {
-    float mv[kU], lv[kU], v0[kU], v1[kU];
+  float l_sum = 0.f, o0 = 0.f, o1 = 0.f;
+  if (cnt <= 8) {  // (uniform) a few candidates: their loads in one round
+    constexpr int kU = 8;
+    float m_run = -INFINITY;
+    for (int base = 0; base < cnt; base += kU) {
+      float mv[kU], lv[kU], v0[kU], v1[kU];
 #pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      const int i = min(base + u, cnt - 1);
+      for (int u = 0; u < kU; ++u) {
+        const int i = min(base + u, cnt - 1);
+        const bool second = i >= cnt0;
+        const int64_t w = second ? lo1 + (i - cnt0) : lo0 + i;
+        const int64_t row = second ? rbase1 + w * (kSKv * kSCols) : rbase0 + w * a.num_heads;
+        // a workgroup with an empty range (fewer tiles than workgroups) wrote
+        // nothing: its row is never read into the sums
+        const bool ok = base + u < cnt && split_begin(sp, w) < split_begin(sp, w + 1);
+        const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + row * 2);
+        const float x0 = a.part_acc[row * kHeadDim + lane];
+        const float x1 = a.part_acc[row * kHeadDim + lane + 64];
+        mv[u] = ok ? ml.x : -INFINITY;  // -inf: weighs nothing
+        lv[u] = ok ? ml.y : 0.f;
+        v0[u] = ok ? x0 : 0.f;
+        v1[u] = ok ? x1 : 0.f;
+      }
+      float mx = m_run;
+#pragma unroll
+      for (int u = 0; u < kU; ++u) mx = fmaxf(mx, mv[u]);
+      if (mx == -INFINITY) continue;  // nothing attended so far (uniform)
+      const float alpha = exp2f(m_run - mx);  // 0 when m_run = -inf
+      l_sum *= alpha;
+      o0 *= alpha;
+      o1 *= alpha;
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const float wgt = mv[u] == -INFINITY ? 0.f : exp2f(mv[u] - mx);  // rows with m = -inf hold zeros
+        l_sum += wgt * lv[u];
+        o0 += wgt * v0[u];
+        o1 += wgt * v1[u];
+      }
+      m_run = mx;
+    }
+  } else {
+    // many candidates (a long sequence over few others): lane i reads the
+    // (m, l) of candidate i (+64k), those that attended something are
+    // compacted into LDS, then every lane accumulates two output dims
+    int nvalid = 0;
+    float m_max = -INFINITY;
+    for (int base = 0; base < cnt; base += 64) {
+      const int i = base + lane;
       const bool second = i >= cnt0;
       const int64_t w = second ? lo1 + (i - cnt0) : lo0 + i;
+      bool ok = i < cnt && split_begin(sp, w) < split_begin(sp, w + 1);
       const int64_t row = second ? rbase1 + w * (kSKv * kSCols) : rbase0 + w * a.num_heads;
-      // a workgroup with an empty range (fewer tiles than workgroups) wrote
-      // nothing: its row is never read into the sums
-      const bool ok = base + u < cnt && split_begin(sp, w) < split_begin(sp, w + 1);
-      const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + row * 2);
-      const float x0 = a.part_acc[row * kHeadDim + lane];
-      const float x1 = a.part_acc[row * kHeadDim + lane + 64];
-      mv[u] = ok ? ml.x : -INFINITY;  // -inf: weighs nothing
-      lv[u] = ok ? ml.y : 0.f;
-      v0[u] = ok ? x0 : 0.f;
-      v1[u] = ok ? x1 : 0.f;
+      float2 ml = {-INFINITY, 0.f};
+      if (ok) ml = *reinterpret_cast<const float2*>(a.part_ml + row * 2);
+      ok = ok && ml.x != -INFINITY;  // a partial with nothing attended weighs 0
+      const uint64_t mask = __builtin_amdgcn_ballot_w64(ok);
+      const int pos = nvalid + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
+                                                         __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0));
+      if (ok) {
+        m_s[pos] = ml.x;
+        l_s[pos] = ml.y;
+        rows[pos] = static_cast<int>(row);
+        m_max = fmaxf(m_max, ml.x);
+      }
+      nvalid += __builtin_popcountll(mask);
     }
-    float mx = m_run;
 #pragma unroll
-    for (int u = 0; u < kU; ++u) mx = fmaxf(mx, mv[u]);
-    if (mx == -INFINITY) continue;  // nothing attended so far (uniform)
-    const float alpha = exp2f(m_run - mx);  // 0 when m_run = -inf
-    l_sum *= alpha;
-    o0 *= alpha;
-    o1 *= alpha;
-#pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      const float wgt = mv[u] == -INFINITY ? 0.f : exp2f(mv[u] - mx);  // rows with m = -inf hold zeros
-      l_sum += wgt * lv[u];
-      o0 += wgt * v0[u];
-      o1 += wgt * v1[u];
+    for (int off = 32; off >= 1; off >>= 1) m_max = fmaxf(m_max, __shfl_xor(m_max, off));
+    __syncthreads();
+    l_sum = 0.f;
+    o0 = 0.f;
+    o1 = 0.f;
+#pragma unroll 4
+    for (int i = 0; i < nvalid; ++i) {
+      const float wgt = exp2f(m_s[i] - m_max);
+      const float* src = a.part_acc + static_cast<int64_t>(rows[i]) * kHeadDim;
+      l_sum += wgt * l_s[i];
+      o0 += wgt * src[lane];
+      o1 += wgt * src[lane + 64];
     }
-    m_run = mx;
   }
   const float inv = l_sum > 0.f ? 1.f / l_sum : 0.f;
   const int64_t obase = static_cast<int64_t>(b) * a.o_sb + static_cast<int64_t>(hq) * a.o_sh;
