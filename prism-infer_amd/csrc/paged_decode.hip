@@ -934,6 +934,18 @@ __global__ void __launch_bounds__(kPlanThreads) paged_decode_stream_plan_kernel(
                                           static_cast<int>(a.num_blocks & 0x7FFFFFFF),
                                           static_cast<int>(a.num_blocks >> 31), share ? 1 : 0, a.stream_nwg,
                                           0, 0, 0};
+  // The compared block-table prefix: its first eight loads per thread go out
+  // before anything is compared, so the whole check is one round of loads.
+  const int items = share ? B * Wc : 0;
+  int val0[8], old0[8];
+#pragma unroll
+  for (int u = 0; u < 8; ++u) {
+    const int idx = u * kPlanThreads + tid;
+    const int b = idx / Wc;
+    const int j = idx - b * Wc;
+    val0[u] = idx < items ? a.bt[static_cast<int64_t>(b) * a.bt_sb + static_cast<int64_t>(j) * a.bt_sn] : -1;
+    old0[u] = idx < items ? key[kPlanKeyBt - kPlanKey + idx] : -1;
+  }
   bool same = true;
   if (tid < kPlanKeyParams - 3) same = key[tid] == key_params[tid];
   if (tid == 0) same = same && key[kPlanKeyParams - 2] == plan[0] && key[kPlanKeyParams - 1] == plan[1];
@@ -953,7 +965,6 @@ __global__ void __launch_bounds__(kPlanThreads) paged_decode_stream_plan_kernel(
   }
   int V = 0;
   stamp(0);
-  const int items = share ? B * Wc : 0;
   // stage the compared block-table prefix, eight loads in flight per thread
   for (int base = 0; base < items; base += 8 * kPlanThreads) {
     int val[8], old[8];
@@ -962,8 +973,13 @@ __global__ void __launch_bounds__(kPlanThreads) paged_decode_stream_plan_kernel(
       const int idx = base + u * kPlanThreads + tid;
       const int b = idx / Wc;
       const int j = idx - b * Wc;
-      val[u] = idx < items ? a.bt[static_cast<int64_t>(b) * a.bt_sb + static_cast<int64_t>(j) * a.bt_sn] : -1;
-      old[u] = idx < items ? key[kPlanKeyBt - kPlanKey + idx] : -1;
+      if (base == 0) {
+        val[u] = val0[u];
+        old[u] = old0[u];
+      } else {
+        val[u] = idx < items ? a.bt[static_cast<int64_t>(b) * a.bt_sb + static_cast<int64_t>(j) * a.bt_sn] : -1;
+        old[u] = idx < items ? key[kPlanKeyBt - kPlanKey + idx] : -1;
+      }
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
