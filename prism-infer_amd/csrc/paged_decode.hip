@@ -834,7 +834,16 @@ constexpr int kPlanWgTime = kPlanVrot + kSMaxVirt;         // measurement aid: p
 // own stream entry, its virtual slot (or -1), and first and end tile of its
 // virtual sequence: what the merge needs, at an offset independent of V.
 constexpr int kPlanRec = kPlanWgTime + 2 * kSMaxWg;
-constexpr int kPlanKey = kPlanRec + 8 * kSMaxBatch;
+// Per streaming workgroup w, 8 ints at kPlanWgRec + 8 w: where its range
+// starts (stream entry, tile within it, the entry's tile count, block-table
+// row, first token, end token, rotation) and the raw block id of its first
+// tile's page (kNoBlock when that page is outside the compared block-table
+// prefix: only pages the plan's key covers may be cached here).  Empty
+// ranges hold entry -1.  The streaming kernel starts from this record
+// instead of searching the prefix sums and reading the entry's metadata.
+constexpr int kPlanWgRec = kPlanRec + 8 * kSMaxBatch;
+constexpr int kNoBlock = INT_MIN;
+constexpr int kPlanKey = kPlanWgRec + 8 * kSMaxWg;
 constexpr int kPlanKeyParams = 12;
 constexpr int kPlanKeyEff = kPlanKey + kPlanKeyParams;       // attended lengths
 constexpr int kPlanKeyBt = kPlanKeyEff + kSMaxBatch;         // compared block-table prefix
@@ -1141,6 +1150,43 @@ __global__ void __launch_bounds__(kPlanThreads) paged_decode_stream_plan_kernel(
   }
   if (tid < B) plan[kPlanKeyEff + tid] = eff_s[tid];
   for (int i = tid; i < items; i += kPlanThreads) plan[kPlanKeyBt + i] = bt_s[i];
+  for (int w = tid; w < a.stream_nwg; w += kPlanThreads) {
+    const int64_t s0 = static_cast<int64_t>(w) * carry / a.stream_nwg;
+    const int64_t s1 = static_cast<int64_t>(w + 1) * carry / a.stream_nwg;
+    int4 r0 = {-1, 0, 0, 0}, r1 = {0, 0, 0, kNoBlock};
+    if (s0 < s1) {
+      // the entry holding tile s0: the last i with tst_s[i] <= s0
+      int lo = 0, hi = NS - 1;
+      while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (tst_s[mid] <= s0) lo = mid;
+        else hi = mid - 1;
+      }
+      const int i = lo;
+      const int ilt = static_cast<int>(s0 - tst_s[i]);
+      const int intl = tst_s[i + 1] - tst_s[i];
+      int bt_row, tok0, n_end, rot;
+      if (i >= V) {
+        bt_row = i - V;
+        tok0 = skip_s[bt_row];
+        n_end = eff_s[bt_row];
+        rot = 0;
+      } else {
+        bt_row = vsrc_s[i];
+        tok0 = 0;
+        n_end = intl * kSTile;
+        rot = (vk_s[i] * vlen_s[i] / vn_s[i]) * (P / kSTile);
+      }
+      const int lr = ilt + rot;
+      const int t0 = tok0 + (lr >= intl ? lr - intl : lr) * kSTile;
+      const int page = t0 / P;
+      r0 = int4{i, ilt, intl, bt_row};
+      r1 = int4{tok0, n_end, rot, (share && page < Wc) ? bt_s[bt_row * Wc + page] : kNoBlock};
+    }
+    int4* rec = reinterpret_cast<int4*>(plan + kPlanWgRec + 8 * w);
+    rec[0] = r0;
+    rec[1] = r1;
+  }
   stamp(8);
   if (tid == 0) {
     plan[0] = V;
@@ -1199,10 +1245,15 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   const int B = a.batch;
 
   // ---- the plan's tile prefix sums (virtual sequences, then real ones)
+  // one round of loads: this workgroup's start record, the plan header and
+  // the prefix sums (copied up to the largest possible entry count, so that
+  // these loads need not wait for V)
+  const int4 wr0 = *reinterpret_cast<const int4*>(a.plan + kPlanWgRec + 8 * blockIdx.x);
+  const int4 wr1 = *reinterpret_cast<const int4*>(a.plan + kPlanWgRec + 8 * blockIdx.x + 4);
+  for (int i = threadIdx.x; i <= B + kSMaxVirt; i += kSThreads) tstart[i] = a.plan[kPlanTstart + i];
   const int V = ld_meta(a.plan);
   const int NS = B + V;
   const int64_t total = ld_meta(a.plan + 1);
-  for (int i = threadIdx.x; i <= NS; i += kSThreads) tstart[i] = a.plan[kPlanTstart + i];
   const StreamSplit sp = stream_split(a, total);
   const int64_t s = split_begin(sp, blockIdx.x);
   const int64_t e = split_begin(sp, blockIdx.x + 1);
@@ -1216,13 +1267,22 @@ paged_decode_stream_kernel(const DecodeArgs a) {
 
   // ---- issue-side tile iterator: stream entry ib, local tile ilt of intl
   // tiles; the block id is re-read only when the page changes.
-  int ib = 0;
-  advance_seq(tstart, NS, s, ib);
-  int ilt = __builtin_amdgcn_readfirstlane(static_cast<int>(s - tstart[ib]));
-  int intl = __builtin_amdgcn_readfirstlane(tstart[ib + 1] - tstart[ib]);
-  int ibt_row, itok0, iend, irot;
-  stream_seq(a, tstart, V, ib, ibt_row, itok0, iend, irot);
-  int ipage = -1, iblk = 0;
+  int ib = __builtin_amdgcn_readfirstlane(wr0.x);
+  int ilt = __builtin_amdgcn_readfirstlane(wr0.y);
+  int intl = __builtin_amdgcn_readfirstlane(wr0.z);
+  int ibt_row = __builtin_amdgcn_readfirstlane(wr0.w);
+  int itok0 = __builtin_amdgcn_readfirstlane(wr1.x);
+  int iend = __builtin_amdgcn_readfirstlane(wr1.y);
+  int irot = __builtin_amdgcn_readfirstlane(wr1.z);
+  const int first_raw = __builtin_amdgcn_readfirstlane(wr1.w);
+  int first_page;
+  {
+    const int lr = ilt + irot;
+    first_page = (itok0 + (lr >= intl ? lr - intl : lr) * kSTile) / a.page_size;
+  }
+  // the first page's block id comes from the record when the plan could cache it
+  int ipage = first_raw != kNoBlock ? first_page : -1;
+  int iblk = (first_raw >= 0 && first_raw < a.num_blocks) ? first_raw : 0;
   int64_t issued = 0;
   auto issue_next = [&]() {
     const int lr = ilt + irot;
@@ -1253,14 +1313,16 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   for (int i = 0; i < kSStages - 1; ++i)
     if (issued < count) issue_next();
 
-  // ---- compute-side iterator (same walk, one tile behind)
-  int b = 0;
-  advance_seq(tstart, NS, s, b);
-  int lt = __builtin_amdgcn_readfirstlane(static_cast<int>(s - tstart[b]));
-  int ntl = __builtin_amdgcn_readfirstlane(tstart[b + 1] - tstart[b]);
-  int cbt_row, ctok0, n_eff, crot;
-  stream_seq(a, tstart, V, b, cbt_row, ctok0, n_eff, crot);
-  int cpage = -1, cok = 0;
+  // ---- compute-side iterator (same walk, one tile behind), from the same record
+  int b = __builtin_amdgcn_readfirstlane(wr0.x);
+  int lt = __builtin_amdgcn_readfirstlane(wr0.y);
+  int ntl = __builtin_amdgcn_readfirstlane(wr0.z);
+  int cbt_row = __builtin_amdgcn_readfirstlane(wr0.w);
+  int ctok0 = __builtin_amdgcn_readfirstlane(wr1.x);
+  int n_eff = __builtin_amdgcn_readfirstlane(wr1.y);
+  int crot = __builtin_amdgcn_readfirstlane(wr1.z);
+  int cpage = first_raw != kNoBlock ? first_page : -1;
+  int cok = first_raw >= 0 && first_raw < a.num_blocks;
   QOperandF8 qop;
   bool colv;
   {
