@@ -175,13 +175,18 @@ paged_prefill_kernel(const PrefillArgs a) {
     }
   }
 
-  // ---- tile loads: thread chunk ids tid, tid + nthreads, ... of kChunks;
-  // scales by threads < 2 * KT (one float each)
-  constexpr int kMaxPer = (kChunks + nthreads - 1) / nthreads;  // chunks per thread
-  u32x4 pre[kMaxPer];
-  float pre_s = 0.f;
+  // ---- tile loads, straight into LDS (load-to-LDS, 16 B per lane): K then
+  // V as kChunks 16-byte chunks; chunk i of the stage lands at byte 16 i,
+  // i.e. key row i / 8, LDS chunk i % 8, which holds the row's global chunk
+  // (i % 8) ^ swz(row).  Scales: threads 0..2KT-1 one float each.
+  // Asm so that the compiler's wait-count pass does not drain these loads
+  // before each LDS read of the other stage.
+  // (waves past the last chunk or scale issue nothing: the waits below are
+  // vmcnt(0), so waves need not issue equal numbers of loads)
+  static_assert(kChunks % 64 == 0, "whole waves of chunks");
+  constexpr int kPer = (kChunks + nthreads - 1) / nthreads;  // chunks per thread
   bool tile_ok = true;
-  auto load_tile = [&](int t) {
+  auto issue_tile = [&](int t, uint8_t* st) {
     const int tok0 = t * KT;
     const int page = tok0 / a.page;
     const int32_t blk = bt_row[static_cast<int64_t>(page) * a.bt_sn];
@@ -191,44 +196,35 @@ paged_prefill_kernel(const PrefillArgs a) {
       return;
     }
     const int row0 = tok0 - page * a.page;
+    const uint32_t st_lds = lds_addr(st);
 #pragma unroll
-    for (int k = 0; k < kMaxPer; ++k) {
-      const int ch = tid + k * nthreads;
-      if (ch < kChunks) {
-        const int isv = ch >= kChunks / 2;
-        const int cw = ch - isv * (kChunks / 2);
-        const int tok = cw / (kRow / 16);
-        const int part = cw % (kRow / 16);
-        const uint8_t* base = isv ? a.v + blk * a.v_sn + static_cast<int64_t>(row0 + tok) * a.v_sp + h * a.v_sh
-                                  : a.k + blk * a.k_sn + static_cast<int64_t>(row0 + tok) * a.k_sp + h * a.k_sh;
-        pre[k] = *reinterpret_cast<const u32x4*>(base + part * 16);
-      }
+    for (int k = 0; k < kPer; ++k) {
+      const int ch = k * nthreads + tid;  // this lane's chunk; the wave's 64 chunks are contiguous
+      if (ch - lane >= kChunks) break;    // wave-uniform
+      const int isv = ch >= kChunks / 2;
+      const int cw = ch - isv * (kChunks / 2);
+      const int tok = cw / (kRow / 16);
+      const int part = (cw % (kRow / 16)) ^ pf_swz(tok);
+      const uint8_t* src = isv ? a.v + blk * a.v_sn + static_cast<int64_t>(row0 + tok) * a.v_sp + h * a.v_sh
+                               : a.k + blk * a.k_sn + static_cast<int64_t>(row0 + tok) * a.k_sp + h * a.k_sh;
+      src += part * 16;
+      const uint32_t m0 = __builtin_amdgcn_readfirstlane(st_lds + static_cast<uint32_t>(ch - lane) * 16);
+      asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(m0)
+                   : "memory", "m0");
     }
     if constexpr (SCALED) {
-      if (tid < 2 * KT) {
-        const int isv = tid >= KT;
-        const int tok = tid - isv * KT;
-        pre_s = isv ? a.vs[blk * a.vs_sn + static_cast<int64_t>(row0 + tok) * a.vs_sp + h * a.vs_sh]
-                    : a.ks[blk * a.ks_sn + static_cast<int64_t>(row0 + tok) * a.ks_sp + h * a.ks_sh];
-      }
+      const int si = tid;
+      const int isv = si >= KT;
+      const int tok = si - isv * KT;
+      const float* src = isv ? a.vs + blk * a.vs_sn + static_cast<int64_t>(row0 + tok) * a.vs_sp + h * a.vs_sh
+                             : a.ks + blk * a.ks_sn + static_cast<int64_t>(row0 + tok) * a.ks_sp + h * a.ks_sh;
+      const uint32_t m0 = __builtin_amdgcn_readfirstlane(st_lds + 2 * kPayload + static_cast<uint32_t>(si - lane) * 4);
+      if (si < 2 * KT)
+        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" : : "v"(src), "s"(m0)
+                     : "memory", "m0");
     } else {
-      pre_s = 1.f;
+      if (tid < 2 * KT) reinterpret_cast<float*>(st + 2 * kPayload)[tid] = 1.f;
     }
-  };
-  auto store_tile = [&](uint8_t* st) {
-    if (!tile_ok) return;
-#pragma unroll
-    for (int k = 0; k < kMaxPer; ++k) {
-      const int ch = tid + k * nthreads;
-      if (ch < kChunks) {
-        const int isv = ch >= kChunks / 2;
-        const int cw = ch - isv * (kChunks / 2);
-        const int tok = cw / (kRow / 16);
-        const int part = cw % (kRow / 16);
-        *reinterpret_cast<u32x4*>(st + isv * kPayload + tok * kRow + ((part ^ pf_swz(tok)) << 4)) = pre[k];
-      }
-    }
-    if (tid < 2 * KT) reinterpret_cast<float*>(st + 2 * kPayload)[tid] = pre_s;
   };
 
   floatx4 acc[kPfColBlocks][8];
@@ -258,13 +254,19 @@ paged_prefill_kernel(const PrefillArgs a) {
   const uint32_t stage_base = lds_addr(stages);
   const int qpos0 = prefix + qb0;  // position of query column 0 of block 0
 
-  load_tile(0);
-  store_tile(stages);
+  issue_tile(0, stages);
   bool cur_ok = tile_ok;
+  __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0)
   __syncthreads();
   for (int t = 0; t < ntiles; ++t) {
     const bool more = t + 1 < ntiles;
-    if (more) load_tile(t + 1);
+    // the next tile streams into the other stage, last read by tile t - 1,
+    // which every wave finished before the barrier that ended that iteration
+    bool next_ok = true;
+    if (more) {
+      issue_tile(t + 1, stages + ((t + 1) & 1) * kStage);
+      next_ok = tile_ok;
+    }
     const uint32_t soff = static_cast<uint32_t>(t & 1) * kStage;
     const uint8_t* st = stages + soff;
     if (cur_ok) {
@@ -383,12 +385,8 @@ paged_prefill_kernel(const PrefillArgs a) {
         }
       }
     }
-    if (more) {
-      // the other stage was last read while computing tile t - 1, which every
-      // wave finished before the barrier that ended that iteration
-      store_tile(stages + ((t + 1) & 1) * kStage);
-      cur_ok = tile_ok;
-    }
+    cur_ok = next_ok;
+    __builtin_amdgcn_s_waitcnt(0xF70);  // vmcnt(0): this wave's part of tile t + 1 has landed
     __syncthreads();
   }
 
