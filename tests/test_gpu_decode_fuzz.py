@@ -1,0 +1,93 @@
+"""GPU parity: seeded random decode configurations against the CPU oracle.
+
+Each seed draws a geometry and a batch:
+- kv heads 1, 2, 4 or 8 and GQA groups 1, 2, 4 or 8;
+- page sizes 16 to 256;
+- batch sizes 1 to 96, with lengths that are ragged, occasionally zero and
+  occasionally the table's full capacity;
+- holes (-1 block ids) in the tables;
+- groups of sequences sharing leading pages.
+
+It runs every kernel family that accepts the geometry (the automatic choice,
+the streaming kernel, the per-split kernel) and checks each against
+``decode_kernel_semantics`` within the decode tolerance.
+"""
+
+from __future__ import annotations
+
+import math
+
+import pytest
+import torch
+
+import oracle
+from _helpers import assert_decode_close, require_gpu
+
+pytestmark = pytest.mark.gpu
+
+FP8 = torch.float8_e4m3fn
+MAX_POOL_TOKENS = 96 * 1024
+
+
+def _config(seed: int):
+    g = torch.Generator().manual_seed(20261130 + seed)
+    pick = lambda xs: xs[int(torch.randint(len(xs), (1,), generator=g))]
+    hkv = pick([1, 2, 4, 8, 8, 8])
+    groups = pick([1, 2, 4, 4, 8])
+    page = pick([16, 32, 64, 256, 256])
+    batch = int(torch.randint(1, 97, (1,), generator=g))
+    max_len = max(1, min(int(torch.randint(1, 12000, (1,), generator=g)), MAX_POOL_TOKENS // batch - page))
+    width = math.ceil(max_len / page) + 1
+    pool = batch * width + 8
+    lens = torch.randint(0, max_len + 1, (batch,), generator=g, dtype=torch.int32)
+    lens[torch.rand(batch, generator=g) < 0.08] = 0
+    lens[torch.rand(batch, generator=g) < 0.08] = width * page          # the table's full capacity
+    tables = torch.randperm(pool, generator=g)[: batch * width].to(torch.int32).view(batch, width).clone()
+    tables[torch.rand(batch, width, generator=g) < 0.04] = -1           # holes: skipped tokens
+    if batch >= 4 and torch.rand(1, generator=g).item() < 0.6:          # a prefix-sharing group
+        members = torch.randperm(batch, generator=g)[: max(2, batch // 3)]
+        shared = int(torch.randint(1, max(2, width), (1,), generator=g))
+        tables[members, :shared] = tables[members[0], :shared]
+    d = 128
+    q = torch.randn(batch, hkv * groups, d, generator=g).to(torch.bfloat16)
+    src_k = torch.randn(pool, page, hkv, d, generator=g).to(torch.bfloat16)
+    src_v = torch.randn(pool, page, hkv, d, generator=g).to(torch.bfloat16)
+    return q, src_k, src_v, tables, lens
+
+
+def _quantize(src):
+    n, p, h, d = src.shape
+    flat = src.reshape(n * p, h, d)
+    k = torch.zeros(n, p, h, d, dtype=FP8)
+    s = torch.zeros(n, p, h, dtype=torch.float32)
+    oracle.store_scaled(flat, flat, k, torch.zeros_like(k), torch.arange(n * p, dtype=torch.int32), s,
+                        torch.zeros_like(s))
+    return k, s
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_random_decode_configs_all_families(seed, monkeypatch):
+    require_gpu()
+    from prism_infer.ops.paged_decode import paged_decode_attention
+
+    q, src_k, src_v, tables, lens = _config(seed)
+    k, ks = _quantize(src_k)
+    v, vs = _quantize(src_v)
+    scale = 128 ** -0.5
+    want = oracle.decode_kernel_semantics(q, k, v, tables, lens, scale, k_scale_cache=ks, v_scale_cache=vs,
+                                          compute_dtype=torch.float32)
+    dev = torch.device("cuda")
+    to = lambda t: t.view(torch.uint8).to(dev).view(FP8) if t.dtype == FP8 else t.to(dev)
+    args = (to(q), to(k), to(v), to(tables), to(lens), scale)
+    kw = dict(k_scale_cache=to(ks), v_scale_cache=to(vs))
+    label = f"seed {seed}: B={q.shape[0]} Hq={q.shape[1]} Hkv={k.shape[2]} page={k.shape[1]} W={tables.shape[1]}"
+    print(label, flush=True)
+    for path in ("auto", "stream", "split"):
+        if path == "auto":
+            monkeypatch.delenv("PRISM_DECODE_PATH", raising=False)
+        else:
+            monkeypatch.setenv("PRISM_DECODE_PATH", path)
+        got = paged_decode_attention(*args, **kw)
+        torch.cuda.synchronize()
+        assert_decode_close(got, want, label=f"{label} path={path}")
+        assert torch.all(got[lens.to(dev) == 0] == 0), "ctx=0 rows must be zeros"
