@@ -59,9 +59,17 @@ def _torch_lib_dir() -> Path:
     return lib
 
 
+# Per-source extra flags.  The prefill kernel's max reductions run without the
+# IEEE mode's NaN quieting (no operand there is a NaN), which halves their cost.
+EXTRA_FLAGS = {
+    "paged_prefill.hip": ["-mno-amdgpu-ieee", "-fno-honor-nans"],
+}
+
+
 def _compile(src: Path) -> Path:
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [_hipcc(), *HIPCC_FLAGS, f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src), "-o", str(obj)]
+    cmd = [_hipcc(), *HIPCC_FLAGS, *EXTRA_FLAGS.get(src.name, []), f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src),
+           "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{proc.stdout}\n{proc.stderr}")

@@ -63,6 +63,14 @@ struct PrefillArgs {
 // 16-key sub-block (spreads the column reads of a sub-block over the banks).
 __device__ __forceinline__ int pf_swz(int t) { return ((2 * t) + ((t & 15) >> 2)) & 7; }
 
+// A wave-uniform pointer, moved to SGPRs.
+__device__ __forceinline__ const uint8_t* uniform_ptr(const uint8_t* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+  return reinterpret_cast<const uint8_t*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 __device__ __forceinline__ void flag_sequence(const PrefillArgs& a, int seq) {
   atomicMin(a.status, seq);
 }
@@ -135,6 +143,9 @@ paged_prefill_kernel(const PrefillArgs a) {
   constexpr int kPayload = KT * kRow;         // K or V payload of a tile
   constexpr int kStage = 2 * kPayload + 2 * KT * 4;
   constexpr int kChunks = 2 * KT * (kRow / 16);  // 16-byte payload chunks per tile (K then V)
+  constexpr int NB = KT >= 32 ? 2 : 1;            // 16-key blocks per softmax step
+  constexpr int kStep = 16 * NB;                  // keys per softmax step
+  using POp = typename std::conditional<NB == 2, f16x8, f16x4>::type;
   __shared__ __attribute__((aligned(16))) uint8_t stages[2 * kStage];
 
   int seq, qblock;
@@ -148,9 +159,10 @@ paged_prefill_kernel(const PrefillArgs a) {
   const int g = lane / 16;
   const int qhead = h * a.groups + wave;
 
-  const int qs = a.cu_q[seq];
-  const int qlen = a.cu_q[seq + 1] - qs;
-  const int ctx = a.ctx[seq];
+  // sequence metadata in SGPRs: every branch on it below is uniform
+  const int qs = __builtin_amdgcn_readfirstlane(a.cu_q[seq]);
+  const int qlen = __builtin_amdgcn_readfirstlane(a.cu_q[seq + 1]) - qs;
+  const int ctx = __builtin_amdgcn_readfirstlane(a.ctx[seq]);
   const int prefix = ctx - qlen;
   const int qb0 = qblock * kPfQTile;                       // first query token of the block
   const int qcount = min(kPfQTile, qlen - qb0);
@@ -197,31 +209,42 @@ paged_prefill_kernel(const PrefillArgs a) {
     }
     const int row0 = tok0 - page * a.page;
     const uint32_t st_lds = lds_addr(st);
+    // every chunk of a wave is in one page and is all K or all V: a uniform
+    // 64-bit base (SGPRs) plus a 32-bit per-lane offset (the host checks
+    // that a page's bytes of one head span less than 2^31)
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
       const int ch = k * nthreads + tid;  // this lane's chunk; the wave's 64 chunks are contiguous
       if (ch - lane >= kChunks) break;    // wave-uniform
-      const int isv = ch >= kChunks / 2;
+      const int isv = (ch - lane) >= kChunks / 2;  // wave-uniform
       const int cw = ch - isv * (kChunks / 2);
       const int tok = cw / (kRow / 16);
       const int part = (cw % (kRow / 16)) ^ pf_swz(tok);
-      const uint8_t* src = isv ? a.v + blk * a.v_sn + static_cast<int64_t>(row0 + tok) * a.v_sp + h * a.v_sh
-                               : a.k + blk * a.k_sn + static_cast<int64_t>(row0 + tok) * a.k_sp + h * a.k_sh;
-      src += part * 16;
+      const uint8_t* base = isv ? a.v + blk * a.v_sn + static_cast<int64_t>(row0) * a.v_sp + h * a.v_sh
+                                : a.k + blk * a.k_sn + static_cast<int64_t>(row0) * a.k_sp + h * a.k_sh;
+      const uint32_t off = static_cast<uint32_t>(tok * static_cast<int>(isv ? a.v_sp : a.k_sp) + part * 16);
       const uint32_t m0 = __builtin_amdgcn_readfirstlane(st_lds + static_cast<uint32_t>(ch - lane) * 16);
-      asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" : : "v"(src), "s"(m0)
-                   : "memory", "m0");
+      asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(off), "s"(uniform_ptr(base)),
+                   "s"(m0) : "memory", "m0");
     }
     if constexpr (SCALED) {
+      // threads 0..KT-1 load the K scales, KT..2KT-1 the V scales (exec-masked
+      // halves of one wave share M0: the LDS address is M0 + 4 * lane)
       const int si = tid;
-      const int isv = si >= KT;
-      const int tok = si - isv * KT;
-      const float* src = isv ? a.vs + blk * a.vs_sn + static_cast<int64_t>(row0 + tok) * a.vs_sp + h * a.vs_sh
-                             : a.ks + blk * a.ks_sn + static_cast<int64_t>(row0 + tok) * a.ks_sp + h * a.ks_sh;
       const uint32_t m0 = __builtin_amdgcn_readfirstlane(st_lds + 2 * kPayload + static_cast<uint32_t>(si - lane) * 4);
-      if (si < 2 * KT)
-        asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dword %0, off" : : "v"(src), "s"(m0)
+      if (si < KT) {
+        const uint8_t* base = uniform_ptr(reinterpret_cast<const uint8_t*>(
+            a.ks + blk * a.ks_sn + static_cast<int64_t>(row0) * a.ks_sp + h * a.ks_sh));
+        const uint32_t off = static_cast<uint32_t>(si * static_cast<int>(a.ks_sp) * 4);
+        asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" : : "v"(off), "s"(base), "s"(m0)
                      : "memory", "m0");
+      } else if (si < 2 * KT) {
+        const uint8_t* base = uniform_ptr(reinterpret_cast<const uint8_t*>(
+            a.vs + blk * a.vs_sn + static_cast<int64_t>(row0) * a.vs_sp + h * a.vs_sh));
+        const uint32_t off = static_cast<uint32_t>((si - KT) * static_cast<int>(a.vs_sp) * 4);
+        asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dword %0, %1" : : "v"(off), "s"(base), "s"(m0)
+                     : "memory", "m0");
+      }
     } else {
       if (tid < 2 * KT) reinterpret_cast<float*>(st + 2 * kPayload)[tid] = 1.f;
     }
@@ -271,39 +294,42 @@ paged_prefill_kernel(const PrefillArgs a) {
     const uint8_t* st = stages + soff;
     if (cur_ok) {
 #pragma unroll 1
-      for (int sb = 0; sb < KT / 16; ++sb) {
-        const int key0 = t * KT + sb * 16;                   // first key of the sub-block
+      for (int sp = 0; sp < KT / kStep; ++sp) {
+        const int key0 = t * KT + sp * kStep;                // first key of the step
         if (key0 > qpos0 + kPfQTile - 1) break;              // above the diagonal for every column
-        const uint8_t* sbp = st + sb * 16 * kRow;
-        const u32x4 k0 = *reinterpret_cast<const u32x4*>(sbp + k_off0);
-        const u32x4 k1 = *reinterpret_cast<const u32x4*>(sbp + k_off1);
-        const float* scl = reinterpret_cast<const float*>(st + 2 * kPayload) + sb * 16 + 4 * g;
-        const floatx4 ksv = *reinterpret_cast<const floatx4*>(scl);
-        const floatx4 vsv = *reinterpret_cast<const floatx4*>(scl + KT);
-        uint32_t ad[4];
+        // per 16-key block b: K rows, scales and the transposed V reads
+        u32x4 kw[NB][2];
+        floatx4 ksv[NB], vsv[NB];
+        uint64_t vt[NB][4];
 #pragma unroll
-        for (int jp = 0; jp < 4; ++jp) ad[jp] = stage_base + soff + sb * 16 * kRow + v_off[jp];
-        uint64_t vt[4];
-        lds_read_tr8_x4(ad, vt);
-        // K operand (A of S^T), shared by the column blocks
-        typename PfQOperand<QDT>::T kop[4];
+        for (int b = 0; b < NB; ++b) {
+          const int sb = sp * NB + b;
+          const uint8_t* sbp = st + sb * 16 * kRow;
+          kw[b][0] = *reinterpret_cast<const u32x4*>(sbp + k_off0);
+          kw[b][1] = *reinterpret_cast<const u32x4*>(sbp + k_off1);
+          const float* scl = reinterpret_cast<const float*>(st + 2 * kPayload) + sb * 16 + 4 * g;
+          ksv[b] = *reinterpret_cast<const floatx4*>(scl);
+          vsv[b] = *reinterpret_cast<const floatx4*>(scl + KT);
+          uint32_t ad[4];
 #pragma unroll
-        for (int cc = 0; cc < 4; ++cc) {
-          const u32x4& kw = (cc < 2) ? k0 : k1;
-          if constexpr (QDT == PRISM_DTYPE_F16) kop[cc] = fp8x8_to_f16x8(kw[(cc & 1) * 2], kw[(cc & 1) * 2 + 1]);
-          else kop[cc] = fp8x8_to_bf16x8(kw[(cc & 1) * 2], kw[(cc & 1) * 2 + 1]);
+          for (int jp = 0; jp < 4; ++jp) ad[jp] = stage_base + soff + sb * 16 * kRow + v_off[jp];
+          lds_read_tr8_x4(ad, vt[b]);
         }
         // keys past the context end may hold any bytes: zero them in V (only
-        // the context's last sub-block can hold such keys; uniform branch)
-        if (key0 + 16 > ctx) {
-          uint32_t keep = 0;
+        // the context's last step can hold such keys; uniform branch)
+        if (key0 + kStep > ctx) {
 #pragma unroll
-          for (int i = 0; i < 4; ++i) keep |= (key0 + 4 * g + i < ctx) ? (0xFFu << (8 * i)) : 0u;
-          const uint64_t keep2 = static_cast<uint64_t>(keep) | (static_cast<uint64_t>(keep) << 32);
+          for (int b = 0; b < NB; ++b) {
+            uint32_t keep = 0;
 #pragma unroll
-          for (int jp = 0; jp < 4; ++jp) vt[jp] &= keep2;
+            for (int i = 0; i < 4; ++i) keep |= (key0 + 16 * b + 4 * g + i < ctx) ? (0xFFu << (8 * i)) : 0u;
+            const uint64_t keep2 = static_cast<uint64_t>(keep) | (static_cast<uint64_t>(keep) << 32);
+#pragma unroll
+            for (int jp = 0; jp < 4; ++jp) vt[b][jp] &= keep2;
+          }
         }
-        const float vmax4 = fmaxf(fmaxf(vsv[0], vsv[1]), fmaxf(vsv[2], vsv[3]));
+        float vmax4 = fmaxf(fmaxf(vsv[0][0], vsv[0][1]), fmaxf(vsv[0][2], vsv[0][3]));
+        if constexpr (NB == 2) vmax4 = fmaxf(vmax4, fmaxf(fmaxf(vsv[1][0], vsv[1][1]), fmaxf(vsv[1][2], vsv[1][3])));
         int vexp = 0;  // wave-uniform power-of-two shift of P * v_scale
         if (__builtin_amdgcn_ballot_w64(vmax4 > kPfF16MaxVScale) != 0) {
           float vmax = vmax4;
@@ -311,37 +337,67 @@ paged_prefill_kernel(const PrefillArgs a) {
           for (int off = 32; off >= 1; off >>= 1) vmax = fmaxf(vmax, __shfl_xor(vmax, off));
           vexp = __builtin_amdgcn_readfirstlane(ilogbf(vmax / kPfF16MaxVScale) + 1);
         }
-        f16x4 vb[8];
+        // per key: k_scale * softmax scale (log2 units), and v_scale with the
+        // tile's power-of-two shift
+        const float down = ldexpf(1.f, -vexp);  // 1 unless the tile's v scales exceed 255
+        floatx4 ksl[NB], vsd[NB];
 #pragma unroll
-        for (int jp = 0; jp < 4; ++jp) {
-          vb[2 * jp] = fp8x4_to_f16x4(static_cast<uint32_t>(vt[jp]));
-          vb[2 * jp + 1] = fp8x4_to_f16x4(static_cast<uint32_t>(vt[jp] >> 32));
+        for (int b = 0; b < NB; ++b) {
+          ksl[b] = ksv[b] * a.scale_log2;
+          vsd[b] = vsv[b] * down;
         }
+        // S^T = K Q^T for both column blocks, one K block at a time (its
+        // operand converted once)
+        floatx4 sc[kPfColBlocks][NB];  // the four per block chained: NB x 2 independent chains
 #pragma unroll
-        for (int cb = 0; cb < kPfColBlocks; ++cb) {
-          floatx4 sca = {0.f, 0.f, 0.f, 0.f}, scb = {0.f, 0.f, 0.f, 0.f};
+        for (int b = 0; b < NB; ++b) {
+          typename PfQOperand<QDT>::T kop[4];
 #pragma unroll
           for (int cc = 0; cc < 4; ++cc) {
-            floatx4& sc = (cc & 1) ? scb : sca;
-            if constexpr (QDT == PRISM_DTYPE_F16)
-              sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[cc], qop[cb].op[cc], sc, 0, 0, 0);
-            else
-              sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[cc], qop[cb].op[cc], sc, 0, 0, 0);
+            const u32x4& w = kw[b][cc >> 1];
+            if constexpr (QDT == PRISM_DTYPE_F16) kop[cc] = fp8x8_to_f16x8(w[(cc & 1) * 2], w[(cc & 1) * 2 + 1]);
+            else kop[cc] = fp8x8_to_bf16x8(w[(cc & 1) * 2], w[(cc & 1) * 2 + 1]);
           }
-          // causal mask: key key0 + 4g + i is visible to column c iff it is
-          // at or before the query's position.  Sub-blocks wholly below the
-          // diagonal of the column block need no mask (uniform branch); columns
-          // without a query hold q = 0 there, so their scores stay finite and
-          // their rows are never written.
-          float x[4];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) x[i] = (sca[i] + scb[i]) * (ksv[i] * a.scale_log2);
-          if (key0 + 15 > qpos0 + cb * kPfCols) {
+          for (int cb = 0; cb < kPfColBlocks; ++cb) {
+            sc[cb][b] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int cc = 0; cc < 4; ++cc) {
+              floatx4& d = sc[cb][b];
+              if constexpr (QDT == PRISM_DTYPE_F16)
+                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[cc], qop[cb].op[cc], d, 0, 0, 0);
+              else
+                d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[cc], qop[cb].op[cc], d, 0, 0, 0);
+            }
+          }
+        }
+        // online softmax per column block -> P (A of O = P V).  One block:
+        // k-slots 4g..4g+3 are keys 4g..4g+3 (16x16x16).  Two blocks: k-slots
+        // 8g..8g+3 are keys 4g..4g+3 of block 0 and 8g+4..8g+7 the same keys
+        // of block 1 (16x16x32), the order the score rows come out in.
+        POp pa[kPfColBlocks];
+#pragma unroll
+        for (int cb = 0; cb < kPfColBlocks; ++cb) {
+          // causal mask: key k is visible to column c iff it is at or before
+          // the query's position.  Steps wholly below the diagonal of the
+          // column block need no mask (uniform branch); columns without a
+          // query hold q = 0 there, so their scores stay finite and their rows
+          // are never written.
+          float x[NB][4];
+#pragma unroll
+          for (int b = 0; b < NB; ++b)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x[b][i] = sc[cb][b][i] * ksl[b][i];
+          if (key0 + kStep - 1 > qpos0 + cb * kPfCols) {
             const int qpos = qpos0 + cb * kPfCols + c;
 #pragma unroll
-            for (int i = 0; i < 4; ++i) x[i] = (colv[cb] && key0 + 4 * g + i <= qpos) ? x[i] : -INFINITY;
+            for (int b = 0; b < NB; ++b)
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+                x[b][i] = (colv[cb] && key0 + 16 * b + 4 * g + i <= qpos) ? x[b][i] : -INFINITY;
           }
-          float tmax = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+          float tmax = fmaxf(fmaxf(x[0][0], x[0][1]), fmaxf(x[0][2], x[0][3]));
+          if constexpr (NB == 2) tmax = fmaxf(tmax, fmaxf(fmaxf(x[1][0], x[1][1]), fmaxf(x[1][2], x[1][3])));
           tmax = wave_max_across_groups(tmax);
           const bool raise = tmax > m_run[cb] + kPfRescaleThreshold;
           if (__builtin_amdgcn_ballot_w64(raise) != 0) {
@@ -357,31 +413,49 @@ paged_prefill_kernel(const PrefillArgs a) {
             }
           }
           const float m_use = (m_run[cb] == -INFINITY) ? 0.f : m_run[cb];
-          float pv[4];
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            // v_exp_f32: arguments are at most 2^3 above the running max;
-            // results below 2^-126 (flushed to 0) weigh nothing next to it
-            const float p = __builtin_amdgcn_exp2f(x[i] - m_use);  // 0 where masked
-            l_run[cb] += p;
-            pv[i] = p * vsv[i];
+          for (int b = 0; b < NB; ++b) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              // v_exp_f32: arguments are at most 2^3 above the running max;
+              // results below 2^-126 (flushed to 0) weigh nothing next to it
+              const float p = __builtin_amdgcn_exp2f(x[b][i] - m_use);  // 0 where masked
+              l_run[cb] += p;
+              pa[cb][4 * b + i] = static_cast<_Float16>(p * vsd[b][i]);
+            }
           }
           if (vexp != 0) {
-            const float down = ldexpf(1.f, -vexp);
 #pragma unroll
             for (int j = 0; j < 8; ++j) acc[cb][j] *= down;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) pv[i] *= down;
           }
-          const f16x4 pa = {static_cast<_Float16>(pv[0]), static_cast<_Float16>(pv[1]),
-                            static_cast<_Float16>(pv[2]), static_cast<_Float16>(pv[3])};
+        }
+        // O += P V: V operand (B) for dims 16 j + c, one N-tile at a time,
+        // shared by the column blocks; k-slots as P's
 #pragma unroll
-          for (int j = 0; j < 8; ++j) acc[cb][j] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, vb[j], acc[cb][j], 0, 0, 0);
-          if (vexp != 0) {
-            const float up = ldexpf(1.f, vexp);
+        for (int jp = 0; jp < 4; ++jp) {
+#pragma unroll
+          for (int hi = 0; hi < 2; ++hi) {
+            const int j = 2 * jp + hi;
+            const f16x4 v0 = fp8x4_to_f16x4(static_cast<uint32_t>(vt[0][jp] >> (32 * hi)));
+            if constexpr (NB == 2) {
+              const f16x4 v1 = fp8x4_to_f16x4(static_cast<uint32_t>(vt[NB - 1][jp] >> (32 * hi)));
+              const f16x8 vb = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+#pragma unroll
+              for (int cb = 0; cb < kPfColBlocks; ++cb)
+                acc[cb][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[cb], vb, acc[cb][j], 0, 0, 0);
+            } else {
+#pragma unroll
+              for (int cb = 0; cb < kPfColBlocks; ++cb)
+                acc[cb][j] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa[cb], v0, acc[cb][j], 0, 0, 0);
+            }
+          }
+        }
+        if (vexp != 0) {
+          const float up = ldexpf(1.f, vexp);
+#pragma unroll
+          for (int cb = 0; cb < kPfColBlocks; ++cb)
 #pragma unroll
             for (int j = 0; j < 8; ++j) acc[cb][j] *= up;
-          }
         }
       }
     }
@@ -430,7 +504,7 @@ template <int QDT, int KT>
 int dispatch_waves(const PrefillArgs& a, bool scaled, int total_q, hipStream_t stream) {
   switch (a.groups) {
     case 1: return launch_prefill<QDT, 16, 1>(a, scaled, total_q, stream);
-    case 2: return launch_prefill<QDT, KT, 2>(a, scaled, total_q, stream);
+    case 2: return launch_prefill<QDT, (KT > 32 ? 32 : KT), 2>(a, scaled, total_q, stream);
     case 4: return launch_prefill<QDT, KT, 4>(a, scaled, total_q, stream);
     case 8: return launch_prefill<QDT, KT, 8>(a, scaled, total_q, stream);
     default:
@@ -500,6 +574,13 @@ extern "C" int prism_paged_prefill(const void* q, int q_dtype, const int64_t q_s
       k_strides[0] % 16 || k_strides[1] % 16 || k_strides[2] % 16 || v_strides[0] % 16 || v_strides[1] % 16 ||
       v_strides[2] % 16) {
     set_error("prism_paged_prefill: q, K/V and out need unit-stride head dims and 16-byte aligned rows");
+    return PRISM_ERR_LAYOUT;
+  }
+  // tile loads address a page's rows of one head by a 32-bit offset
+  if ((page_size - 1) * k_strides[1] + kPfD > INT32_MAX || (page_size - 1) * v_strides[1] + kPfD > INT32_MAX ||
+      (k_scale && ((page_size - 1) * k_scale_strides[1] >= INT32_MAX / 4 ||
+                   (page_size - 1) * v_scale_strides[1] >= INT32_MAX / 4))) {
+    set_error("prism_paged_prefill: a page's token rows must span less than 2 GiB");
     return PRISM_ERR_LAYOUT;
   }
   if (batch == 0 || total_q == 0) return PRISM_OK;
