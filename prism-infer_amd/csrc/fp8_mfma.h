@@ -58,6 +58,27 @@ __device__ __forceinline__ void lds_read_tr8_x4(const uint32_t (&ad)[4], uint64_
       : "memory");
 }
 
+// Eight transposed reads: the four addresses at byte offsets OFF0 and OFF1
+// (immediates), one wait for all of them.
+template <int OFF0, int OFF1>
+__device__ __forceinline__ void lds_read_tr8_x8(const uint32_t (&ad)[4], uint64_t (&o0)[4], uint64_t (&o1)[4]) {
+  static_assert(OFF0 >= 0 && OFF1 >= 0 && OFF0 < 65536 && OFF1 < 65536, "ds offsets are 16-bit");
+  asm volatile(
+      "ds_read_b64_tr_b8 %0, %8 offset:%12\n\t"
+      "ds_read_b64_tr_b8 %1, %9 offset:%12\n\t"
+      "ds_read_b64_tr_b8 %2, %10 offset:%12\n\t"
+      "ds_read_b64_tr_b8 %3, %11 offset:%12\n\t"
+      "ds_read_b64_tr_b8 %4, %8 offset:%13\n\t"
+      "ds_read_b64_tr_b8 %5, %9 offset:%13\n\t"
+      "ds_read_b64_tr_b8 %6, %10 offset:%13\n\t"
+      "ds_read_b64_tr_b8 %7, %11 offset:%13\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(o0[0]), "=&v"(o0[1]), "=&v"(o0[2]), "=&v"(o0[3]), "=&v"(o1[0]), "=&v"(o1[1]), "=&v"(o1[2]),
+        "=&v"(o1[3])
+      : "v"(ad[0]), "v"(ad[1]), "v"(ad[2]), "v"(ad[3]), "i"(OFF0), "i"(OFF1)
+      : "memory");
+}
+
 // Max over the four 16-lane groups (lanes l, l^16, l^32, l^48) with the
 // gfx950 lane-swap instructions (VALU, no LDS round trip).
 __device__ __forceinline__ float wave_max_across_groups(float v) {

@@ -145,6 +145,7 @@ paged_prefill_kernel(const PrefillArgs a) {
   constexpr int kChunks = 2 * KT * (kRow / 16);  // 16-byte payload chunks per tile (K then V)
   constexpr int NB = KT >= 32 ? 2 : 1;            // 16-key blocks per softmax step
   constexpr int kStep = 16 * NB;                  // keys per softmax step
+  static_assert(NB == 1 || KT / kStep <= 2, "the V reads below cover two steps per tile");
   using POp = typename std::conditional<NB == 2, f16x8, f16x4>::type;
   __shared__ __attribute__((aligned(16))) uint8_t stages[2 * kStage];
 
@@ -153,7 +154,7 @@ paged_prefill_kernel(const PrefillArgs a) {
   const int h = blockIdx.y;
   constexpr int nthreads = 64 * NW;
   const int tid = threadIdx.x;
-  const int wave = tid / 64;
+  const int wave = NW == 1 ? 0 : __builtin_amdgcn_readfirstlane(tid / 64);  // uniform: SGPR arithmetic below
   const int lane = tid % 64;
   const int c = lane % 16;
   const int g = lane / 16;
@@ -214,16 +215,17 @@ paged_prefill_kernel(const PrefillArgs a) {
     // that a page's bytes of one head span less than 2^31)
 #pragma unroll
     for (int k = 0; k < kPer; ++k) {
-      const int ch = k * nthreads + tid;  // this lane's chunk; the wave's 64 chunks are contiguous
-      if (ch - lane >= kChunks) break;    // wave-uniform
-      const int isv = (ch - lane) >= kChunks / 2;  // wave-uniform
+      const int ch0 = k * nthreads + wave * 64;  // the wave's first chunk (uniform); 64 contiguous chunks
+      const int ch = ch0 + lane;
+      if (ch0 >= kChunks) break;
+      const int isv = ch0 >= kChunks / 2;
       const int cw = ch - isv * (kChunks / 2);
       const int tok = cw / (kRow / 16);
       const int part = (cw % (kRow / 16)) ^ pf_swz(tok);
       const uint8_t* base = isv ? a.v + blk * a.v_sn + static_cast<int64_t>(row0) * a.v_sp + h * a.v_sh
                                 : a.k + blk * a.k_sn + static_cast<int64_t>(row0) * a.k_sp + h * a.k_sh;
       const uint32_t off = static_cast<uint32_t>(tok * static_cast<int>(isv ? a.v_sp : a.k_sp) + part * 16);
-      const uint32_t m0 = __builtin_amdgcn_readfirstlane(st_lds + static_cast<uint32_t>(ch - lane) * 16);
+      const uint32_t m0 = __builtin_amdgcn_readfirstlane(st_lds + static_cast<uint32_t>(ch0) * 16);
       asm volatile("s_mov_b32 m0, %2\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, %1" : : "v"(off), "s"(uniform_ptr(base)),
                    "s"(m0) : "memory", "m0");
     }
@@ -231,7 +233,7 @@ paged_prefill_kernel(const PrefillArgs a) {
       // threads 0..KT-1 load the K scales, KT..2KT-1 the V scales (exec-masked
       // halves of one wave share M0: the LDS address is M0 + 4 * lane)
       const int si = tid;
-      const uint32_t m0 = __builtin_amdgcn_readfirstlane(st_lds + 2 * kPayload + static_cast<uint32_t>(si - lane) * 4);
+      const uint32_t m0 = __builtin_amdgcn_readfirstlane(st_lds + 2 * kPayload + static_cast<uint32_t>(wave * 64) * 4);
       if (si < KT) {
         const uint8_t* base = uniform_ptr(reinterpret_cast<const uint8_t*>(
             a.ks + blk * a.ks_sn + static_cast<int64_t>(row0) * a.ks_sp + h * a.ks_sh));
@@ -293,7 +295,7 @@ paged_prefill_kernel(const PrefillArgs a) {
     const uint32_t soff = static_cast<uint32_t>(t & 1) * kStage;
     const uint8_t* st = stages + soff;
     if (cur_ok) {
-#pragma unroll 1
+#pragma unroll
       for (int sp = 0; sp < KT / kStep; ++sp) {
         const int key0 = t * KT + sp * kStep;                // first key of the step
         if (key0 > qpos0 + kPfQTile - 1) break;              // above the diagonal for every column
@@ -310,10 +312,19 @@ paged_prefill_kernel(const PrefillArgs a) {
           const float* scl = reinterpret_cast<const float*>(st + 2 * kPayload) + sb * 16 + 4 * g;
           ksv[b] = *reinterpret_cast<const floatx4*>(scl);
           vsv[b] = *reinterpret_cast<const floatx4*>(scl + KT);
+        }
+        {
           uint32_t ad[4];
 #pragma unroll
-          for (int jp = 0; jp < 4; ++jp) ad[jp] = stage_base + soff + sb * 16 * kRow + v_off[jp];
-          lds_read_tr8_x4(ad, vt[b]);
+          for (int jp = 0; jp < 4; ++jp) ad[jp] = stage_base + soff + v_off[jp];
+          if constexpr (NB == 2) {
+            if (sp == 0) lds_read_tr8_x8<0, 16 * kRow>(ad, vt[0], vt[NB - 1]);
+            else lds_read_tr8_x8<2 * 16 * kRow, 3 * 16 * kRow>(ad, vt[0], vt[NB - 1]);
+          } else {
+#pragma unroll
+            for (int jp = 0; jp < 4; ++jp) ad[jp] += sp * 16 * kRow;
+            lds_read_tr8_x4(ad, vt[0]);
+          }
         }
         // keys past the context end may hold any bytes: zero them in V (only
         // the context's last step can hold such keys; uniform branch)
@@ -498,12 +509,12 @@ int launch_prefill(const PrefillArgs& a, bool scaled, int total_q, hipStream_t s
   return check_launch("paged_prefill_kernel launch");
 }
 
-// Key tiles of 64 (pages of a multiple of 64 tokens) or 16; one wave per
-// query head of the GQA group (1, 2, 4 or 8).
+// Key tiles of 64, 32 or 16 keys (the largest dividing the page; at most 32
+// for one or two waves); one wave per query head of the GQA group.
 template <int QDT, int KT>
 int dispatch_waves(const PrefillArgs& a, bool scaled, int total_q, hipStream_t stream) {
   switch (a.groups) {
-    case 1: return launch_prefill<QDT, 16, 1>(a, scaled, total_q, stream);
+    case 1: return launch_prefill<QDT, (KT > 32 ? 32 : KT), 1>(a, scaled, total_q, stream);
     case 2: return launch_prefill<QDT, (KT > 32 ? 32 : KT), 2>(a, scaled, total_q, stream);
     case 4: return launch_prefill<QDT, KT, 4>(a, scaled, total_q, stream);
     case 8: return launch_prefill<QDT, KT, 8>(a, scaled, total_q, stream);
@@ -515,8 +526,9 @@ int dispatch_waves(const PrefillArgs& a, bool scaled, int total_q, hipStream_t s
 
 template <int QDT>
 int dispatch_tile(const PrefillArgs& a, bool scaled, int total_q, hipStream_t stream) {
-  // one wave would hold 16 chunks of a 64-key tile in flight: too many VGPRs
-  if (a.page % 64 == 0 && a.groups > 1) return dispatch_waves<QDT, 64>(a, scaled, total_q, stream);
+  // a tile lies in one page
+  if (a.page % 64 == 0) return dispatch_waves<QDT, 64>(a, scaled, total_q, stream);
+  if (a.page % 32 == 0) return dispatch_waves<QDT, 32>(a, scaled, total_q, stream);
   return dispatch_waves<QDT, 16>(a, scaled, total_q, stream);
 }
 
