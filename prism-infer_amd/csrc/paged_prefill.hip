@@ -386,34 +386,46 @@ paged_prefill_kernel(const PrefillArgs a) {
         // k-slots 4g..4g+3 are keys 4g..4g+3 (16x16x16).  Two blocks: k-slots
         // 8g..8g+3 are keys 4g..4g+3 of block 0 and 8g+4..8g+7 the same keys
         // of block 1 (16x16x32), the order the score rows come out in.
+        // Both column blocks go through each phase together (one branch per
+        // phase), so their dependency chains interleave.
         POp pa[kPfColBlocks];
+        float x[kPfColBlocks][NB][4];
 #pragma unroll
-        for (int cb = 0; cb < kPfColBlocks; ++cb) {
-          // causal mask: key k is visible to column c iff it is at or before
-          // the query's position.  Steps wholly below the diagonal of the
-          // column block need no mask (uniform branch); columns without a
-          // query hold q = 0 there, so their scores stay finite and their rows
-          // are never written.
-          float x[NB][4];
+        for (int cb = 0; cb < kPfColBlocks; ++cb)
 #pragma unroll
           for (int b = 0; b < NB; ++b)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) x[b][i] = sc[cb][b][i] * ksl[b][i];
-          if (key0 + kStep - 1 > qpos0 + cb * kPfCols) {
+            for (int i = 0; i < 4; ++i) x[cb][b][i] = sc[cb][b][i] * ksl[b][i];
+        // causal mask: key k is visible to column c iff it is at or before
+        // the query's position.  Steps wholly below the diagonal of both
+        // column blocks need no mask (uniform branch); columns without a
+        // query hold q = 0 there, so their scores stay finite and their rows
+        // are never written.
+        if (key0 + kStep - 1 > qpos0) {
+#pragma unroll
+          for (int cb = 0; cb < kPfColBlocks; ++cb) {
             const int qpos = qpos0 + cb * kPfCols + c;
 #pragma unroll
             for (int b = 0; b < NB; ++b)
 #pragma unroll
               for (int i = 0; i < 4; ++i)
-                x[b][i] = (colv[cb] && key0 + 16 * b + 4 * g + i <= qpos) ? x[b][i] : -INFINITY;
+                x[cb][b][i] = (colv[cb] && key0 + 16 * b + 4 * g + i <= qpos) ? x[cb][b][i] : -INFINITY;
           }
-          float tmax = fmaxf(fmaxf(x[0][0], x[0][1]), fmaxf(x[0][2], x[0][3]));
-          if constexpr (NB == 2) tmax = fmaxf(tmax, fmaxf(fmaxf(x[1][0], x[1][1]), fmaxf(x[1][2], x[1][3])));
-          tmax = wave_max_across_groups(tmax);
-          const bool raise = tmax > m_run[cb] + kPfRescaleThreshold;
-          if (__builtin_amdgcn_ballot_w64(raise) != 0) {
-            const float m_new = raise ? tmax : m_run[cb];
-            const float alpha = raise ? __builtin_amdgcn_exp2f(m_run[cb] - m_new) : 1.f;
+        }
+        float tmax[kPfColBlocks];
+        bool raise[kPfColBlocks];
+#pragma unroll
+        for (int cb = 0; cb < kPfColBlocks; ++cb) {
+          float t = fmaxf(fmaxf(x[cb][0][0], x[cb][0][1]), fmaxf(x[cb][0][2], x[cb][0][3]));
+          if constexpr (NB == 2) t = fmaxf(t, fmaxf(fmaxf(x[cb][1][0], x[cb][1][1]), fmaxf(x[cb][1][2], x[cb][1][3])));
+          tmax[cb] = wave_max_across_groups(t);
+          raise[cb] = tmax[cb] > m_run[cb] + kPfRescaleThreshold;
+        }
+        if (__builtin_amdgcn_ballot_w64(raise[0] || raise[1]) != 0) {
+#pragma unroll
+          for (int cb = 0; cb < kPfColBlocks; ++cb) {
+            const float m_new = raise[cb] ? tmax[cb] : m_run[cb];
+            const float alpha = raise[cb] ? __builtin_amdgcn_exp2f(m_run[cb] - m_new) : 1.f;
             m_run[cb] = m_new;
             l_run[cb] *= alpha;
 #pragma unroll
@@ -423,22 +435,30 @@ paged_prefill_kernel(const PrefillArgs a) {
               for (int j = 0; j < 8; ++j) acc[cb][j][i] *= ai;
             }
           }
+        }
+#pragma unroll
+        for (int cb = 0; cb < kPfColBlocks; ++cb) {
           const float m_use = (m_run[cb] == -INFINITY) ? 0.f : m_run[cb];
+          float p[NB][4];
 #pragma unroll
           for (int b = 0; b < NB; ++b) {
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               // v_exp_f32: arguments are at most 2^3 above the running max;
               // results below 2^-126 (flushed to 0) weigh nothing next to it
-              const float p = __builtin_amdgcn_exp2f(x[b][i] - m_use);  // 0 where masked
-              l_run[cb] += p;
-              pa[cb][4 * b + i] = static_cast<_Float16>(p * vsd[b][i]);
+              p[b][i] = __builtin_amdgcn_exp2f(x[cb][b][i] - m_use);  // 0 where masked
+              pa[cb][4 * b + i] = static_cast<_Float16>(p[b][i] * vsd[b][i]);
             }
           }
-          if (vexp != 0) {
+          float ps = (p[0][0] + p[0][1]) + (p[0][2] + p[0][3]);
+          if constexpr (NB == 2) ps += (p[1][0] + p[1][1]) + (p[1][2] + p[1][3]);
+          l_run[cb] += ps;
+        }
+        if (vexp != 0) {
+#pragma unroll
+          for (int cb = 0; cb < kPfColBlocks; ++cb)
 #pragma unroll
             for (int j = 0; j < 8; ++j) acc[cb][j] *= down;
-          }
         }
         // O += P V: V operand (B) for dims 16 j + c, one N-tile at a time,
         // shared by the column blocks; k-slots as P's
