@@ -149,6 +149,9 @@ def main() -> int:
     parser.add_argument("--no-extras", action="store_true", help="skip store/compaction/single-sequence extras")
     parser.add_argument("--copy-probe", action="store_true",
                         help="only run a plain 1 GiB device copy (reference for rocprof FETCH/WRITE_SIZE scaling)")
+    parser.add_argument("--prefill-probe", action="store_true",
+                        help="only run the paged-prefill extra warm, 3 + 10 calls (target for rocprof statistics "
+                             "and SQ counters of the prefill kernel)")
     args = parser.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -177,6 +180,24 @@ def main() -> int:
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes_read": src.numel(), "copy_probe_bytes_written": dst.numel(), "calls": 5}))
+        return 0
+
+    if args.prefill_probe:
+        from types import SimpleNamespace  # noqa: PLC0415
+
+        from prism_infer.ops.paged_prefill import _launch_paged_prefill  # noqa: PLC0415
+
+        pw = workloads.prefill_chunked(dev)
+        pctx = SimpleNamespace(block_tables=pw.block_tables, context_lens=pw.context_lens,
+                               cu_seqlens_q=pw.cu_seqlens_q)
+        call = lambda i: _launch_paged_prefill(  # noqa: E731
+            pw.q, pw.k_cache, pw.v_cache, pctx, num_heads=pw.num_heads, num_kv_heads=pw.num_kv_heads,
+            scale=pw.scale, k_scale_cache=pw.k_scale, v_scale_cache=pw.v_scale)
+        for i in range(3):
+            call(i)
+        s = _time_loop(call, 10, torch)
+        print(json.dumps({"prefill_probe_us_warm": round(s * 1e6, 2), "TFLOPs": round(pw.flops() / s / 1e12, 1),
+                          "mfma_frac": round(pw.flops() / s / MFMA_BF16_PEAK, 4), "calls": 13}))
         return 0
 
     # ---- headline workload: decode_mixed, one pool per rotated layer
