@@ -228,7 +228,6 @@ paged_decode_split_kernel(const DecodeArgs a) {
     return;
   }
   const int t_end = min(t_begin + a.split, n_eff);
-  const int nsplit = (n_eff + a.split - 1) / a.split;
 
   // ---- query operand (B of QK): column c = q head h*G + c, k slot 8g+e of
   // chunk cc <-> dim 32g + 8cc + e.
@@ -406,7 +405,7 @@ paged_decode_split_kernel(const DecodeArgs a) {
   // ---- finish: total l per q head c, then per accumulator row 4g+i.
   float l_tot = l_run + __shfl_xor(l_run, 16);
   l_tot += __shfl_xor(l_tot, 32);
-  if (nsplit == 1) {
+  if (a.max_splits == 1) {  // no combine launch: write the output
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int qr = 4 * g + i;
@@ -438,6 +437,58 @@ paged_decode_split_kernel(const DecodeArgs a) {
   }
 }
 
+constexpr int kCombineSmallMax = 64;  // split slots the one-round combine takes
+
+// Merge split-K partials when there are at most MS split slots: one round of
+// loads.  Lane s reads split s's (m, l); every lane reads its two output dims
+// of every split; all of it goes out together with the context length.  Rows
+// of splits past the context's last one may hold anything and are never read
+// into the sums.  With more than one split slot the split kernel always
+// writes partials, so this kernel writes every output row (zeros for an
+// empty context).
+template <int QDT, int MS>
+__global__ void __launch_bounds__(64) paged_decode_combine_small_kernel(const DecodeArgs a) {
+  const int b = blockIdx.x;
+  const int hq = blockIdx.y;
+  const int lane = threadIdx.x;
+  const int64_t row0 = static_cast<int64_t>(b) * a.max_splits * a.num_heads + hq;
+  const int ms = a.max_splits;  // <= MS
+  float2 ml = {-INFINITY, 0.f};
+  if (lane < ms) ml = *reinterpret_cast<const float2*>(a.part_ml + (row0 + static_cast<int64_t>(lane) * a.num_heads) * 2);
+  float v0[MS], v1[MS];
+#pragma unroll
+  for (int s = 0; s < MS; ++s) {
+    const int64_t r = row0 + static_cast<int64_t>(s < ms ? s : 0) * a.num_heads;
+    v0[s] = a.part_acc[r * kHeadDim + lane];
+    v1[s] = a.part_acc[r * kHeadDim + lane + 64];
+  }
+  const int n_eff = effective_len(a, b);
+  const int nsplit = (n_eff + a.split - 1) / a.split;  // 0 .. ms; no early exit, so the loads stay ahead
+  const float m = lane < nsplit ? ml.x : -INFINITY;
+  float m_max = m;
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) m_max = fmaxf(m_max, __shfl_xor(m_max, off));
+  const float m_use = (m_max == -INFINITY) ? 0.f : m_max;
+  const float w = lane < nsplit ? exp2f(m - m_use) : 0.f;  // 0 for m = -inf
+  float l_sum = w * (lane < nsplit ? ml.y : 0.f);
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) l_sum += __shfl_xor(l_sum, off);
+  float o0 = 0.f, o1 = 0.f;
+#pragma unroll
+  for (int s = 0; s < MS; ++s) {
+    // selects, not branches: rows past nsplit contribute exactly 0 (their
+    // contents, NaN included, are never multiplied)
+    const bool live = s < nsplit;
+    const float ws = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), s));
+    o0 += live ? ws * v0[s] : 0.f;
+    o1 += live ? ws * v1[s] : 0.f;
+  }
+  const float inv = l_sum > 0.f ? 1.f / l_sum : 0.f;
+  const int64_t base = static_cast<int64_t>(b) * a.o_sb + static_cast<int64_t>(hq) * a.o_sh;
+  store_out<QDT>(a.out, base + lane * a.o_sd, o0 * inv);
+  store_out<QDT>(a.out, base + (lane + 64) * a.o_sd, o1 * inv);
+}
+
 // Merge split-K partials: grid (batch, num_heads), one wave each.
 template <int QDT>
 __global__ void __launch_bounds__(64) paged_decode_combine_kernel(const DecodeArgs a) {
@@ -445,8 +496,7 @@ __global__ void __launch_bounds__(64) paged_decode_combine_kernel(const DecodeAr
   const int hq = blockIdx.y;
   const int lane = threadIdx.x;
   const int n_eff = effective_len(a, b);
-  const int nsplit = (n_eff + a.split - 1) / a.split;
-  if (nsplit <= 1) return;
+  const int nsplit = (n_eff + a.split - 1) / a.split;  // 0 for an empty context: zeros below
   const int64_t row0 = static_cast<int64_t>(b) * a.max_splits * a.num_heads + hq;
   float m_max = -INFINITY;
   for (int s = lane; s < nsplit; s += 64) m_max = fmaxf(m_max, a.part_ml[(row0 + static_cast<int64_t>(s) * a.num_heads) * 2]);
@@ -1809,7 +1859,10 @@ int choose_split(int batch, int num_kv_heads, int page_size, int width) {
   const int64_t tiles = static_cast<int64_t>(batch) * ceil_div(cap, kTile);
   const int64_t target = static_cast<int64_t>(device_cu_count()) * 8;
   int64_t per = tiles / (target > 0 ? target : 1);
-  if (per < 2) per = 2;
+  // at least two tiles per split, or one when every split slot of the table
+  // fits the one-round combine (a short table: shorter splits, same merge cost)
+  const int64_t min_per = ceil_div(cap, kTile) <= kCombineSmallMax ? 1 : 2;
+  if (per < min_per) per = min_per;
   // round down to a power of two number of tiles
   int64_t p2 = 1;
   while (p2 * 2 <= per) p2 *= 2;
@@ -1920,8 +1973,15 @@ int launch_all(int stage, const DecodeArgs& args, const Geometry& geo, bool page
     if (rc) return rc;
   }
   if (stage != 1 && geo.max_splits > 1) {
-    hipLaunchKernelGGL(paged_decode_combine_kernel<QDT>, dim3(args.batch, args.num_heads), dim3(64), 0, stream,
-                       args);
+    const dim3 grid(args.batch, args.num_heads);
+    if (geo.max_splits <= 16)
+      hipLaunchKernelGGL((paged_decode_combine_small_kernel<QDT, 16>), grid, dim3(64), 0, stream, args);
+    else if (geo.max_splits <= 32)
+      hipLaunchKernelGGL((paged_decode_combine_small_kernel<QDT, 32>), grid, dim3(64), 0, stream, args);
+    else if (geo.max_splits <= kCombineSmallMax)
+      hipLaunchKernelGGL((paged_decode_combine_small_kernel<QDT, kCombineSmallMax>), grid, dim3(64), 0, stream, args);
+    else
+      hipLaunchKernelGGL(paged_decode_combine_kernel<QDT>, grid, dim3(64), 0, stream, args);
     return check_launch("paged_decode_combine_kernel launch");
   }
   return PRISM_OK;
