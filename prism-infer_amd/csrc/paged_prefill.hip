@@ -347,15 +347,9 @@ paged_prefill_kernel(const PrefillArgs a) {
 #pragma unroll
           for (int off = 32; off >= 1; off >>= 1) vmax = fmaxf(vmax, __shfl_xor(vmax, off));
           vexp = __builtin_amdgcn_readfirstlane(ilogbf(vmax / kPfF16MaxVScale) + 1);
-        }
-        // per key: k_scale * softmax scale (log2 units), and v_scale with the
-        // tile's power-of-two shift
-        const float down = ldexpf(1.f, -vexp);  // 1 unless the tile's v scales exceed 255
-        floatx4 ksl[NB], vsd[NB];
+          const float down = ldexpf(1.f, -vexp);
 #pragma unroll
-        for (int b = 0; b < NB; ++b) {
-          ksl[b] = ksv[b] * a.scale_log2;
-          vsd[b] = vsv[b] * down;
+          for (int b = 0; b < NB; ++b) vsv[b] *= down;  // P * v_scale enters shifted down by 2^vexp
         }
         // S^T = K Q^T for both column blocks, one K block at a time (its
         // operand converted once)
@@ -395,7 +389,7 @@ paged_prefill_kernel(const PrefillArgs a) {
 #pragma unroll
           for (int b = 0; b < NB; ++b)
 #pragma unroll
-            for (int i = 0; i < 4; ++i) x[cb][b][i] = sc[cb][b][i] * ksl[b][i];
+            for (int i = 0; i < 4; ++i) x[cb][b][i] = sc[cb][b][i] * ksv[b][i];  // score / softmax scale
         // causal mask: key k is visible to column c iff it is at or before
         // the query's position.  Steps wholly below the diagonal of both
         // column blocks need no mask (uniform branch); columns without a
@@ -418,7 +412,7 @@ paged_prefill_kernel(const PrefillArgs a) {
         for (int cb = 0; cb < kPfColBlocks; ++cb) {
           float t = fmaxf(fmaxf(x[cb][0][0], x[cb][0][1]), fmaxf(x[cb][0][2], x[cb][0][3]));
           if constexpr (NB == 2) t = fmaxf(t, fmaxf(fmaxf(x[cb][1][0], x[cb][1][1]), fmaxf(x[cb][1][2], x[cb][1][3])));
-          tmax[cb] = wave_max_across_groups(t);
+          tmax[cb] = wave_max_across_groups(t) * a.scale_log2;  // log2 units (the scale is positive)
           raise[cb] = tmax[cb] > m_run[cb] + kPfRescaleThreshold;
         }
         if (__builtin_amdgcn_ballot_w64(raise[0] || raise[1]) != 0) {
@@ -446,8 +440,8 @@ paged_prefill_kernel(const PrefillArgs a) {
             for (int i = 0; i < 4; ++i) {
               // v_exp_f32: arguments are at most 2^3 above the running max;
               // results below 2^-126 (flushed to 0) weigh nothing next to it
-              p[b][i] = __builtin_amdgcn_exp2f(x[cb][b][i] - m_use);  // 0 where masked
-              pa[cb][4 * b + i] = static_cast<_Float16>(p[b][i] * vsd[b][i]);
+              p[b][i] = __builtin_amdgcn_exp2f(fmaf(x[cb][b][i], a.scale_log2, -m_use));  // 0 where masked
+              pa[cb][4 * b + i] = static_cast<_Float16>(p[b][i] * vsv[b][i]);
             }
           }
           float ps = (p[0][0] + p[0][1]) + (p[0][2] + p[0][3]);
@@ -455,6 +449,7 @@ paged_prefill_kernel(const PrefillArgs a) {
           l_run[cb] += ps;
         }
         if (vexp != 0) {
+          const float down = ldexpf(1.f, -vexp);
 #pragma unroll
           for (int cb = 0; cb < kPfColBlocks; ++cb)
 #pragma unroll
