@@ -91,3 +91,46 @@ def test_random_decode_configs_all_families(seed, monkeypatch):
         torch.cuda.synchronize()
         assert_decode_close(got, want, label=f"{label} path={path}")
         assert torch.all(got[lens.to(dev) == 0] == 0), "ctx=0 rows must be zeros"
+
+
+@pytest.mark.parametrize("batch", [300, 1024, 1030])
+def test_large_batches_all_families(batch, monkeypatch):
+    """Batches past the prefix-sharing analysis (256), at the streaming path's
+    limit (1024) and past it (the per-split path takes over): ragged and zero
+    lengths, holes and shared leading pages, on every family that accepts them."""
+
+    require_gpu()
+    from prism_infer import _native
+    from prism_infer.ops.paged_decode import paged_decode_attention
+
+    g = torch.Generator().manual_seed(20261204 + batch)
+    page, width, hkv, groups, d = 16, 8, 8, 4, 128
+    pool = batch * width + 8
+    lens = torch.randint(0, width * page + 1, (batch,), generator=g, dtype=torch.int32)
+    lens[torch.rand(batch, generator=g) < 0.05] = 0
+    tables = torch.randperm(pool, generator=g)[: batch * width].to(torch.int32).view(batch, width).clone()
+    tables[torch.rand(batch, width, generator=g) < 0.03] = -1
+    members = torch.randperm(batch, generator=g)[:64]
+    tables[members, :3] = tables[members[0], :3]  # a group sharing three leading pages
+    q = torch.randn(batch, hkv * groups, d, generator=g).to(torch.bfloat16)
+    k, ks = _quantize(torch.randn(pool, page, hkv, d, generator=g).to(torch.bfloat16))
+    v, vs = _quantize(torch.randn(pool, page, hkv, d, generator=g).to(torch.bfloat16))
+    scale = d ** -0.5
+    want = oracle.decode_kernel_semantics(q, k, v, tables, lens, scale, k_scale_cache=ks, v_scale_cache=vs,
+                                          compute_dtype=torch.float32)
+    dev = torch.device("cuda")
+    to = lambda t: t.view(torch.uint8).to(dev).view(FP8) if t.dtype == FP8 else t.to(dev)
+    args = (to(q), to(k), to(v), to(tables), to(lens), scale)
+    kw = dict(k_scale_cache=to(ks), v_scale_cache=to(vs))
+    family = _native.lib().prism_paged_decode_kernel_family(batch, hkv * groups, hkv, d, page, width, 3)
+    print(f"B={batch}: automatic family {family}", flush=True)
+    assert family == (2 if batch <= 1024 else 1), "streaming up to 1024 sequences, per-split beyond"
+    for path in ("auto", "split") + (("stream",) if batch <= 1024 else ()):
+        if path == "auto":
+            monkeypatch.delenv("PRISM_DECODE_PATH", raising=False)
+        else:
+            monkeypatch.setenv("PRISM_DECODE_PATH", path)
+        got = paged_decode_attention(*args, **kw)
+        torch.cuda.synchronize()
+        assert_decode_close(got, want, label=f"B={batch} path={path}")
+        assert torch.all(got[lens.to(dev) == 0] == 0), "ctx=0 rows must be zeros"
