@@ -51,3 +51,17 @@ def test_random_prefill_configs(seed):
     c = _case(20261300 + seed, cfg["seqs"], num_heads=cfg["num_heads"], num_kv_heads=cfg["num_kv_heads"],
               page=cfg["page"], scaled=cfg["scaled"], qdtype=cfg["qdtype"])
     _check(c, label)
+
+
+def test_many_short_sequences():
+    """200 sequences (the device-side sequence lookup scans them 64 at a time),
+    chunks of 1 to 40 tokens over prefixes of 0 to 300."""
+
+    require_gpu()
+    g = torch.Generator().manual_seed(20261205)
+    seqs = []
+    for _ in range(200):
+        qlen = int(torch.randint(1, 41, (1,), generator=g))
+        seqs.append((qlen, qlen + int(torch.randint(0, 301, (1,), generator=g))))
+    c = _case(20261206, seqs, num_heads=16, num_kv_heads=4, page=64)
+    _check(c, "200 short sequences")
