@@ -68,6 +68,10 @@ struct DecodeArgs {
   float scale_log2;  // sm_scale * log2(e)
   int cache_dtype;
   int debug;         // measurement aid for the stream kernel (0 in normal use)
+  // streaming path: tokens per 1 KB LDS row (8 / num_kv_heads) and per tile
+  // (16 rows); the streaming and merge kernels take the former as a template
+  // parameter, the plan kernel reads both
+  int s_tpr, s_ttok;
 };
 
 // Read-only int32 metadata (block tables, context lengths) through the
@@ -574,8 +578,15 @@ __global__ void __launch_bounds__(64) paged_decode_combine_kernel(const DecodeAr
 // * Softmax rescaling is lazy: the running max moves only when a score
 //   exceeds it by more than 2^8, which after the first tiles is rare.
 
-constexpr int kSKv = 8;                                 // kv heads on this path
-constexpr int kSTile = 16;                              // tokens per tile
+// The tile is 16 rows of 1 KB.  A row holds 8 head slots of 128 bytes: one
+// token of an 8-kv-head cache, or 8 / Hkv consecutive tokens of an Hkv-head
+// cache (Hkv = 1, 2, 4), whose token rows are 128 * Hkv bytes.  Wave h owns
+// slot h: kv head h % Hkv, token h / Hkv of each row.  Everything below the
+// row level (loads, LDS layout, swizzle, MFMAs) is the same for every Hkv;
+// the scale of (row r, slot h) is element 8 r + h of the tile's scales in
+// both layouts.
+constexpr int kSKv = 8;                                 // head slots per row (waves per workgroup)
+constexpr int kSTile = 16;                              // rows per tile (tokens: 16 * 8 / Hkv)
 constexpr int kSStages = 4;                             // pipeline depth per workgroup
 constexpr int kSWgPerCu = 1;                            // workgroups per CU
 constexpr int kSRow = kSKv * kHeadDim;                  // 1024 bytes per token row
@@ -667,12 +678,16 @@ __device__ __forceinline__ StreamLanePlan stream_plan(int wave, int lane) {
   "s_mov_b32 m0, %[lv1]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v1], off" POL "\n\t" \
   "s_mov_b32 m0, %[ls]\n\ts_nop 0\n\tglobal_load_lds_dword %[sp], off" POL
 
+template <int TPR>
 __device__ __forceinline__ void stream_issue(const DecodeArgs& a, const StreamLanePlan& pl, int t0, int blk,
                                              uint32_t stage_lds, bool nt) {
+  // off0 is a multiple of the tile's tokens, so a whole number of rows;
+  // token rows are kSRow / TPR bytes and kSKv / TPR scales
   const int off0 = t0 % a.page_size;
-  const uint8_t* kbase = a.k + blk * a.k_sblk + static_cast<int64_t>(off0) * kSRow;
-  const uint8_t* vbase = a.v + blk * a.v_sblk + static_cast<int64_t>(off0) * kSRow;
-  const float* sp = (pl.which ? a.vs : a.ks) + blk * a.ks_sblk + static_cast<int64_t>(off0) * kSKv + pl.soff;
+  const uint8_t* kbase = a.k + blk * a.k_sblk + static_cast<int64_t>(off0) * (kSRow / TPR);
+  const uint8_t* vbase = a.v + blk * a.v_sblk + static_cast<int64_t>(off0) * (kSRow / TPR);
+  const float* sp =
+      (pl.which ? a.vs : a.ks) + blk * a.ks_sblk + static_cast<int64_t>(off0) * (kSKv / TPR) + pl.soff;
   const uint8_t* k0 = kbase + pl.goff[0];
   const uint8_t* k1 = kbase + pl.goff[1];
   const uint8_t* v0 = vbase + pl.goff[0];
@@ -866,7 +881,9 @@ __device__ __forceinline__ void stream_load_q8(const DecodeArgs& a, int qrow, in
 // (workgroup, stream entry) indexes a partial uniquely as w + entry.
 
 constexpr int kSCols = 16;                 // query columns of the MFMA operand
+constexpr int kSMinKv = 4;                 // fewest kv heads on the streaming path (2 token slots)
 constexpr int kSMaxWg = 1024;              // grid size bound of the streaming kernel
+constexpr int kSMaxTpr = kSKv / kSMinKv;    // token slots per kv head, at most
 constexpr int kSMaxVirt = 128;             // virtual sequences (>= 2 members each)
 constexpr int kSShareMaxBatch = 256;       // batches above this are not analysed
 constexpr int kPlanMaxPages = 64;          // leading pages compared per sequence
@@ -992,7 +1009,7 @@ __global__ void __launch_bounds__(kPlanThreads) paged_decode_stream_plan_kernel(
   const int key_params[kPlanKeyParams] = {kPlanMagic, B, a.width, P, a.groups,
                                           static_cast<int>(a.num_blocks & 0x7FFFFFFF),
                                           static_cast<int>(a.num_blocks >> 31), share ? 1 : 0, a.stream_nwg,
-                                          0, 0, 0};
+                                          a.num_kv_heads, 0, 0};
   // The compared block-table prefix: its first eight loads per thread go out
   // before anything is compared, so the whole check is one round of loads.
   const int items = share ? B * Wc : 0;
@@ -1006,7 +1023,7 @@ __global__ void __launch_bounds__(kPlanThreads) paged_decode_stream_plan_kernel(
     old0[u] = idx < items ? key[kPlanKeyBt - kPlanKey + idx] : -1;
   }
   bool same = true;
-  if (tid < kPlanKeyParams - 3) same = key[tid] == key_params[tid];
+  if (tid < kPlanKeyParams - 2) same = key[tid] == key_params[tid];
   if (tid == 0) same = same && key[kPlanKeyParams - 2] == plan[0] && key[kPlanKeyParams - 1] == plan[1];
   if (tid < B) {
     const int n = effective_len(a, tid);
@@ -1168,8 +1185,8 @@ __global__ void __launch_bounds__(kPlanThreads) paged_decode_stream_plan_kernel(
   for (int base = 0; base < NS; base += kPlanThreads) {
     const int i = base + tid;
     int n = 0;
-    if (i < V) n = vlen_s[i] * (P / kSTile);
-    else if (i < NS) n = (eff_s[i - V] - skip_s[i - V] + kSTile - 1) / kSTile;
+    if (i < V) n = vlen_s[i] * (P / a.s_ttok);
+    else if (i < NS) n = (eff_s[i - V] - skip_s[i - V] + a.s_ttok - 1) / a.s_ttok;
     int chunk_total;
     const int incl = plan_scan(n, wsum_s, chunk_total);
     if (i < NS) tst_s[i + 1] = carry + incl;
@@ -1191,9 +1208,9 @@ __global__ void __launch_bounds__(kPlanThreads) paged_decode_stream_plan_kernel(
   for (int i = tid; i < V * kSCols; i += kPlanThreads) plan[kPlanVmem + i] = vmem_s[i];
   if (tid < V) {
     plan[kPlanVsrc + tid] = vsrc_s[tid];
-    plan[kPlanVrot + tid] = (vk_s[tid] * vlen_s[tid] / vn_s[tid]) * (P / kSTile);
+    plan[kPlanVrot + tid] = (vk_s[tid] * vlen_s[tid] / vn_s[tid]) * (P / a.s_ttok);
   }
-  if (tid < kPlanKeyParams - 3) plan[kPlanKey + tid] = key_params[tid];
+  if (tid < kPlanKeyParams - 2) plan[kPlanKey + tid] = key_params[tid];
   if (tid == 0) {  // copies of the plan header, checked before the plan is reused
     plan[kPlanKey + kPlanKeyParams - 2] = V;
     plan[kPlanKey + kPlanKeyParams - 1] = carry;
@@ -1224,11 +1241,11 @@ __global__ void __launch_bounds__(kPlanThreads) paged_decode_stream_plan_kernel(
       } else {
         bt_row = vsrc_s[i];
         tok0 = 0;
-        n_end = intl * kSTile;
-        rot = (vk_s[i] * vlen_s[i] / vn_s[i]) * (P / kSTile);
+        n_end = intl * a.s_ttok;
+        rot = (vk_s[i] * vlen_s[i] / vn_s[i]) * (P / a.s_ttok);
       }
       const int lr = ilt + rot;
-      const int t0 = tok0 + (lr >= intl ? lr - intl : lr) * kSTile;
+      const int t0 = tok0 + (lr >= intl ? lr - intl : lr) * a.s_ttok;
       const int page = t0 / P;
       r0 = int4{i, ilt, intl, bt_row};
       r1 = int4{tok0, n_end, rot, (share && page < Wc) ? bt_s[bt_row * Wc + page] : kNoBlock};
@@ -1247,6 +1264,7 @@ __global__ void __launch_bounds__(kPlanThreads) paged_decode_stream_plan_kernel(
 // Walk parameters of stream entry i (i < V: virtual sequence i, else real
 // sequence i - V): block-table row, first token, end token, and the tile at
 // which a virtual sequence starts its walk (it wraps around).
+template <int TPR>
 __device__ __forceinline__ void stream_seq(const DecodeArgs& a, const int* tstart, int V, int i, int& bt_row,
                                            int& tok0, int& n_end, int& rot) {
   if (i >= V) {
@@ -1258,16 +1276,19 @@ __device__ __forceinline__ void stream_seq(const DecodeArgs& a, const int* tstar
   } else {
     bt_row = ld_meta(a.plan + kPlanVsrc + i);
     tok0 = 0;
-    n_end = (tstart[i + 1] - tstart[i]) * kSTile;
+    n_end = (tstart[i + 1] - tstart[i]) * (kSTile * TPR);
     rot = ld_meta(a.plan + kPlanVrot + i);
   }
 }
 
-// Query column c of wave h for stream entry i: real sequence b -> q head
-// h*G + c (c < G); virtual sequence -> q head h*G + qh of member m, c = m*G + qh.
-__device__ __forceinline__ void stream_column(const DecodeArgs& a, int V, int i, int h, int c, int& qrow,
+// Query column c of wave h (kv head hk = h % Hkv) for stream entry i: real
+// sequence b -> q head hk*G + c (c < G); virtual sequence -> q head hk*G + qh
+// of member m, c = m*G + qh.
+template <int TPR>
+__device__ __forceinline__ void stream_column(const DecodeArgs& a, int V, int i, int h_slot, int c, int& qrow,
                                               int& qhead, bool& valid) {
   const int G = a.groups;
+  const int h = h_slot % (kSKv / TPR);  // kv head of the slot
   if (i >= V) {
     valid = c < G;
     qrow = i - V;
@@ -1283,9 +1304,10 @@ __device__ __forceinline__ void stream_column(const DecodeArgs& a, int V, int i,
 }
 
 // kSWgPerCu 8-wave workgroups per CU need 2 * kSWgPerCu waves per SIMD.
-template <int QDT, bool QVEC>
+template <int QDT, bool QVEC, int TPR>
 __global__ void __launch_bounds__(kSThreads) __attribute__((amdgpu_waves_per_eu(2 * kSWgPerCu)))
 paged_decode_stream_kernel(const DecodeArgs a) {
+  constexpr int kTTok = kSTile * TPR;  // tokens per tile
   __shared__ __attribute__((aligned(16))) uint8_t stages[kSStages * kSStage];
   __shared__ int tstart[kSMaxBatch + kSMaxVirt + 1];
   const int lane = threadIdx.x & 63;
@@ -1328,7 +1350,7 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   int first_page;
   {
     const int lr = ilt + irot;
-    first_page = (itok0 + (lr >= intl ? lr - intl : lr) * kSTile) / a.page_size;
+    first_page = (itok0 + (lr >= intl ? lr - intl : lr) * kTTok) / a.page_size;
   }
   // the first page's block id comes from the record when the plan could cache it
   int ipage = first_raw != kNoBlock ? first_page : -1;
@@ -1336,7 +1358,7 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   int64_t issued = 0;
   auto issue_next = [&]() {
     const int lr = ilt + irot;
-    const int t0 = itok0 + (lr >= intl ? lr - intl : lr) * kSTile;
+    const int t0 = itok0 + (lr >= intl ? lr - intl : lr) * kTTok;
     const int page = __builtin_amdgcn_readfirstlane(t0 / a.page_size);
     if (page != ipage) {
       ipage = page;
@@ -1345,7 +1367,7 @@ paged_decode_stream_kernel(const DecodeArgs a) {
       iblk = (raw >= 0 && raw < a.num_blocks) ? raw : 0;
     }
     if (!(a.debug & 2))
-      stream_issue(a, pl, t0, iblk, stage0 + static_cast<uint32_t>(issued % kSStages) * kSStage,
+      stream_issue<TPR>(a, pl, t0, iblk, stage0 + static_cast<uint32_t>(issued % kSStages) * kSStage,
                    ib >= V && !(a.debug & 16));
     ++issued;
     if (++ilt == intl && issued < count) {  // next stream entry with tiles
@@ -1356,7 +1378,7 @@ paged_decode_stream_kernel(const DecodeArgs a) {
       ib = __builtin_amdgcn_readfirstlane(ib);
       ilt = 0;
       ipage = -1;
-      stream_seq(a, tstart, V, ib, ibt_row, itok0, iend, irot);
+      stream_seq<TPR>(a, tstart, V, ib, ibt_row, itok0, iend, irot);
     }
   };
 #pragma unroll
@@ -1377,7 +1399,7 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   bool colv;
   {
     int qrow, qhead;
-    stream_column(a, V, b, h, c, qrow, qhead, colv);
+    stream_column<TPR>(a, V, b, h, c, qrow, qhead, colv);
     stream_load_q8<QDT, QVEC>(a, qrow, qhead, colv, g, qop);
   }
 
@@ -1417,7 +1439,7 @@ paged_decode_stream_kernel(const DecodeArgs a) {
     if (issued < count) issue_next();
 
     const int lr = lt + crot;
-    const int t0 = ctok0 + (lr >= ntl ? lr - ntl : lr) * kSTile;
+    const int t0 = ctok0 + (lr >= ntl ? lr - ntl : lr) * kTTok;
     {
       const int page = __builtin_amdgcn_readfirstlane(t0 / a.page_size);
       if (page != cpage) {
@@ -1462,12 +1484,13 @@ paged_decode_stream_kernel(const DecodeArgs a) {
       // Masked slots get score -inf (weight 0) and v scale 0, and their V
       // bytes are zeroed: rows past the end may hold anything, and the MFMA
       // would turn 0 * NaN into NaN.
-      if (t0 + kSTile > n_eff) {
-        const int lim = n_eff - t0 - 4 * g;  // valid slots of this lane: min(max(lim, 0), 4)
+      if (t0 + kTTok > n_eff) {
+        // row 4g + i of this wave's slot is token t0 + tpr * (4g + i) + h / Hkv
+        const int tok_g = t0 + TPR * 4 * g + h / (kSKv / TPR);
         uint32_t keep = 0;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const bool tv = i < lim;
+          const bool tv = tok_g + TPR * i < n_eff;
           x[i] = tv ? x[i] : -INFINITY;
           vsm[i] = tv ? vsm[i] : 0.f;
           keep |= tv ? (0xFFu << (8 * i)) : 0u;
@@ -1538,12 +1561,12 @@ paged_decode_stream_kernel(const DecodeArgs a) {
     if (seq_ends) {
       float l_tot = l_run + __shfl_xor(l_run, 16);
       l_tot += __shfl_xor(l_tot, 32);
-      // partial rows: real entry b at (wg + b) * Hq + q head; virtual entry v
+      // partial rows: real entry b at (wg + b) * 8G + slot * G + column; virtual entry v
       // at vrow0 + ((wg + v) * 8 + h) * 16 + column
       const bool virt = b < V;
       const int ncols = virt ? kSCols : a.groups;
       const int64_t row0 = virt ? a.vrow0 + ((static_cast<int64_t>(blockIdx.x) + b) * kSKv + h) * kSCols
-                                : (static_cast<int64_t>(blockIdx.x) + b) * a.num_heads + h * a.groups;
+                                : (static_cast<int64_t>(blockIdx.x) + b) * (kSKv * a.groups) + h * a.groups;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const int qr = 4 * g + i;
@@ -1572,9 +1595,9 @@ paged_decode_stream_kernel(const DecodeArgs a) {
         b = __builtin_amdgcn_readfirstlane(b);
         lt = 0;
         cpage = -1;
-        stream_seq(a, tstart, V, b, cbt_row, ctok0, n_eff, crot);
+        stream_seq<TPR>(a, tstart, V, b, cbt_row, ctok0, n_eff, crot);
         int qrow, qhead;
-        stream_column(a, V, b, h, c, qrow, qhead, colv);
+        stream_column<TPR>(a, V, b, h, c, qrow, qhead, colv);
         stream_load_q8<QDT, QVEC>(a, qrow, qhead, colv, g, qop);
       }
     } else {
@@ -1597,13 +1620,13 @@ paged_decode_stream_kernel(const DecodeArgs a) {
 // their (m, l) and accumulators loaded together: two rounds of dependent
 // loads (the sequence's plan record, then the partials).  More candidates
 // are read lane-parallel first.
-template <int QDT>
+template <int QDT, int TPR>
 __global__ void __launch_bounds__(64) paged_decode_stream_combine_kernel(const DecodeArgs a) {
   // the tail's and the virtual sequence's tile ranges are disjoint, so at
-  // most one workgroup meets both: at most nwg + 1 candidates
-  __shared__ float m_s[kSMaxWg + 1];
-  __shared__ float l_s[kSMaxWg + 1];
-  __shared__ int rows[kSMaxWg + 1];
+  // most one workgroup meets both: at most (nwg + 1) * TPR candidates
+  __shared__ float m_s[(kSMaxWg + 1) * TPR];
+  __shared__ float l_s[(kSMaxWg + 1) * TPR];
+  __shared__ int rows[(kSMaxWg + 1) * TPR];
   const int b = blockIdx.x;
   const int hq = blockIdx.y;
   const int lane = threadIdx.x;
@@ -1617,8 +1640,13 @@ __global__ void __launch_bounds__(64) paged_decode_stream_combine_kernel(const D
     lo0 = static_cast<int>(split_owner(sp, first));
     cnt0 = static_cast<int>(split_owner(sp, end - 1)) - lo0 + 1;
   }
-  // row of workgroup w: real (w + V + b) * Hq + hq; virtual vrow0 + ((w + v) * 8 + hk) * 16 + col
-  const int64_t rbase0 = static_cast<int64_t>(V + b) * a.num_heads + hq;
+  // Candidates are (workgroup w, token slot s < 8 / Hkv) pairs: the waves of
+  // slots hk + Hkv * s of w each streamed a share of the tokens.  Rows: real
+  // (w + V + b) * 8G + (hk + Hkv s) * G + qh; virtual
+  // vrow0 + ((w + v) * 8 + hk + Hkv s) * 16 + m * G + qh.
+  constexpr int tl = TPR == 1 ? 0 : (TPR == 2 ? 1 : (TPR == 4 ? 2 : 3));  // log2 of the token slots
+  constexpr int hkv = kSKv / TPR;
+  const int64_t rbase0 = static_cast<int64_t>(V + b) * (kSKv * a.groups) + hq;
   int64_t rbase1 = 0;
   if (vslot >= 0) {
     const int v = vslot / kSCols;
@@ -1628,7 +1656,17 @@ __global__ void __launch_bounds__(64) paged_decode_stream_combine_kernel(const D
     lo1 = static_cast<int>(split_owner(sp, vfirst));
     cnt1 = static_cast<int>(split_owner(sp, vend - 1)) - lo1 + 1;
   }
-  const int cnt = cnt0 + cnt1;
+  const int cnt = (cnt0 + cnt1) << tl;
+  // candidate i: its row and whether its workgroup had a range at all
+  auto cand = [&](int i, int64_t& row, bool& ok) {
+    const int wi = i >> tl;
+    const int sl = i & ((1 << tl) - 1);
+    const bool second = wi >= cnt0;
+    const int64_t w = second ? lo1 + (wi - cnt0) : lo0 + wi;
+    row = second ? rbase1 + w * (kSKv * kSCols) + sl * (hkv * kSCols)
+                 : rbase0 + w * (kSKv * a.groups) + sl * a.num_heads;
+    ok = split_begin(sp, w) < split_begin(sp, w + 1);
+  };
   float l_sum = 0.f, o0 = 0.f, o1 = 0.f;
   if (cnt <= 8) {  // (uniform) a few candidates: their loads in one round
     constexpr int kU = 8;
@@ -1637,13 +1675,12 @@ __global__ void __launch_bounds__(64) paged_decode_stream_combine_kernel(const D
       float mv[kU], lv[kU], v0[kU], v1[kU];
 #pragma unroll
       for (int u = 0; u < kU; ++u) {
-        const int i = min(base + u, cnt - 1);
-        const bool second = i >= cnt0;
-        const int64_t w = second ? lo1 + (i - cnt0) : lo0 + i;
-        const int64_t row = second ? rbase1 + w * (kSKv * kSCols) : rbase0 + w * a.num_heads;
+        int64_t row;
+        bool ok;
+        cand(min(base + u, cnt - 1), row, ok);
         // a workgroup with an empty range (fewer tiles than workgroups) wrote
         // nothing: its row is never read into the sums
-        const bool ok = base + u < cnt && split_begin(sp, w) < split_begin(sp, w + 1);
+        ok = ok && base + u < cnt;
         const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + row * 2);
         const float x0 = a.part_acc[row * kHeadDim + lane];
         const float x1 = a.part_acc[row * kHeadDim + lane + 64];
@@ -1677,10 +1714,10 @@ __global__ void __launch_bounds__(64) paged_decode_stream_combine_kernel(const D
     float m_max = -INFINITY;
     for (int base = 0; base < cnt; base += 64) {
       const int i = base + lane;
-      const bool second = i >= cnt0;
-      const int64_t w = second ? lo1 + (i - cnt0) : lo0 + i;
-      bool ok = i < cnt && split_begin(sp, w) < split_begin(sp, w + 1);
-      const int64_t row = second ? rbase1 + w * (kSKv * kSCols) : rbase0 + w * a.num_heads;
+      int64_t row;
+      bool ok;
+      cand(min(i, cnt - 1), row, ok);
+      ok = ok && i < cnt;
       float2 ml = {-INFINITY, 0.f};
       if (ok) ml = *reinterpret_cast<const float2*>(a.part_ml + row * 2);
       ok = ok && ml.x != -INFINITY;  // a partial with nothing attended weighs 0
@@ -1893,10 +1930,11 @@ Geometry geometry(int batch, int num_heads, int num_kv_heads, int head_dim, int 
     geo.ml_off = geo.acc_off + align_up(rows * head_dim * 4, 256);
     geo.ws_bytes = geo.ml_off + align_up(rows * 2 * 4, 256);
   }
-  geo.stream_shape = num_kv_heads == kSKv && page_size % kSTile == 0 && batch <= kSMaxBatch && !stream_disabled() &&
+  const int ttok = (num_kv_heads == kSKv || num_kv_heads == kSMinKv) ? kSTile * (kSKv / num_kv_heads) : 0;
+  geo.stream_shape = ttok > 0 && page_size % ttok == 0 && batch <= kSMaxBatch && !stream_disabled() &&
                      device_cu_count() * kSWgPerCu <= kSMaxWg;
   if (geo.stream_shape && forced_path() != 2) {
-    const int64_t cap_tiles = static_cast<int64_t>(batch) * ceil_div(static_cast<int64_t>(width) * page_size, kSTile);
+    const int64_t cap_tiles = static_cast<int64_t>(batch) * ceil_div(static_cast<int64_t>(width) * page_size, ttok);
     if (cap_tiles < 8LL * device_cu_count() * kSWgPerCu) geo.stream_shape = false;
   }
   if (geo.stream_shape) {
@@ -1905,8 +1943,10 @@ Geometry geometry(int batch, int num_heads, int num_kv_heads, int head_dim, int 
     geo.stream_nwg = device_cu_count() * kSWgPerCu;
     const int members = kSCols / (num_heads / num_kv_heads);
     const int64_t vmax = (batch <= kSShareMaxBatch && members >= 2) ? std::min(kSMaxVirt, batch / 2) : 0;
-    // real rows: (wg + V + b); virtual rows: (wg + v)
-    geo.stream_vrow0 = (static_cast<int64_t>(geo.stream_nwg) + vmax + batch) * num_heads;
+    // real rows: (wg + V + b) * 8G (one set of G per head slot); virtual
+    // rows: (wg + v) * 8 * 16
+    const int64_t slot_rows = static_cast<int64_t>(kSKv) * (num_heads / num_kv_heads);
+    geo.stream_vrow0 = (static_cast<int64_t>(geo.stream_nwg) + vmax + batch) * slot_rows;
     const int64_t rows =
         geo.stream_vrow0 + (vmax > 0 ? (static_cast<int64_t>(geo.stream_nwg) + vmax) * kSKv * kSCols : 0);
     geo.stream_acc_off = plan_bytes;
@@ -1924,19 +1964,24 @@ int launch_stream(int stage, const DecodeArgs& args, const Geometry& geo, hipStr
     int rc = check_launch("paged_decode_stream_plan_kernel launch");
     if (rc || stage == 3) return rc;
   }
+  const bool two = args.s_tpr == 2;  // 4 kv heads: two tokens per row
   if (stage == 0 || stage == 1) {
     int rc;
-    if (args.q_vec)
-      hipLaunchKernelGGL((paged_decode_stream_kernel<QDT, true>), dim3(geo.stream_nwg), dim3(kSThreads), 0, stream, args);
-    else
-      hipLaunchKernelGGL((paged_decode_stream_kernel<QDT, false>), dim3(geo.stream_nwg), dim3(kSThreads), 0, stream,
-                         args);
+    const dim3 grid(geo.stream_nwg), block(kSThreads);
+    if (args.q_vec) {
+      if (two) hipLaunchKernelGGL((paged_decode_stream_kernel<QDT, true, 2>), grid, block, 0, stream, args);
+      else hipLaunchKernelGGL((paged_decode_stream_kernel<QDT, true, 1>), grid, block, 0, stream, args);
+    } else {
+      if (two) hipLaunchKernelGGL((paged_decode_stream_kernel<QDT, false, 2>), grid, block, 0, stream, args);
+      else hipLaunchKernelGGL((paged_decode_stream_kernel<QDT, false, 1>), grid, block, 0, stream, args);
+    }
     rc = check_launch("paged_decode_stream_kernel launch");
     if (rc) return rc;
   }
   if (stage != 1) {
-    hipLaunchKernelGGL(paged_decode_stream_combine_kernel<QDT>, dim3(args.batch, args.num_heads), dim3(64), 0, stream,
-                       args);
+    const dim3 grid(args.batch, args.num_heads);
+    if (two) hipLaunchKernelGGL((paged_decode_stream_combine_kernel<QDT, 2>), grid, dim3(64), 0, stream, args);
+    else hipLaunchKernelGGL((paged_decode_stream_combine_kernel<QDT, 1>), grid, dim3(64), 0, stream, args);
     return check_launch("paged_decode_stream_combine_kernel launch");
   }
   return PRISM_OK;
@@ -2152,9 +2197,12 @@ extern "C" int prism_paged_decode_stage(
   }
   const bool page_aligned = (page_size % kTile) == 0;
   // Streaming path: canonical contiguous page layout with scales.
-  const bool use_stream = geo.fast && geo.stream_shape && k_scale != nullptr && k_strides[1] == kSRow &&
-                          k_strides[2] == kHeadDim && v_strides[1] == kSRow && v_strides[2] == kHeadDim &&
-                          ks_strides[1] == kSKv && ks_strides[2] == 1 && vs_strides[1] == kSKv && vs_strides[2] == 1 &&
+  // (token rows of num_kv_heads * 128 bytes, contiguous within a page)
+  const int64_t tok_bytes = static_cast<int64_t>(num_kv_heads) * kHeadDim;
+  const bool use_stream = geo.fast && geo.stream_shape && k_scale != nullptr && k_strides[1] == tok_bytes &&
+                          k_strides[2] == kHeadDim && v_strides[1] == tok_bytes && v_strides[2] == kHeadDim &&
+                          ks_strides[1] == num_kv_heads && ks_strides[2] == 1 && vs_strides[1] == num_kv_heads &&
+                          vs_strides[2] == 1 &&
                           ks_strides[0] == vs_strides[0] && aligned(k_scale, 16) && aligned(v_scale, 16) &&
                           ks_strides[0] % 4 == 0;
   if (use_stream) {
@@ -2162,6 +2210,8 @@ extern "C" int prism_paged_decode_stage(
     args.part_acc = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + geo.stream_acc_off);
     args.part_ml = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + geo.stream_ml_off);
     args.vrow0 = geo.stream_vrow0;
+    args.s_tpr = kSKv / num_kv_heads;
+    args.s_ttok = kSTile * args.s_tpr;
     const char* share = getenv("PRISM_DECODE_SHARE");  // "0" turns the shared-page analysis off
     args.share = !(share && share[0] == '0');
     args.stream_nwg = geo.stream_nwg;

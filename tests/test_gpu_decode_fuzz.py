@@ -134,3 +134,45 @@ def test_large_batches_all_families(batch, monkeypatch):
         torch.cuda.synchronize()
         assert_decode_close(got, want, label=f"B={batch} path={path}")
         assert torch.all(got[lens.to(dev) == 0] == 0), "ctx=0 rows must be zeros"
+
+
+@pytest.mark.parametrize("hq", [16, 32])
+def test_four_kv_heads_streaming(hq, monkeypatch):
+    """Four kv heads (a tensor-parallel shard of an 8-head model) on the
+    streaming path: two tokens per LDS row, two waves per kv head, merged per
+    token slot; a group of sequences sharing two leading pages exercises the
+    virtual sequences."""
+
+    require_gpu()
+    from prism_infer import _native
+    from prism_infer.ops.paged_decode import paged_decode_attention
+
+    g = torch.Generator().manual_seed(20261207 + hq)
+    batch, page, hkv, d = 48, 256, 4, 128
+    width = 13
+    pool = batch * width + 8
+    lens = torch.randint(100, width * page + 1, (batch,), generator=g, dtype=torch.int32)
+    lens[:3] = torch.tensor([1, 2, 33], dtype=torch.int32)  # tails shorter than a tile
+    lens[5] = 0
+    tables = torch.randperm(pool, generator=g)[: batch * width].to(torch.int32).view(batch, width).clone()
+    members = torch.arange(10, 26)
+    lens[members] = torch.clamp(lens[members], min=2 * page + 1)
+    tables[members, :2] = tables[members[0], :2]  # 16 sequences share two leading pages
+    tables[40, 4] = -1  # a hole
+    q = torch.randn(batch, hq, d, generator=g).to(torch.bfloat16)
+    k, ks = _quantize(torch.randn(pool, page, hkv, d, generator=g).to(torch.bfloat16))
+    v, vs = _quantize(torch.randn(pool, page, hkv, d, generator=g).to(torch.bfloat16))
+    scale = d ** -0.5
+    want = oracle.decode_kernel_semantics(q, k, v, tables, lens, scale, k_scale_cache=ks, v_scale_cache=vs,
+                                          compute_dtype=torch.float32)
+    assert _native.lib().prism_paged_decode_kernel_family(batch, hq, hkv, d, page, width, 3) == 2
+    dev = torch.device("cuda")
+    to = lambda t: t.view(torch.uint8).to(dev).view(FP8) if t.dtype == FP8 else t.to(dev)
+    args = (to(q), to(k), to(v), to(tables), to(lens), scale)
+    kw = dict(k_scale_cache=to(ks), v_scale_cache=to(vs))
+    for path in ("stream", "split"):
+        monkeypatch.setenv("PRISM_DECODE_PATH", path)
+        got = paged_decode_attention(*args, **kw)
+        torch.cuda.synchronize()
+        assert_decode_close(got, want, label=f"Hkv=4 Hq={hq} path={path}")
+        assert torch.all(got[lens.to(dev) == 0] == 0), "ctx=0 rows must be zeros"
