@@ -136,19 +136,19 @@ def test_large_batches_all_families(batch, monkeypatch):
         assert torch.all(got[lens.to(dev) == 0] == 0), "ctx=0 rows must be zeros"
 
 
-@pytest.mark.parametrize("hq", [16, 32])
-def test_four_kv_heads_streaming(hq, monkeypatch):
-    """Four kv heads (a tensor-parallel shard of an 8-head model) on the
-    streaming path: two tokens per LDS row, two waves per kv head, merged per
-    token slot; a group of sequences sharing two leading pages exercises the
-    virtual sequences."""
+@pytest.mark.parametrize("hkv,hq", [(4, 16), (4, 32), (2, 8), (2, 16)])
+def test_fewer_kv_heads_streaming(hkv, hq, monkeypatch):
+    """Four or two kv heads (tensor-parallel shards of an 8-head model) on the
+    streaming path: two or four tokens per LDS row, as many waves per kv head,
+    merged per token slot; a group of sequences sharing two leading pages
+    exercises the virtual sequences."""
 
     require_gpu()
     from prism_infer import _native
     from prism_infer.ops.paged_decode import paged_decode_attention
 
-    g = torch.Generator().manual_seed(20261207 + hq)
-    batch, page, hkv, d = 48, 256, 4, 128
+    g = torch.Generator().manual_seed(20261207 + 100 * hkv + hq)
+    batch, page, d = 48, 256, 128
     width = 13
     pool = batch * width + 8
     lens = torch.randint(100, width * page + 1, (batch,), generator=g, dtype=torch.int32)
@@ -174,5 +174,5 @@ def test_four_kv_heads_streaming(hq, monkeypatch):
         monkeypatch.setenv("PRISM_DECODE_PATH", path)
         got = paged_decode_attention(*args, **kw)
         torch.cuda.synchronize()
-        assert_decode_close(got, want, label=f"Hkv=4 Hq={hq} path={path}")
+        assert_decode_close(got, want, label=f"Hkv={hkv} Hq={hq} path={path}")
         assert torch.all(got[lens.to(dev) == 0] == 0), "ctx=0 rows must be zeros"
