@@ -881,7 +881,7 @@ __device__ __forceinline__ void stream_load_q8(const DecodeArgs& a, int qrow, in
 // (workgroup, stream entry) indexes a partial uniquely as w + entry.
 
 constexpr int kSCols = 16;                 // query columns of the MFMA operand
-constexpr int kSMinKv = 2;                 // fewest kv heads on the streaming path (4 token slots)
+constexpr int kSMinKv = 1;                 // fewest kv heads on the streaming path (8 token slots)
 constexpr int kSMaxWg = 1024;              // grid size bound of the streaming kernel
 constexpr int kSMaxVirt = 128;             // virtual sequences (>= 2 members each)
 constexpr int kSShareMaxBatch = 256;       // batches above this are not analysed
@@ -1929,7 +1929,10 @@ Geometry geometry(int batch, int num_heads, int num_kv_heads, int head_dim, int 
     geo.ml_off = geo.acc_off + align_up(rows * head_dim * 4, 256);
     geo.ws_bytes = geo.ml_off + align_up(rows * 2 * 4, 256);
   }
-  const int ttok = (num_kv_heads == 8 || num_kv_heads == 4 || num_kv_heads == 2) ? kSTile * (kSKv / num_kv_heads) : 0;
+  const int ttok = (num_kv_heads > 0 && num_kv_heads <= kSKv && (kSKv % num_kv_heads) == 0 &&
+                    (num_kv_heads & (num_kv_heads - 1)) == 0)
+                       ? kSTile * (kSKv / num_kv_heads)
+                       : 0;  // 8, 4, 2 or 1 kv heads
   geo.stream_shape = ttok > 0 && page_size % ttok == 0 && batch <= kSMaxBatch && !stream_disabled() &&
                      device_cu_count() * kSWgPerCu <= kSMaxWg;
   if (geo.stream_shape && forced_path() != 2) {
@@ -1963,17 +1966,19 @@ int launch_stream(int stage, const DecodeArgs& args, const Geometry& geo, hipStr
     int rc = check_launch("paged_decode_stream_plan_kernel launch");
     if (rc || stage == 3) return rc;
   }
-  // token slots per row: 1 (8 kv heads), 2 (4) or 4 (2)
+  // token slots per row: 1 (8 kv heads), 2 (4), 4 (2) or 8 (1)
   if (stage == 0 || stage == 1) {
     const dim3 grid(geo.stream_nwg), block(kSThreads);
 #define PRISM_LAUNCH_STREAM(V, T) \
   hipLaunchKernelGGL((paged_decode_stream_kernel<QDT, V, T>), grid, block, 0, stream, args)
     if (args.q_vec) {
-      if (args.s_tpr == 4) PRISM_LAUNCH_STREAM(true, 4);
+      if (args.s_tpr == 8) PRISM_LAUNCH_STREAM(true, 8);
+      else if (args.s_tpr == 4) PRISM_LAUNCH_STREAM(true, 4);
       else if (args.s_tpr == 2) PRISM_LAUNCH_STREAM(true, 2);
       else PRISM_LAUNCH_STREAM(true, 1);
     } else {
-      if (args.s_tpr == 4) PRISM_LAUNCH_STREAM(false, 4);
+      if (args.s_tpr == 8) PRISM_LAUNCH_STREAM(false, 8);
+      else if (args.s_tpr == 4) PRISM_LAUNCH_STREAM(false, 4);
       else if (args.s_tpr == 2) PRISM_LAUNCH_STREAM(false, 2);
       else PRISM_LAUNCH_STREAM(false, 1);
     }
@@ -1983,7 +1988,8 @@ int launch_stream(int stage, const DecodeArgs& args, const Geometry& geo, hipStr
   }
   if (stage != 1) {
     const dim3 grid(args.batch, args.num_heads);
-    if (args.s_tpr == 4) hipLaunchKernelGGL((paged_decode_stream_combine_kernel<QDT, 4>), grid, dim3(64), 0, stream, args);
+    if (args.s_tpr == 8) hipLaunchKernelGGL((paged_decode_stream_combine_kernel<QDT, 8>), grid, dim3(64), 0, stream, args);
+    else if (args.s_tpr == 4) hipLaunchKernelGGL((paged_decode_stream_combine_kernel<QDT, 4>), grid, dim3(64), 0, stream, args);
     else if (args.s_tpr == 2) hipLaunchKernelGGL((paged_decode_stream_combine_kernel<QDT, 2>), grid, dim3(64), 0, stream, args);
     else hipLaunchKernelGGL((paged_decode_stream_combine_kernel<QDT, 1>), grid, dim3(64), 0, stream, args);
     return check_launch("paged_decode_stream_combine_kernel launch");
