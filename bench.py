@@ -287,7 +287,7 @@ def main() -> int:
 
     if not args.no_extras:
         result["decode_step_graph"] = _graph_steps(step, len(layers), outs, alg_bytes, torch)
-        result["decode_tp2_shard"] = _tp2_shard(base, torch)
+        result["decode_tp_shards"] = {f"tp{tp}": _tp_shard(base, torch, tp) for tp in (2, 4, 8)}
         result["extras"] = _extras(torch, dev, workloads)
     del layers, outs, ws
     torch.cuda.empty_cache()
@@ -301,11 +301,11 @@ def main() -> int:
     return 0
 
 
-def _tp2_shard(base, torch, steps: int = 50) -> dict:
-    """One tensor-parallel rank's share of the headline step at TP = 2: the
-    same sequences and pages with the first 4 of the 8 kv heads (a contiguous
-    4-head cache, Hq = 16), plan check + streaming kernel + merge per step,
-    warm, eager, no layer rotation."""
+def _tp_shard(base, torch, tp: int, steps: int = 50) -> dict:
+    """One tensor-parallel rank's share of the headline step at TP = tp: the
+    same sequences and pages with the first 8 / tp of the 8 kv heads (a
+    contiguous cache of that many heads, Hq = 32 / tp), plan check + streaming
+    kernel + merge per step, warm, eager, no layer rotation."""
 
     from prism_infer import _native  # noqa: PLC0415
     from prism_infer.ops.paged_decode import (  # noqa: PLC0415
@@ -313,9 +313,10 @@ def _tp2_shard(base, torch, steps: int = 50) -> dict:
         decode_workspace_bytes,
     )
 
-    q = base.q[:, :16].contiguous()
-    k, v = base.k_cache[:, :, :4].contiguous(), base.v_cache[:, :, :4].contiguous()
-    ks, vs = base.k_scale[:, :, :4].contiguous(), base.v_scale[:, :, :4].contiguous()
+    hkv, hq = 8 // tp, 32 // tp
+    q = base.q[:, :hq].contiguous()
+    k, v = base.k_cache[:, :, :hkv].contiguous(), base.v_cache[:, :, :hkv].contiguous()
+    ks, vs = base.k_scale[:, :, :hkv].contiguous(), base.v_scale[:, :, :hkv].contiguous()
     ws = torch.empty(decode_workspace_bytes(q, k, base.block_tables), dtype=torch.uint8, device=q.device)
     out = torch.empty_like(q)
     call = lambda i, stage=0: _launch_paged_decode_attention(  # noqa: E731
@@ -325,13 +326,14 @@ def _tp2_shard(base, torch, steps: int = 50) -> dict:
         call(i)
     s = _time_loop(call, steps, torch)
     kernel = _time_loop(lambda i: call(i, 1), steps, torch)
-    family = _native.lib().prism_paged_decode_kernel_family(base.batch, 16, 4, 128, 256, base.block_tables.shape[1], 3)
+    family = _native.lib().prism_paged_decode_kernel_family(base.batch, hq, hkv, 128, 256, base.block_tables.shape[1],
+                                                            3)
     shard = type(base)(**{**base.__dict__, "q": q, "k_cache": k, "v_cache": v, "k_scale": ks, "v_scale": vs})
     shard_bytes = shard.algorithmic_bytes()
     del k, v, ks, vs, ws, shard
     return {"us_per_layer": round(s * 1e6, 2), "GBps": round(shard_bytes / s / 1e9, 1),
             "pct_of_hbm_peak": round(100.0 * shard_bytes / s / 1e9 / HBM_PEAK_GBPS, 2),
-            "kernel_us": round(kernel * 1e6, 2), "kernel_family": int(family), "kv_heads": 4, "q_heads": 16,
+            "kernel_us": round(kernel * 1e6, 2), "kernel_family": int(family), "kv_heads": hkv, "q_heads": hq,
             "timing": "warm, eager, HIP events"}
 
 
