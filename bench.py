@@ -1,11 +1,10 @@
 """Benchmark of the scaled-FP8 paged KV hot path on one MI355X.
 
-Headline (BASELINE.json metric): paged-decode achieved HBM GB/s (and % of the
-8 TB/s peak) plus us/layer on the batch-64 mixed-context workload
-(``decode_mixed``: 64 sequences, lengths U[1k, 16k], 32 of them sharing one
-4096-token prefix, 32 q / 8 kv heads, head_dim 128, 256-token scaled-FP8
-pages).  A step is one layer's decode over the batch (split-K kernel +
-combine).  Steps rotate over ``--layers`` independent KV pools so that each
+Headline: paged-decode achieved HBM GB/s (and % of the 8 TB/s peak) plus
+us/layer on the batch-64 mixed-context workload (``decode_mixed``: 64
+sequences, lengths U[1k, 16k], 32 of them sharing one 4096-token prefix,
+32 q / 8 kv heads, head_dim 128, 256-token scaled-FP8 pages).  A step is one
+layer's decode over the batch (plan check, streaming kernel, merge).  Steps rotate over ``--layers`` independent KV pools so that each
 step reads its pages cold from HBM (the 256 MB MALL cannot hold a layer).
 
 ``value`` = algorithmic bytes / time per step, where algorithmic bytes count
