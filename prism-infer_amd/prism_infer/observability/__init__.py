@@ -9,7 +9,7 @@ The ops keep the reference's region names (``attention.kv_store.*``,
 
 from __future__ import annotations
 
-from contextlib import contextmanager, nullcontext
+from contextlib import nullcontext
 from typing import Any, Callable
 
 _PROVIDER: Callable[..., Any] | None = None
@@ -28,4 +28,4 @@ def profile_region(name: str, cuda: bool = True, metadata: dict | None = None):
     return _PROVIDER(name, cuda=cuda, metadata=metadata)
 
 
-__all__ = ["install_profile_provider", "profile_region", "contextmanager"]
+__all__ = ["install_profile_provider", "profile_region"]

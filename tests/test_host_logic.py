@@ -23,9 +23,12 @@ from prism_infer.engine.kv_quantization import (
     FP8_E4M3FN_MAX,
     KV_SCALE_DTYPE,
     PER_TOKEN_HEAD_SCALE_FLOOR,
+    KVStorageBytes,
     kv_block_storage_bytes,
+    kv_cache_storage_bytes,
     kv_token_layer_bytes,
     scale_cache_shape,
+    tensor_storage_bytes,
 )
 
 REPO = Path(__file__).resolve().parents[1]
@@ -62,6 +65,36 @@ def test_scale_cache_shape_and_errors():
                                payload_dtype=torch.bfloat16, token_head_scales=False)
 
 
+def test_allocated_cache_bytes_equal_pages_times_block_bytes():
+    # The engine's cache is [K|V, layers, blocks, page, heads, dim] with scales
+    # [K|V, layers, blocks, page, heads] (model_runner.py:817-837); its bytes must be
+    # num_blocks times the per-block figure, and one block's slice (the view
+    # bench_system.py:574 measures) exactly the per-block figure.
+    L, N, P, H, D = 3, 5, 16, 4, 32
+    payload = torch.empty((2, L, N, P, H, D), dtype=torch.float8_e4m3fn)
+    scales = torch.empty((2, L, N, P, H), dtype=torch.float32)
+    per_block = kv_block_storage_bytes(num_layers=L, page_size=P, num_kv_heads=H, head_dim=D,
+                                       payload_dtype=torch.float8_e4m3fn, token_head_scales=True)
+    whole = kv_cache_storage_bytes(payload, scales)
+    assert isinstance(whole, KVStorageBytes)
+    assert whole == KVStorageBytes(N * per_block.payload, N * per_block.scales)
+    assert tensor_storage_bytes(payload[:, :, 0]) == per_block.payload
+    assert tensor_storage_bytes(scales[:, :, 0]) == per_block.scales
+    dense = torch.empty((2, L, N, P, H, D), dtype=torch.bfloat16)
+    assert kv_cache_storage_bytes(dense, None) == KVStorageBytes(dense.numel() * 2, 0)
+    assert tensor_storage_bytes(None) == 0
+    with pytest.raises(TypeError):
+        tensor_storage_bytes([1, 2])
+    with pytest.raises(TypeError):
+        kv_cache_storage_bytes(None, scales)
+    with pytest.raises(TypeError):
+        kv_block_storage_bytes(num_layers=1, page_size=1, num_kv_heads=1, head_dim=1,
+                               payload_dtype="fp8", token_head_scales=True)
+    with pytest.raises(ValueError):
+        kv_block_storage_bytes(num_layers=True, page_size=1, num_kv_heads=1, head_dim=1,
+                               payload_dtype=torch.bfloat16, token_head_scales=False)
+
+
 def test_in_place_plan_reference_case():
     plan = plan_in_place([0, 1, 2], [0, 1, 2, 7, 8, 9], 4, logical_prompt_len=10)
     assert plan.source_slots == (0, 1, 2, 7, 8, 9)
@@ -91,6 +124,47 @@ def test_plan_validation():
         plan_in_place([0], [0, 1], 4, logical_prompt_len=8)
     with pytest.raises(ValueError):
         plan_out_of_place([0, 1], [0, 5], 4, [1])
+
+
+def test_in_place_plan_refuses_shared_pages():
+    # kv_compaction_coordinator.py:49-58: pages with ref_count != 1 are never rewritten
+    counts = {4: 1, 6: 2, 8: 1}
+    with pytest.raises(RuntimeError, match=r"prefix-shared blocks; shared_block_ids=\[6\]"):
+        plan_in_place([4, 6, 8], [0, 5], 4, logical_prompt_len=12, ref_counts=counts)
+    with pytest.raises(RuntimeError, match="shared_block_ids=\\[4, 8\\]"):
+        plan_in_place([4, 6, 8], [0, 5], 4, logical_prompt_len=12,
+                      ref_counts=lambda b: 1 if b == 6 else 0)
+    plan = plan_in_place([4, 6, 8], [0, 5], 4, logical_prompt_len=12, ref_counts={4: 1, 6: 1, 8: 1})
+    assert plan.source_slots == (16, 25) and plan.destination_slots == (16, 17)
+    # the out-of-place plan only reads the old pages, so sharing them is allowed
+    assert plan_out_of_place([4, 6], [1], 4, [9]).destination_slots == (36,)
+
+
+def test_plan_validate_catches_tampering():
+    import dataclasses
+
+    plan = plan_in_place([5, 2, 9], [0, 3, 6], 4, logical_prompt_len=9, compacted_logical_len=7)
+    plan.validate(4)
+    bad = {
+        "plan must compact into the existing page-table prefix": dict(new_block_table=(2, 5)),
+        "plan released blocks must be the old page-table suffix": dict(released_block_ids=()),
+        "plan compact block count is inconsistent": dict(new_block_table=(5,)),
+        "plan destination slots are not a dense physical tail": dict(destination_slots=(20, 21, 23)),
+        "physical prompt length must equal source slots": dict(source_slots=(20, 23)),
+        "plan retained positions must be sorted and unique": dict(retained_positions=(0, 6, 3)),
+        "plan retained positions exceed compacted prefix": dict(retained_positions=(0, 3, 7)),
+        "compacted logical prefix is outside prompt bounds": dict(compacted_logical_len=10),
+        "plan source slots do not follow the retained positions": dict(source_slots=(20, 23, 11)),
+    }
+    for message, change in bad.items():
+        with pytest.raises(ValueError, match=message):
+            dataclasses.replace(plan, **change).validate(4)
+    with pytest.raises(ValueError, match="negative block id"):
+        plan_in_place([0, -1], [0], 4, logical_prompt_len=8)
+    with pytest.raises(ValueError, match="names a block twice"):
+        plan_in_place([3, 3], [0], 4, logical_prompt_len=8)
+    with pytest.raises(ValueError, match="names a block twice"):
+        plan_out_of_place([0, 1], [0, 1, 2, 3, 4], 4, [7, 7])
 
 
 def test_out_of_place_plan_is_disjoint():
