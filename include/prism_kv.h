@@ -142,11 +142,24 @@ int prism_paged_decode_split_tokens(int batch, int num_heads, int num_kv_heads, 
  * Kernel family a scaled-FP8 geometry selects: 0 generic, 1 per-split (split-K
  * partials + combine), 2 streaming (tile-balanced persistent kernel + merge).
  * Family 2 additionally needs the canonical dense cache layout at call time
- * (otherwise family 1 runs).  PRISM_DECODE_PATH=split|stream in the
- * environment forces a family where the geometry allows it.
+ * (otherwise family 1 runs).  A forced family (see below) applies where the
+ * geometry allows it.
  */
 int prism_paged_decode_kernel_family(int batch, int num_heads, int num_kv_heads, int head_dim,
                                      int page_size, int max_blocks_per_seq, int cache_dtype);
+
+/*
+ * Process-wide kernel-family overrides (no counterpart in the reference, whose
+ * Triton op has one kernel; used by tests to run every family on the same
+ * inputs).  path: 0 automatic, 1 per-split, 2 streaming; split_tokens: 0
+ * automatic, else tokens per split (rounded up to 32); share: 1 analyse
+ * shared prefixes on the device, 0 treat every page as private.  Initial
+ * values come from PRISM_DECODE_PATH / PRISM_DECODE_SPLIT / PRISM_DECODE_SHARE,
+ * read once at the first call.  No override skips work or changes results
+ * beyond the decode tolerance.
+ */
+int prism_paged_decode_set_overrides(int path, int split_tokens, int share);
+void prism_paged_decode_get_overrides(int out[3]);
 
 /*
  * Physical slot compaction.  Replaces the kernels behind

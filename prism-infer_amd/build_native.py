@@ -66,30 +66,37 @@ EXTRA_FLAGS = {
 }
 
 
-def _compile(src: Path) -> Path:
-    obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [_hipcc(), *HIPCC_FLAGS, *EXTRA_FLAGS.get(src.name, []), f"-I{INCLUDE}", f"-I{CSRC}", "-c", str(src),
-           "-o", str(obj)]
+def _compile(src: Path, build_dir: Path = BUILD_DIR, defines: tuple = ()) -> Path:
+    obj = build_dir / (src.stem + ".o")
+    cmd = [_hipcc(), *HIPCC_FLAGS, *EXTRA_FLAGS.get(src.name, []), *(f"-D{d}" for d in defines), f"-I{INCLUDE}",
+           f"-I{CSRC}", "-c", str(src), "-o", str(obj)]
     proc = subprocess.run(cmd, capture_output=True, text=True)
     if proc.returncode != 0:
         raise RuntimeError(f"hipcc failed for {src.name}:\n{proc.stdout}\n{proc.stderr}")
     return obj
 
 
-def build(verbose: bool = True) -> Path:
-    """Compile all sources and link the shared library; returns its path."""
+def build(verbose: bool = True, *, out_dir: Path = OUT_DIR, measure: bool = False) -> Path:
+    """Compile all sources and link the shared library; returns its path.
 
-    BUILD_DIR.mkdir(exist_ok=True)
-    OUT_DIR.mkdir(parents=True, exist_ok=True)
+    ``measure=True`` builds the measurement variant (PRISM_DECODE_MEASURE:
+    the streaming decode kernel's skip/timestamp switches) into ``out_dir``;
+    the product library never has them.
+    """
+
+    build_dir = BUILD_DIR / ("measure" if measure else "product")
+    build_dir.mkdir(parents=True, exist_ok=True)
+    out_dir.mkdir(parents=True, exist_ok=True)
+    defines = ("PRISM_DECODE_MEASURE",) if measure else ()
     sources = sorted(CSRC.glob("*.hip"))
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")
     workers = min(len(sources), int(os.environ.get("MAX_JOBS", "8")), 8)
     with ThreadPoolExecutor(max_workers=workers) as pool:
-        objects = list(pool.map(_compile, sources))
+        objects = list(pool.map(lambda src: _compile(src, build_dir, defines), sources))
     torch_lib = _torch_lib_dir()
-    out = OUT_DIR / LIB_NAME
-    tmp = OUT_DIR / (LIB_NAME + ".tmp")
+    out = out_dir / LIB_NAME
+    tmp = out_dir / (LIB_NAME + ".tmp")
     # Link with the host compiler against torch's libamdhip64 (see module doc).
     cmd = [
         "g++", "-shared", "-o", str(tmp), *map(str, objects),
@@ -106,7 +113,11 @@ def build(verbose: bool = True) -> Path:
 
 if __name__ == "__main__":
     try:
-        build()
+        if "--measure" in sys.argv[1:]:
+            i = sys.argv.index("--measure")
+            build(out_dir=Path(sys.argv[i + 1]).resolve(), measure=True)
+        else:
+            build()
     except RuntimeError as exc:
         print(exc, file=sys.stderr)
         sys.exit(1)

@@ -27,11 +27,24 @@
 //   kernel merges them; single-split sequences are written directly.
 // Generic path (any other supported shape): one wave per (sequence, q head),
 //   lane-per-token scores, lane-per-dim accumulation, no split-K.
+#include <atomic>
+
 #include "common.h"
 #include "fp8_mfma.h"
 
 namespace prism {
 namespace {
+
+// Measurement aids of the streaming kernel (bit 1: skip compute, 2: skip
+// loads, 4: plan phase stamps, 8: per-workgroup start/end times, 16: default
+// cache policy for private pages) exist only in a build that defines
+// PRISM_DECODE_MEASURE (read from PRISM_STREAM_DEBUG there).  The product
+// library compiles them out: it always loads and computes every tile.
+#ifdef PRISM_DECODE_MEASURE
+#define PRISM_DBG(a) ((a).debug)
+#else
+#define PRISM_DBG(a) 0
+#endif
 
 constexpr float kLog2e = 1.4426950408889634f;
 constexpr int kTile = 32;          // tokens per tile
@@ -999,7 +1012,7 @@ __global__ void __launch_bounds__(kPlanThreads) paged_decode_stream_plan_kernel(
   const bool share = a.share && B <= kSShareMaxBatch && M >= 2 && Wc >= 1;
   const uint64_t t_start = __builtin_amdgcn_s_memtime();
   auto stamp = [&](int k) {  // measurement aid: cycles since start of each phase (debug bit 4)
-    if ((a.debug & 4) && tid == 0) plan[4 + k] = static_cast<int>(__builtin_amdgcn_s_memtime() - t_start);
+    if ((PRISM_DBG(a) & 4) && tid == 0) plan[4 + k] = static_cast<int>(__builtin_amdgcn_s_memtime() - t_start);
   };
 
   // Global memory is only read until the final write-out: a barrier after
@@ -1365,9 +1378,9 @@ paged_decode_stream_kernel(const DecodeArgs a) {
           ld_meta(a.bt + static_cast<int64_t>(ibt_row) * a.bt_sb + static_cast<int64_t>(page) * a.bt_sn);
       iblk = (raw >= 0 && raw < a.num_blocks) ? raw : 0;
     }
-    if (!(a.debug & 2))
+    if (!(PRISM_DBG(a) & 2))
       stream_issue<TPR>(a, pl, t0, iblk, stage0 + static_cast<uint32_t>(issued % kSStages) * kSStage,
-                   ib >= V && !(a.debug & 16));
+                   ib >= V && !(PRISM_DBG(a) & 16));
     ++issued;
     if (++ilt == intl && issued < count) {  // next stream entry with tiles
       do {
@@ -1448,7 +1461,7 @@ paged_decode_stream_kernel(const DecodeArgs a) {
         cok = raw >= 0 && raw < a.num_blocks;
       }
     }
-    if (cok && !(a.debug & 1)) {
+    if (cok && !(PRISM_DBG(a) & 1)) {
       const uint32_t slot = static_cast<uint32_t>(done % kSStages) * kSStage;
       const uint8_t* stp = stages + slot;
       // ---- all LDS reads of the tile first, so their latencies overlap
@@ -1603,7 +1616,7 @@ paged_decode_stream_kernel(const DecodeArgs a) {
       ++lt;
     }
   }
-  if ((a.debug & 8) && threadIdx.x == 0) {  // measurement aid: start and end (100 MHz clock)
+  if ((PRISM_DBG(a) & 8) && threadIdx.x == 0) {  // measurement aid: start and end (100 MHz clock)
     const uint64_t t_end = __builtin_amdgcn_s_memrealtime();
     a.plan[kPlanWgTime + 2 * blockIdx.x] = static_cast<int>(t_begin & 0x7FFFFFFF);
     a.plan[kPlanWgTime + 2 * blockIdx.x + 1] = static_cast<int>(t_end & 0x7FFFFFFF);
@@ -1871,11 +1884,32 @@ struct Geometry {
 // unset, the streaming kernel is used when the batch offers enough tiles to
 // keep every workgroup busy and the per-split kernel otherwise (lower latency
 // for one or a few short sequences).
-int forced_path() {
-  const char* env = getenv("PRISM_DECODE_PATH");
-  if (!env || env[0] != 's') return 0;
-  return env[1] == 'p' ? 1 : (env[1] == 't' ? 2 : 0);  // 1 = split, 2 = stream
+// Kernel-family overrides: PRISM_DECODE_PATH (split|stream), PRISM_DECODE_SPLIT
+// (tokens per split) and PRISM_DECODE_SHARE=0 (no shared-page analysis) are
+// read from the environment once, on the first decode call of the process;
+// prism_paged_decode_set_overrides changes them afterwards (tests run every
+// family on the same inputs).  None of them skips work.
+struct EnvOverrides {
+  std::atomic<int> path{0};   // 0 automatic, 1 split, 2 stream
+  std::atomic<int> split{0};  // 0 automatic, else tokens per split
+  std::atomic<int> share{1};
+};
+
+EnvOverrides& env_overrides() {
+  static EnvOverrides* o = [] {
+    auto* x = new EnvOverrides;
+    const char* p = getenv("PRISM_DECODE_PATH");
+    if (p && p[0] == 's') x->path = p[1] == 'p' ? 1 : (p[1] == 't' ? 2 : 0);
+    const char* sp = getenv("PRISM_DECODE_SPLIT");
+    if (sp) x->split = atoi(sp);
+    const char* sh = getenv("PRISM_DECODE_SHARE");
+    x->share = (sh && sh[0] == '0') ? 0 : 1;
+    return x;
+  }();  // thread-safe one-time initialisation
+  return *o;
 }
+
+int forced_path() { return env_overrides().path.load(); }
 
 bool stream_disabled() { return forced_path() == 1; }
 
@@ -1886,9 +1920,8 @@ bool fast_geometry(int num_heads, int num_kv_heads, int head_dim, int cache_dtyp
 }
 
 int choose_split(int batch, int num_kv_heads, int page_size, int width) {
-  const char* env = getenv("PRISM_DECODE_SPLIT");
-  if (env) {
-    int v = atoi(env);
+  {
+    const int v = env_overrides().split.load();
     if (v >= kTile) return static_cast<int>(align_up(v, kTile));
   }
   const int64_t cap = static_cast<int64_t>(width) * page_size;
@@ -2044,6 +2077,26 @@ int launch_all(int stage, const DecodeArgs& args, const Geometry& geo, bool page
 
 }  // namespace
 }  // namespace prism
+
+extern "C" int prism_paged_decode_set_overrides(int path, int split_tokens, int share) {
+  prism::clear_error();
+  if (path < 0 || path > 2 || split_tokens < 0 || share < 0 || share > 1) {
+    prism::set_error("prism_paged_decode_set_overrides: path must be 0-2, split_tokens >= 0, share 0 or 1");
+    return PRISM_ERR_INVALID;
+  }
+  auto& o = prism::env_overrides();
+  o.path = path;
+  o.split = split_tokens;
+  o.share = share;
+  return PRISM_OK;
+}
+
+extern "C" void prism_paged_decode_get_overrides(int out[3]) {
+  auto& o = prism::env_overrides();
+  out[0] = o.path.load();
+  out[1] = o.split.load();
+  out[2] = o.share.load();
+}
 
 extern "C" int64_t prism_paged_decode_workspace_bytes(int batch, int num_heads, int num_kv_heads, int head_dim,
                                                       int page_size, int max_blocks_per_seq, int cache_dtype) {
@@ -2201,10 +2254,12 @@ extern "C" int prism_paged_decode_stage(
   args.max_splits = geo.fast ? geo.max_splits : 1;
   args.scale_log2 = scale * kLog2e;
   args.cache_dtype = cache_dtype;
+#ifdef PRISM_DECODE_MEASURE
   {
-    const char* dbg = getenv("PRISM_STREAM_DEBUG");  // 1: skip compute, 2: skip loads, 16: default cache policy for private pages
+    const char* dbg = getenv("PRISM_STREAM_DEBUG");
     args.debug = dbg ? atoi(dbg) : 0;
   }
+#endif
   const bool page_aligned = (page_size % kTile) == 0;
   // Streaming path: canonical contiguous page layout with scales.
   // (token rows of num_kv_heads * 128 bytes, contiguous within a page)
@@ -2222,8 +2277,7 @@ extern "C" int prism_paged_decode_stage(
     args.vrow0 = geo.stream_vrow0;
     args.s_tpr = kSKv / num_kv_heads;
     args.s_ttok = kSTile * args.s_tpr;
-    const char* share = getenv("PRISM_DECODE_SHARE");  // "0" turns the shared-page analysis off
-    args.share = !(share && share[0] == '0');
+    args.share = env_overrides().share.load();
     args.stream_nwg = geo.stream_nwg;
   }
   hipStream_t stream = static_cast<hipStream_t>(stream_ptr);

@@ -46,6 +46,8 @@ SIGNATURES: dict[str, tuple] = {
     "prism_paged_decode_workspace_bytes": (_I64, [_I, _I, _I, _I, _I, _I, _I]),
     "prism_paged_decode_split_tokens": (_I, [_I, _I, _I, _I, _I, _I, _I]),
     "prism_paged_decode_kernel_family": (_I, [_I, _I, _I, _I, _I, _I, _I]),
+    "prism_paged_decode_set_overrides": (_I, [_I, _I, _I]),
+    "prism_paged_decode_get_overrides": (None, [ctypes.POINTER(ctypes.c_int)]),
     "prism_paged_decode": (
         _I,
         [_VP, _I, _I64P, _VP, _VP, _I, _I64P, _I64P, _VP, _VP, _I64P, _I64P, _VP, _I64P, _VP, _VP, _VP,

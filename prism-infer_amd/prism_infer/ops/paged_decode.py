@@ -264,5 +264,34 @@ __all__ = [
     "HAS_TRITON",
     "decode_workspace",
     "decode_workspace_bytes",
+    "get_decode_overrides",
     "paged_decode_attention",
+    "set_decode_overrides",
 ]
+
+
+_PATH_CODES = {"auto": 0, "split": 1, "stream": 2}
+
+
+def set_decode_overrides(path: str = "auto", split_tokens: int = 0, share: bool = True) -> None:
+    """Force a decode kernel family for this process (tests, A/B runs).
+
+    ``path``: "auto", "split" or "stream" (where the geometry allows it);
+    ``split_tokens``: 0 for the automatic split-K size; ``share``: False treats
+    every page as private (no device-side prefix-sharing analysis).  Results
+    stay within the decode tolerance whatever is chosen.
+    """
+
+    if path not in _PATH_CODES:
+        raise ValueError(f"path must be one of {sorted(_PATH_CODES)}, got {path!r}")
+    _native.check(_native.lib().prism_paged_decode_set_overrides(_PATH_CODES[path], int(split_tokens), int(share)),
+                  "set_decode_overrides")
+
+
+def get_decode_overrides() -> tuple[str, int, bool]:
+    import ctypes  # noqa: PLC0415
+
+    out = (ctypes.c_int * 3)()
+    _native.lib().prism_paged_decode_get_overrides(out)
+    names = {v: k for k, v in _PATH_CODES.items()}
+    return names[out[0]], int(out[1]), bool(out[2])

@@ -24,3 +24,14 @@ def _oracle_built():
 
     build_oracle()
     yield
+
+
+@pytest.fixture(autouse=True)
+def _reset_decode_overrides():
+    """Every test starts and ends with the automatic decode kernel choice."""
+
+    yield
+    from prism_infer import _native
+
+    if _native.available():
+        _native.lib().prism_paged_decode_set_overrides(0, 0, 1)

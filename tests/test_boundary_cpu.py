@@ -168,3 +168,18 @@ def test_compaction_contract_and_no_cpu_fallback():
         compact_kv_slots(cache[0, 0], src, src)
     with pytest.raises(RuntimeError, match="no CPU fallback"):
         compact_kv_slots(cache, src, torch.tensor([3, 4]))
+
+
+def test_decode_overrides_round_trip():
+    """The family overrides are process state set through the C ABI (no GPU needed)."""
+
+    from prism_infer.ops.paged_decode import get_decode_overrides, set_decode_overrides
+
+    set_decode_overrides(path="split", split_tokens=64, share=False)
+    assert get_decode_overrides() == ("split", 64, False)
+    set_decode_overrides()
+    assert get_decode_overrides() == ("auto", 0, True)
+    with pytest.raises(ValueError):
+        set_decode_overrides(path="fast")
+    with pytest.raises(ValueError):
+        set_decode_overrides(split_tokens=-1)

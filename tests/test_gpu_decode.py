@@ -7,6 +7,8 @@ import math
 import pytest
 import torch
 
+from prism_infer.ops.paged_decode import set_decode_overrides
+
 import oracle
 from _helpers import assert_decode_close, compact_to_cpu, require_gpu
 
@@ -20,7 +22,7 @@ def decode_path(request, monkeypatch):
     """Run a test with the default kernel choice and with each family forced."""
 
     if request.param != "auto":
-        monkeypatch.setenv("PRISM_DECODE_PATH", request.param)
+        set_decode_overrides(path=request.param)
     return request.param
 
 
@@ -237,9 +239,9 @@ def test_long_context_b256_config(monkeypatch):
     run = lambda: paged_decode_attention(w.q, w.k_cache, w.v_cache, w.block_tables, w.context_lens, w.scale,
                                          k_scale_cache=w.k_scale, v_scale_cache=w.v_scale,
                                          max_context_len=w.max_context_len)
-    monkeypatch.setenv("PRISM_DECODE_PATH", "stream")
+    set_decode_overrides(path="stream")
     out_stream = run()
-    monkeypatch.setenv("PRISM_DECODE_PATH", "split")
+    set_decode_overrides(path="split")
     out_split = run()
     torch.cuda.synchronize()
     assert_decode_close(out_stream, out_split, label="decode_long stream vs split")
@@ -364,7 +366,7 @@ def test_shared_prefix_groups(decode_path, monkeypatch):
     assert torch.all(got[22] == 0)
     got_cap = _decode_gpu(q, k, v, ks, vs, tables, lens, 0.0883, max_ctx=700)
     assert_decode_close(got_cap, _oracle(q, k, v, ks, vs, tables, lens, 0.0883, max_ctx=700), label="max_ctx 700")
-    monkeypatch.setenv("PRISM_DECODE_SHARE", "0")
+    set_decode_overrides(path="auto", share=False)
     plain = _decode_gpu(q, k, v, ks, vs, tables, lens, 0.0883)
     assert_decode_close(plain, want, label="sharing analysis off")
 
@@ -377,7 +379,7 @@ def test_large_batch_prefix_groups_deterministic(monkeypatch):
     require_gpu()
     from prism_infer.ops.paged_decode import paged_decode_attention
 
-    monkeypatch.setenv("PRISM_DECODE_PATH", "stream")
+    set_decode_overrides(path="stream")
     g = torch.Generator().manual_seed(20260812)
     batch, width, pool = 128, 20, 2600
     dev = torch.device("cuda")

@@ -20,6 +20,8 @@ import math
 import pytest
 import torch
 
+from prism_infer.ops.paged_decode import set_decode_overrides
+
 import oracle
 from _helpers import assert_decode_close, require_gpu
 
@@ -84,9 +86,9 @@ def test_random_decode_configs_all_families(seed, monkeypatch):
     print(label, flush=True)
     for path in ("auto", "stream", "split"):
         if path == "auto":
-            monkeypatch.delenv("PRISM_DECODE_PATH", raising=False)
+            set_decode_overrides(path="auto")
         else:
-            monkeypatch.setenv("PRISM_DECODE_PATH", path)
+            set_decode_overrides(path=path)
         got = paged_decode_attention(*args, **kw)
         torch.cuda.synchronize()
         assert_decode_close(got, want, label=f"{label} path={path}")
@@ -127,9 +129,9 @@ def test_large_batches_all_families(batch, monkeypatch):
     assert family == (2 if batch <= 1024 else 1), "streaming up to 1024 sequences, per-split beyond"
     for path in ("auto", "split") + (("stream",) if batch <= 1024 else ()):
         if path == "auto":
-            monkeypatch.delenv("PRISM_DECODE_PATH", raising=False)
+            set_decode_overrides(path="auto")
         else:
-            monkeypatch.setenv("PRISM_DECODE_PATH", path)
+            set_decode_overrides(path=path)
         got = paged_decode_attention(*args, **kw)
         torch.cuda.synchronize()
         assert_decode_close(got, want, label=f"B={batch} path={path}")
@@ -170,7 +172,7 @@ def test_fewer_kv_heads_streaming(hkv, hq, monkeypatch):
     args = (to(q), to(k), to(v), to(tables), to(lens), scale)
     kw = dict(k_scale_cache=to(ks), v_scale_cache=to(vs))
     for path in ("stream", "split"):
-        monkeypatch.setenv("PRISM_DECODE_PATH", path)
+        set_decode_overrides(path=path)
         # one kv head makes 128-token tiles: this batch is too small for the
         # automatic choice to stream, so the family is checked as forced
         family = _native.lib().prism_paged_decode_kernel_family(batch, hq, hkv, d, page, width, 3)

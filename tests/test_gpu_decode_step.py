@@ -13,6 +13,8 @@ from __future__ import annotations
 import pytest
 import torch
 
+from prism_infer.ops.paged_decode import set_decode_overrides
+
 import oracle
 from _helpers import assert_decode_close, require_gpu
 
@@ -94,7 +96,7 @@ def test_graph_captured_store_and_decode_replays(path, monkeypatch):
     from prism_infer.engine.decode_attention import PagedKVDecodeAttention, pack_decode_metadata
 
     if path == "stream":
-        monkeypatch.setenv("PRISM_DECODE_PATH", "stream")
+        set_decode_overrides(path="stream")
     g = torch.Generator().manual_seed(20260813)
     batch, width, pool = 8, 6, 64
     k_src = torch.randn(pool, 256, 8, 128, generator=g).to(torch.bfloat16)
