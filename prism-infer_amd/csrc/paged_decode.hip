@@ -608,6 +608,7 @@ constexpr int kSScaleBytes = kSTile * kSKv * 4;         // 512 B of k scales per
 constexpr int kSStage = 2 * kSKBytes + 2 * kSScaleBytes;  // 33792 bytes
 constexpr int kSMaxBatch = 1024;
 constexpr int kSThreads = 64 * kSKv;
+constexpr int kSWaves = kSKv;  // waves per streaming workgroup
 constexpr int kSLoadsPerStage = 5;                      // per lane: 2 K, 2 V, 1 scale
 constexpr float kSRescaleThreshold = 8.0f;              // log2 domain
 // PV is one f16 MFMA per N-tile, with P * v_scale as f16 (2^-11 relative).
@@ -616,6 +617,14 @@ constexpr float kSRescaleThreshold = 8.0f;              // log2 domain
 // P * v_scale by 2^-k and the accumulators by 2^-k before its MFMAs and by
 // 2^k after them, exact powers of two.
 constexpr float kSF16MaxVScale = 255.0f;
+
+// 16-byte LDS reads at a byte address of the LDS aperture.
+__device__ __forceinline__ u32x4 lds_load_b128(uint32_t addr) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) u32x4*>(static_cast<uintptr_t>(addr));
+}
+__device__ __forceinline__ floatx4 lds_load_f4(uint32_t addr) {
+  return *reinterpret_cast<const __attribute__((address_space(3))) floatx4*>(static_cast<uintptr_t>(addr));
+}
 
 __device__ __forceinline__ int stream_swz(int t) { return ((2 * t) + (t >> 2)) & 7; }
 
@@ -684,43 +693,39 @@ __device__ __forceinline__ StreamLanePlan stream_plan(int wave, int lane) {
 // load-to-LDS read at 256 workgroups).  Shared pages, which the virtual
 // sequences of one group each walk, keep the default policy so their
 // re-reads can hit in the caches.
-#define PRISM_STREAM_ISSUE_ASM(POL)                                            \
-  "s_mov_b32 m0, %[lk0]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[k0], off" POL "\n\t" \
-  "s_mov_b32 m0, %[lv0]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v0], off" POL "\n\t" \
-  "s_mov_b32 m0, %[lk1]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[k1], off" POL "\n\t" \
-  "s_mov_b32 m0, %[lv1]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[v1], off" POL "\n\t" \
-  "s_mov_b32 m0, %[ls]\n\ts_nop 0\n\tglobal_load_lds_dword %[sp], off" POL
+// One tile's loads go out as scalar page base + 32-bit per-lane offset (the
+// `saddr` form): the per-lane offsets are loop invariant, so a tile costs
+// three 64-bit scalar adds and no vector address arithmetic.
+#define PRISM_STREAM_ISSUE_ASM(POL)                                                       \
+  "s_mov_b32 m0, %[lk0]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[g0], %[kb]" POL "\n\t"   \
+  "s_mov_b32 m0, %[lv0]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[g0], %[vb]" POL "\n\t"   \
+  "s_mov_b32 m0, %[lk1]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[g1], %[kb]" POL "\n\t"   \
+  "s_mov_b32 m0, %[lv1]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[g1], %[vb]" POL "\n\t"   \
+  "s_mov_b32 m0, %[ls]\n\ts_nop 0\n\tglobal_load_lds_dword %[gs], %[sb]" POL
 
-template <int TPR>
-__device__ __forceinline__ void stream_issue(const DecodeArgs& a, const StreamLanePlan& pl, int t0, int blk,
-                                             uint32_t stage_lds, bool nt) {
-  // off0 is a multiple of the tile's tokens, so a whole number of rows;
-  // token rows are kSRow / TPR bytes and kSKv / TPR scales
-  const int off0 = t0 % a.page_size;
-  const uint8_t* kbase = a.k + blk * a.k_sblk + static_cast<int64_t>(off0) * (kSRow / TPR);
-  const uint8_t* vbase = a.v + blk * a.v_sblk + static_cast<int64_t>(off0) * (kSRow / TPR);
-  const float* sp =
-      (pl.which ? a.vs : a.ks) + blk * a.ks_sblk + static_cast<int64_t>(off0) * (kSKv / TPR) + pl.soff;
-  const uint8_t* k0 = kbase + pl.goff[0];
-  const uint8_t* k1 = kbase + pl.goff[1];
-  const uint8_t* v0 = vbase + pl.goff[0];
-  const uint8_t* v1 = vbase + pl.goff[1];
-  const uint32_t lk0 = __builtin_amdgcn_readfirstlane(stage_lds + pl.lk[0]);
-  const uint32_t lk1 = __builtin_amdgcn_readfirstlane(stage_lds + pl.lk[1]);
+// kb / vb: the tile's first K / V byte; sb: its first scale of this lane's
+// kind (k or v); stage_lds: the stage's LDS address.
+__device__ __forceinline__ void stream_issue(const StreamLanePlan& pl, const uint8_t* kb, const uint8_t* vb,
+                                             const float* sb, uint32_t stage_lds, bool nt) {
+  const uint32_t lk0 = stage_lds + pl.lk[0];
+  const uint32_t lk1 = stage_lds + pl.lk[1];
   const uint32_t lv0 = lk0 + kSKBytes;
   const uint32_t lv1 = lk1 + kSKBytes;
-  const uint32_t ls = __builtin_amdgcn_readfirstlane(stage_lds + pl.ls);
+  const uint32_t ls = stage_lds + pl.ls;
+  const uint32_t g0 = static_cast<uint32_t>(pl.goff[0]);
+  const uint32_t g1 = static_cast<uint32_t>(pl.goff[1]);
+  const uint32_t gs = static_cast<uint32_t>(pl.soff) * 4u;
   if (nt) {  // wave-uniform
     asm volatile(PRISM_STREAM_ISSUE_ASM(" nt")
                  :
-                 : [k0] "v"(k0), [k1] "v"(k1), [v0] "v"(v0), [v1] "v"(v1), [sp] "v"(sp), [lk0] "s"(lk0),
-                   [lk1] "s"(lk1), [lv0] "s"(lv0), [lv1] "s"(lv1), [ls] "s"(ls)
+                 : [g0] "v"(g0), [g1] "v"(g1), [gs] "v"(gs), [kb] "s"(kb), [vb] "s"(vb), [sb] "s"(sb),
+                   [lk0] "s"(lk0), [lk1] "s"(lk1), [lv0] "s"(lv0), [lv1] "s"(lv1), [ls] "s"(ls)
                  : "memory", "m0");
   } else {
     asm volatile(PRISM_STREAM_ISSUE_ASM("")
                  :
-                 : [k0] "v"(k0), [k1] "v"(k1), [v0] "v"(v0), [v1] "v"(v1), [sp] "v"(sp), [lk0] "s"(lk0),
-                   [lk1] "s"(lk1), [lv0] "s"(lv0), [lv1] "s"(lv1), [ls] "s"(ls)
+                 : [g0] "v"(g0), [g1] "v"(g1), [gs] "v"(gs), [kb] "s"(kb), [vb] "s"(vb), [sb] "s"(sb),
+                   [lk0] "s"(lk0), [lk1] "s"(lk1), [lv0] "s"(lv0), [lv1] "s"(lv1), [ls] "s"(ls)
                  : "memory", "m0");
   }
 }
@@ -910,8 +915,10 @@ constexpr int kPlanWgTime = kPlanVrot + kSMaxVirt;         // measurement aid: p
 // inputs equal the key left by the previous call on the same workspace keeps
 // that plan (every layer of a decode step has the same metadata).
 // Per real sequence b, 8 ints at kPlanRec + 8 b: first and end tile of its
-// own stream entry, its virtual slot (or -1), and first and end tile of its
-// virtual sequence: what the merge needs, at an offset independent of V.
+// own stream entry, its virtual slot (or -1), first and end tile of its
+// virtual sequence, and the number of partial flushes its output waits for
+// (workgroups meeting its own tiles plus those meeting its virtual
+// sequence's): what the merge needs, at an offset independent of V.
 constexpr int kPlanRec = kPlanWgTime + 2 * kSMaxWg;
 // Per streaming workgroup w, 8 ints at kPlanWgRec + 8 w: where its range
 // starts (stream entry, tile within it, the entry's tile count, block-table
@@ -926,7 +933,13 @@ constexpr int kPlanKey = kPlanWgRec + 8 * kSMaxWg;
 constexpr int kPlanKeyParams = 12;
 constexpr int kPlanKeyEff = kPlanKey + kPlanKeyParams;       // attended lengths
 constexpr int kPlanKeyBt = kPlanKeyEff + kSMaxBatch;         // compared block-table prefix
-constexpr int kPlanInts = kPlanKeyBt + kSShareMaxBatch * kPlanMaxPages;
+// Per real sequence b, one int at kPlanCnt + b: how many workgroups have
+// flushed a partial that sequence's output depends on in the running call.
+// The plan kernel zeroes them whenever it computes a plan; the workgroup whose
+// flush completes a sequence merges it and sets the counter back to 0, so a
+// call that reuses the plan finds them at zero.
+constexpr int kPlanCnt = kPlanKeyBt + kSShareMaxBatch * kPlanMaxPages;
+constexpr int kPlanInts = kPlanCnt + kSMaxBatch + kSMaxWg;  // + measurement aid: finish times
 constexpr int kPlanMagic = 0x504C414E;
 constexpr int kPlanThreads = 1024;
 constexpr int kPlanHashBits = 10;
@@ -954,6 +967,18 @@ __device__ __forceinline__ int64_t split_begin(const StreamSplit& sp, int64_t w)
 // split_begin(w) <= t, i.e. ceil((t + 1) * nwg / total) - 1.
 __device__ __forceinline__ int64_t split_owner(const StreamSplit& sp, int64_t t) {
   return ((t + 1) * sp.nwg + sp.total - 1) / sp.total - 1;
+}
+
+// Number of streaming workgroups whose ranges meet tiles [first, end) of a
+// stream of `total` tiles split over nwg workgroups: each such workgroup
+// flushes one partial for that tile range.  With total >= nwg every range is
+// non-empty and the owners of first and end - 1 bound them; with fewer tiles
+// than workgroups every range holds at most one tile.
+__device__ __forceinline__ int stream_owner_count(int first, int end, int total, int nwg) {
+  if (end <= first) return 0;
+  if (total < nwg) return end - first;
+  const StreamSplit sp{total, nwg};
+  return static_cast<int>(split_owner(sp, end - 1) - split_owner(sp, first)) + 1;
 }
 
 // Inclusive prefix sum over the workgroup (every thread calls it): shuffles
@@ -1213,9 +1238,14 @@ __global__ void __launch_bounds__(kPlanThreads) paged_decode_stream_plan_kernel(
     plan[kPlanVslot + tid] = vslot_s[tid];
     const int vs = vslot_s[tid];
     const int v = vs >= 0 ? vs / kSCols : 0;
+    const int first = tst_s[V + tid], end = tst_s[V + tid + 1];
+    const int vfirst = vs >= 0 ? tst_s[v] : 0, vend = vs >= 0 ? tst_s[v + 1] : 0;
+    const int expect = stream_owner_count(first, end, carry, a.stream_nwg) +
+                       stream_owner_count(vfirst, vend, carry, a.stream_nwg);
     int4* rec = reinterpret_cast<int4*>(plan + kPlanRec + 8 * tid);
-    rec[0] = int4{tst_s[V + tid], tst_s[V + tid + 1], vs, vs >= 0 ? tst_s[v] : 0};
-    rec[1] = int4{vs >= 0 ? tst_s[v + 1] : 0, 0, 0, 0};
+    rec[0] = int4{first, end, vs, vfirst};
+    rec[1] = int4{vend, expect, 0, 0};
+    plan[kPlanCnt + tid] = 0;
   }
   for (int i = tid; i < V * kSCols; i += kPlanThreads) plan[kPlanVmem + i] = vmem_s[i];
   if (tid < V) {
@@ -1315,6 +1345,184 @@ __device__ __forceinline__ void stream_column(const DecodeArgs& a, int V, int i,
   qhead = h * G + (valid ? qh : 0);
 }
 
+// Partials cross workgroups (and XCDs, whose L2 caches are not coherent with
+// each other) inside one launch.  They are written with device-scope stores
+// (sc1: written through to the device-coherent level) and read back with
+// device-scope loads (sc1 buffer loads), so neither side needs a cache-wide
+// writeback or invalidate.  A flush is counted only after the writer's
+// stores have completed (s_waitcnt vmcnt(0)), and the merging workgroup
+// loads the partials only after the counter told it every flush is in.
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+constexpr int kCoherentLoad = 16;  // buffer-load cache policy: sc1 (device scope)
+
+__device__ __forceinline__ floatx4 load_coherent4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(byte_off), 0, kCoherentLoad);
+  return floatx4{__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3])};
+}
+
+__device__ __forceinline__ float2 load_coherent2(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(byte_off), 0, kCoherentLoad);
+  return float2{__uint_as_float(v[0]), __uint_as_float(v[1])};
+}
+
+// Output of real sequence b from the streaming partials, by the whole
+// workgroup: thread t owns q head t / 16 and dims 8 (t % 16) .. + 7 (the
+// partial layout is covered for up to 32 q heads per pass).  The candidates
+// are the (workgroup, token slot) pairs whose workgroups met b's own tiles or
+// its virtual sequence's tiles; their rows follow the layout the streaming
+// kernel writes (real entry e of workgroup w at (w + e) * 8G + slot * G +
+// column; virtual entry v at vrow0 + ((w + v) * 8 + slot) * 16 + column).  A
+// partial with m = -inf attended nothing and weighs 0.  Eight candidates are
+// loaded per round, (m, l) and 32 accumulator bytes each, with a running
+// maximum across rounds; the usual sequence has at most eight, so its merge
+// is one round of loads.  `rec` is b's plan record (first, end, virtual slot,
+// virtual first, virtual end).
+template <int QDT, int TPR>
+__device__ __forceinline__ void stream_merge_seq(const DecodeArgs& a, int V, int b, const int* rec,
+                                                 const StreamSplit& sp) {
+  constexpr int tl = TPR == 1 ? 0 : (TPR == 2 ? 1 : (TPR == 4 ? 2 : 3));  // log2 of the token slots
+  constexpr int hkv = kSKv / TPR;
+  constexpr int kU = 8;
+  const int first = rec[0], end = rec[1], vslot = rec[2], vfirst = rec[3], vend = rec[4];
+  int lo0 = 0, cnt0 = 0, lo1 = 0, cnt1 = 0;
+  if (end > first) {
+    lo0 = static_cast<int>(split_owner(sp, first));
+    cnt0 = static_cast<int>(split_owner(sp, end - 1)) - lo0 + 1;
+  }
+  if (vslot >= 0) {
+    lo1 = static_cast<int>(split_owner(sp, vfirst));
+    cnt1 = static_cast<int>(split_owner(sp, vend - 1)) - lo1 + 1;
+  }
+  const int cnt = (cnt0 + cnt1) << tl;
+  const int d0 = 8 * (threadIdx.x & 15);
+  // whole-region resources (the partial region is far below 4 GiB)
+  const __amdgpu_buffer_rsrc_t acc_r = __builtin_amdgcn_make_buffer_rsrc(a.part_acc, 0, 0x7FFFFFFF, 0x00020000);
+  const __amdgpu_buffer_rsrc_t ml_r = __builtin_amdgcn_make_buffer_rsrc(a.part_ml, 0, 0x7FFFFFFF, 0x00020000);
+  for (int hq = threadIdx.x >> 4; hq < a.num_heads; hq += kSThreads / 16) {
+    const int64_t rbase0 = static_cast<int64_t>(V + b) * (kSKv * a.groups) + hq;
+    int64_t rbase1 = 0;
+    if (vslot >= 0) {
+      const int v = vslot / kSCols;
+      const int m = vslot - v * kSCols;
+      const int hk = hq / a.groups;
+      rbase1 = a.vrow0 + (static_cast<int64_t>(v) * kSKv + hk) * kSCols + m * a.groups + (hq - hk * a.groups);
+    }
+    float m_run = -INFINITY, l_sum = 0.f;
+    float o[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) o[j] = 0.f;
+    for (int base = 0; base < cnt; base += kU) {
+      float mv[kU], lv[kU];
+      floatx4 x0[kU], x1[kU];
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const int i = min(base + u, cnt - 1);
+        const int wi = i >> tl;
+        const int sl = i & ((1 << tl) - 1);
+        const bool second = wi >= cnt0;
+        const int64_t w = second ? lo1 + (wi - cnt0) : lo0 + wi;
+        const int64_t row = second ? rbase1 + w * (kSKv * kSCols) + sl * (hkv * kSCols)
+                                   : rbase0 + w * (kSKv * a.groups) + sl * a.num_heads;
+        // a workgroup with an empty range (fewer tiles than workgroups) wrote nothing
+        const bool ok = base + u < cnt && split_begin(sp, w) < split_begin(sp, w + 1);
+        const float2 ml = load_coherent2(ml_r, static_cast<uint32_t>(row * 8));
+        const uint32_t off = static_cast<uint32_t>((row * kHeadDim + d0) * 4);
+        x0[u] = load_coherent4(acc_r, off);
+        x1[u] = load_coherent4(acc_r, off + 16);
+        mv[u] = ok ? ml.x : -INFINITY;
+        lv[u] = ok ? ml.y : 0.f;
+      }
+      float mx = m_run;
+#pragma unroll
+      for (int u = 0; u < kU; ++u) mx = fmaxf(mx, mv[u]);
+      if (mx == -INFINITY) continue;  // nothing attended so far
+      const float alpha = exp2f(m_run - mx);  // 0 while m_run = -inf
+      l_sum *= alpha;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] *= alpha;
+#pragma unroll
+      for (int u = 0; u < kU; ++u) {
+        const float wgt = mv[u] == -INFINITY ? 0.f : exp2f(mv[u] - mx);  // rows with m = -inf weigh 0
+        l_sum += wgt * lv[u];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          o[j] += wgt * (wgt != 0.f ? x0[u][j] : 0.f);
+          o[4 + j] += wgt * (wgt != 0.f ? x1[u][j] : 0.f);
+        }
+      }
+      m_run = mx;
+    }
+    const float inv = l_sum > 0.f ? 1.f / l_sum : 0.f;
+    const int64_t obase = static_cast<int64_t>(b) * a.o_sb + static_cast<int64_t>(hq) * a.o_sh;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) store_out<QDT>(a.out, obase + (d0 + j) * a.o_sd, o[j] * inv);
+  }
+}
+
+// End of a streaming workgroup's range.  Every wave has written the partials
+// of the stream entries [e_first, e_first + nent) it met (nent = 0: an empty
+// range).  Each flush is counted on the sequences it serves (a virtual entry
+// serves each of its members); the workgroup whose count completes a
+// sequence merges that sequence's output and resets its counter.  Sequences
+// that attend no token at all (no tiles, no flushes) get zeros from
+// workgroup b % nwg.  `scratch` is LDS no longer in use (the drained stages).
+template <int QDT, int TPR>
+__device__ __forceinline__ void stream_finish(const DecodeArgs& a, int V, const int* tstart, int e_first, int nent,
+                                              int* scratch) {
+  constexpr int kRec = 5;
+  int* n_merge = scratch;
+  int* merge_rec = scratch + 4;  // per merged sequence: b, then its 5-int plan record (stride 8)
+  // this wave's partial stores have completed (device scope): the flushes may be counted
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  if (threadIdx.x == 0) *n_merge = 0;
+  __syncthreads();
+  int* cnt = a.plan + kPlanCnt;
+  const int members = kSCols / a.groups;
+  for (int t = threadIdx.x; t < nent * kSCols; t += kSThreads) {
+    const int i = e_first + t / kSCols;
+    const int slot = t - (t / kSCols) * kSCols;
+    if (tstart[i + 1] == tstart[i]) continue;  // no tiles: never flushed
+    int seq = -1;
+    if (i >= V) seq = slot == 0 ? i - V : -1;
+    else if (slot < members) seq = a.plan[kPlanVmem + i * kSCols + slot];
+    if (seq < 0) continue;
+    const int4 r0 = *reinterpret_cast<const int4*>(a.plan + kPlanRec + 8 * seq);
+    const int2 r1 = *reinterpret_cast<const int2*>(a.plan + kPlanRec + 8 * seq + 4);  // virtual end, expected
+    const int prev = __hip_atomic_fetch_add(cnt + seq, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (prev + 1 == r1.y) {
+      __hip_atomic_store(cnt + seq, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      int* e = merge_rec + 8 * atomicAdd(n_merge, 1);
+      e[0] = seq;
+      e[1] = r0.x;
+      e[2] = r0.y;
+      e[3] = r0.z;
+      e[4] = r0.w;
+      e[5] = r1.x;
+    }
+  }
+  // zeros for sequences without a single partial
+  for (int b = blockIdx.x; b < a.batch; b += a.stream_nwg) {
+    if (a.plan[kPlanRec + 8 * b + 5] != 0) continue;  // uniform
+    for (int e = threadIdx.x; e < a.num_heads * kHeadDim; e += kSThreads) {
+      const int hq = e / kHeadDim;
+      const int d = e - hq * kHeadDim;
+      store_out<QDT>(a.out, static_cast<int64_t>(b) * a.o_sb + static_cast<int64_t>(hq) * a.o_sh + d * a.o_sd, 0.f);
+    }
+  }
+  __syncthreads();
+  const int nm = *n_merge;
+  if (nm == 0) return;
+  const StreamSplit sp = stream_split(a, a.plan[1]);
+  for (int k = 0; k < nm; ++k) {
+    const int* e = merge_rec + 8 * k;
+    stream_merge_seq<QDT, TPR>(a, V, e[0], e + 1, sp);
+  }
+  static_assert(kRec + 1 <= 8, "merge record stride");
+}
+
 // kSWgPerCu 8-wave workgroups per CU need 2 * kSWgPerCu waves per SIMD.
 template <int QDT, bool QVEC, int TPR>
 __global__ void __launch_bounds__(kSThreads) __attribute__((amdgpu_waves_per_eu(2 * kSWgPerCu)))
@@ -1323,7 +1531,7 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t stages[kSStages * kSStage];
   __shared__ int tstart[kSMaxBatch + kSMaxVirt + 1];
   const int lane = threadIdx.x & 63;
-  const int h = threadIdx.x >> 6;
+  const int h = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // head slot of this wave (uniform)
   const int g = lane >> 4;
   const int c = lane & 15;
   const int B = a.batch;
@@ -1341,72 +1549,108 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   const StreamSplit sp = stream_split(a, total);
   const int64_t s = split_begin(sp, blockIdx.x);
   const int64_t e = split_begin(sp, blockIdx.x + 1);
-  if (s >= e) return;  // uniform across the workgroup
   __syncthreads();
+  if (s >= e) {  // uniform: an empty range flushes nothing
+    stream_finish<QDT, TPR>(a, V, tstart, 0, 0, reinterpret_cast<int*>(stages));
+    return;
+  }
   const uint64_t t_begin = __builtin_amdgcn_s_memrealtime();
 
   const StreamLanePlan pl = stream_plan(h, lane);
   const uint32_t stage0 = lds_addr(stages);
-  const int64_t count = e - s;
+  const int count = static_cast<int>(e - s);
+  const int P = a.page_size;
+  const int tpp = P / kTTok;  // tiles per page (the streaming shape has P % kTTok == 0)
+  const float* sbase = pl.which ? a.vs : a.ks;  // wave-uniform: the scales this wave's lanes load
 
-  // ---- issue-side tile iterator: stream entry ib, local tile ilt of intl
-  // tiles; the block id is re-read only when the page changes.
-  int ib = __builtin_amdgcn_readfirstlane(wr0.x);
-  int ilt = __builtin_amdgcn_readfirstlane(wr0.y);
-  int intl = __builtin_amdgcn_readfirstlane(wr0.z);
-  int ibt_row = __builtin_amdgcn_readfirstlane(wr0.w);
-  int itok0 = __builtin_amdgcn_readfirstlane(wr1.x);
-  int iend = __builtin_amdgcn_readfirstlane(wr1.y);
-  int irot = __builtin_amdgcn_readfirstlane(wr1.z);
-  const int first_raw = __builtin_amdgcn_readfirstlane(wr1.w);
-  int first_page;
-  {
-    const int lr = ilt + irot;
-    first_page = (itok0 + (lr >= intl ? lr - intl : lr) * kTTok) / a.page_size;
-  }
-  // the first page's block id comes from the record when the plan could cache it
-  int ipage = first_raw != kNoBlock ? first_page : -1;
-  int iblk = (first_raw >= 0 && first_raw < a.num_blocks) ? first_raw : 0;
-  int64_t issued = 0;
+  // ---- issue side: walks this workgroup's tiles kSStages - 1 ahead of the
+  // compute side.  Per stream entry: physical tile pt of ntl (virtual walks
+  // start at a rotation and wrap), tile-in-page tip, and the scalar addresses
+  // of the tile's K, V and scale rows, advanced by constants; the block id
+  // is read only when the page changes.  Per stage it records for the
+  // compute side how many of the tile's tokens are attended (0: the block id
+  // is invalid, skip the tile).
+  int ie = __builtin_amdgcn_readfirstlane(wr0.x);
+  int ileft, intl, ipt, itip, ipage, ipage0, irow, it0, itok0, iend;
+  const uint8_t* ikb;
+  const uint8_t* ivb;
+  const float* isb;
+  bool ivalid;
+  uint32_t stage_nv = 0;  // byte s: attended tokens of the tile in stage s
+  auto ipage_set = [&](int raw_or_load) {
+    // raw_or_load: a block id already known, or kNoBlock to read it
+    int raw = raw_or_load;
+    if (raw == kNoBlock)
+      raw = ld_meta(a.bt + static_cast<int64_t>(irow) * a.bt_sb + static_cast<int64_t>(ipage) * a.bt_sn);
+    ivalid = raw >= 0 && raw < a.num_blocks;
+    const int64_t blk = ivalid ? raw : 0;  // loads of an invalid block read page 0 and are skipped
+    const int64_t tip_rows = static_cast<int64_t>(itip) * kSTile;
+    ikb = a.k + blk * a.k_sblk + tip_rows * kSRow;
+    ivb = a.v + blk * a.v_sblk + tip_rows * kSRow;
+    isb = sbase + blk * a.ks_sblk + tip_rows * kSKv;
+  };
+  auto ientry = [&](int lt, int first_raw) {
+    intl = __builtin_amdgcn_readfirstlane(tstart[ie + 1] - tstart[ie]);
+    int rot;
+    stream_seq<TPR>(a, tstart, V, ie, irow, itok0, iend, rot);
+    irow = __builtin_amdgcn_readfirstlane(irow);
+    itok0 = __builtin_amdgcn_readfirstlane(itok0);
+    iend = __builtin_amdgcn_readfirstlane(iend);
+    rot = __builtin_amdgcn_readfirstlane(rot);
+    ileft = intl - lt;
+    ipt = lt + rot;
+    if (ipt >= intl) ipt -= intl;
+    it0 = itok0 + ipt * kTTok;
+    ipage = it0 / P;
+    itip = (it0 - ipage * P) / kTTok;
+    ipage0 = itok0 / P;
+    ipage_set(first_raw);
+  };
+  ientry(__builtin_amdgcn_readfirstlane(wr0.y), __builtin_amdgcn_readfirstlane(wr1.w));
+  int issued = 0;
+  int istage = 0;
   auto issue_next = [&]() {
-    const int lr = ilt + irot;
-    const int t0 = itok0 + (lr >= intl ? lr - intl : lr) * kTTok;
-    const int page = __builtin_amdgcn_readfirstlane(t0 / a.page_size);
-    if (page != ipage) {
-      ipage = page;
-      const int32_t raw =
-          ld_meta(a.bt + static_cast<int64_t>(ibt_row) * a.bt_sb + static_cast<int64_t>(page) * a.bt_sn);
-      iblk = (raw >= 0 && raw < a.num_blocks) ? raw : 0;
-    }
+    const int nv = ivalid ? min(iend - it0, kTTok) : 0;
+    stage_nv = (stage_nv & ~(0xFFu << (8 * istage))) | (static_cast<uint32_t>(nv) << (8 * istage));
     if (!(PRISM_DBG(a) & 2))
-      stream_issue<TPR>(a, pl, t0, iblk, stage0 + static_cast<uint32_t>(issued % kSStages) * kSStage,
-                   ib >= V && !(PRISM_DBG(a) & 16));
+      stream_issue(pl, ikb, ivb, isb, stage0 + static_cast<uint32_t>(istage) * kSStage,
+                   ie >= V && !(PRISM_DBG(a) & 16));
     ++issued;
-    if (++ilt == intl && issued < count) {  // next stream entry with tiles
+    istage = istage == kSStages - 1 ? 0 : istage + 1;
+    if (issued == count) return;  // the range is done (no page past it is read)
+    if (--ileft == 0) {  // the entry is done: the next one with tiles
       do {
-        ++ib;
-        intl = __builtin_amdgcn_readfirstlane(tstart[ib + 1] - tstart[ib]);
-      } while (intl == 0 && ib + 1 < NS);
-      ib = __builtin_amdgcn_readfirstlane(ib);
-      ilt = 0;
-      ipage = -1;
-      stream_seq<TPR>(a, tstart, V, ib, ibt_row, itok0, iend, irot);
+        ++ie;
+      } while (tstart[ie + 1] == tstart[ie] && ie + 1 < NS);
+      ie = __builtin_amdgcn_readfirstlane(ie);
+      ientry(0, kNoBlock);
+      return;
+    }
+    ++ipt;
+    it0 += kTTok;
+    ++itip;
+    ikb += kSKBytes;
+    ivb += kSKBytes;
+    isb += kSTile * kSKv;
+    if (ipt == intl) {  // a rotated walk wraps to the entry's first tile
+      ipt = 0;
+      it0 = itok0;
+      ipage = ipage0;
+      itip = 0;
+      ipage_set(kNoBlock);
+    } else if (itip == tpp) {
+      ++ipage;
+      itip = 0;
+      ipage_set(kNoBlock);
     }
   };
 #pragma unroll
   for (int i = 0; i < kSStages - 1; ++i)
     if (issued < count) issue_next();
 
-  // ---- compute-side iterator (same walk, one tile behind), from the same record
+  // ---- compute side: entry b, tiles left in it for this workgroup
   int b = __builtin_amdgcn_readfirstlane(wr0.x);
-  int lt = __builtin_amdgcn_readfirstlane(wr0.y);
-  int ntl = __builtin_amdgcn_readfirstlane(wr0.z);
-  int cbt_row = __builtin_amdgcn_readfirstlane(wr0.w);
-  int ctok0 = __builtin_amdgcn_readfirstlane(wr1.x);
-  int n_eff = __builtin_amdgcn_readfirstlane(wr1.y);
-  int crot = __builtin_amdgcn_readfirstlane(wr1.z);
-  int cpage = first_raw != kNoBlock ? first_page : -1;
-  int cok = first_raw >= 0 && first_raw < a.num_blocks;
+  int cleft = min(__builtin_amdgcn_readfirstlane(wr0.z) - __builtin_amdgcn_readfirstlane(wr0.y), count);
   QOperandF8 qop;
   bool colv;
   {
@@ -1421,10 +1665,10 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   float m_run = -INFINITY;  // running max (log2 domain) of query column c
   float l_run = 0.f;        // this lane's share of the running sum
 
-  // Per-lane LDS offsets inside a stage (loop invariant).
-  const uint32_t k_off0 = c * kSRow + h * kHeadDim + (((2 * g) ^ stream_swz(c)) << 4);
-  const uint32_t k_off1 = c * kSRow + h * kHeadDim + (((2 * g + 1) ^ stream_swz(c)) << 4);
-  const uint32_t s_off = 2 * kSKBytes + (h * kSTile + 4 * g) * 4;
+  // Per-lane LDS addresses inside stage 0 (loop invariant).
+  const uint32_t k_off0 = stage0 + c * kSRow + h * kHeadDim + (((2 * g) ^ stream_swz(c)) << 4);
+  const uint32_t k_off1 = stage0 + c * kSRow + h * kHeadDim + (((2 * g + 1) ^ stream_swz(c)) << 4);
+  const uint32_t s_off = stage0 + 2 * kSKBytes + (h * kSTile + 4 * g) * 4;
   uint32_t v_off[4];
   {
     const int r = c >> 1;              // row of the 8x16 byte matrix this lane addresses
@@ -1433,76 +1677,72 @@ paged_decode_stream_kernel(const DecodeArgs a) {
 #pragma unroll
     for (int jp = 0; jp < 4; ++jp) {
       const int chunk = 2 * jp + (r >> 2);
-      v_off[jp] = kSKBytes + t * kSRow + h * kHeadDim + ((chunk ^ stream_swz(t)) << 4) + half * 8;
+      v_off[jp] = stage0 + kSKBytes + t * kSRow + h * kHeadDim + ((chunk ^ stream_swz(t)) << 4) + half * 8;
     }
   }
+  // first token this lane's score rows refer to, relative to the tile:
+  // row 4g + i of this wave's slot is token TPR * (4g + i) + h / Hkv
+  const int tok_lane = TPR * 4 * g + h / (kSKv / TPR);
 
-  for (int64_t done = 0; done < count; ++done) {
+  int cstage = 0;
+  for (int done = 0; done < count; ++done) {
     // Wait for this tile's loads (the younger tiles' loads may stay in flight),
     // then one barrier: every wave's loads have landed and every wave has
     // finished the previous tile, whose stage the refill below reuses.
-    const int64_t younger = issued - done - 1;
-    static_assert(kSStages >= 2 && kSStages <= 4, "wait table covers 1..3 younger tiles");
-    if (kSStages > 3 && younger >= 3) __builtin_amdgcn_s_waitcnt(0xF70 | (3 * kSLoadsPerStage));
-    else if (kSStages > 2 && younger >= 2) __builtin_amdgcn_s_waitcnt(0xF70 | (2 * kSLoadsPerStage));
-    else if (younger >= 1) __builtin_amdgcn_s_waitcnt(0xF70 | (1 * kSLoadsPerStage));
-    else __builtin_amdgcn_s_waitcnt(0xF70);
+    static_assert(kSStages == 4, "wait counts below assume three tiles in flight");
+    if (done + 3 < count) {  // steady state: three younger tiles in flight
+      __builtin_amdgcn_s_waitcnt(0xF70 | (3 * kSLoadsPerStage));
+    } else {
+      const int younger = count - done - 1;
+      if (younger == 2) __builtin_amdgcn_s_waitcnt(0xF70 | (2 * kSLoadsPerStage));
+      else if (younger == 1) __builtin_amdgcn_s_waitcnt(0xF70 | (1 * kSLoadsPerStage));
+      else __builtin_amdgcn_s_waitcnt(0xF70);
+    }
     stream_barrier();
+    const int nv = __builtin_amdgcn_readfirstlane((stage_nv >> (8 * cstage)) & 0xFF);
     if (issued < count) issue_next();
 
-    const int lr = lt + crot;
-    const int t0 = ctok0 + (lr >= ntl ? lr - ntl : lr) * kTTok;
-    {
-      const int page = __builtin_amdgcn_readfirstlane(t0 / a.page_size);
-      if (page != cpage) {
-        cpage = page;
-        const int32_t raw =
-            ld_meta(a.bt + static_cast<int64_t>(cbt_row) * a.bt_sb + static_cast<int64_t>(page) * a.bt_sn);
-        cok = raw >= 0 && raw < a.num_blocks;
-      }
-    }
-    if (cok && !(PRISM_DBG(a) & 1)) {
-      const uint32_t slot = static_cast<uint32_t>(done % kSStages) * kSStage;
-      const uint8_t* stp = stages + slot;
+    if (nv != 0 && !(PRISM_DBG(a) & 1)) {
+      const uint32_t slot = static_cast<uint32_t>(cstage) * kSStage;
       // ---- all LDS reads of the tile first, so their latencies overlap
-      const u32x4 k0 = *reinterpret_cast<const u32x4*>(stp + k_off0);
-      const u32x4 k1 = *reinterpret_cast<const u32x4*>(stp + k_off1);
-      const floatx4 ks = *reinterpret_cast<const floatx4*>(stp + s_off);
-      const floatx4 vs = *reinterpret_cast<const floatx4*>(stp + s_off + kSScaleBytes);
+      const u32x4 k0 = lds_load_b128(k_off0 + slot);
+      const u32x4 k1 = lds_load_b128(k_off1 + slot);
+      const floatx4 ks = lds_load_f4(s_off + slot);
+      const floatx4 vs = lds_load_f4(s_off + slot + kSScaleBytes);
       uint32_t ad[4];
 #pragma unroll
-      for (int jp = 0; jp < 4; ++jp) ad[jp] = stage0 + slot + v_off[jp];
+      for (int jp = 0; jp < 4; ++jp) ad[jp] = v_off[jp] + slot;
       uint64_t vt[4];
       lds_read_tr8_x4(ad, vt);
       // ---- QK over 16 tokens: the K bytes are the fp8 MFMA's A operand as
-      // they are (row = token c, k = dims 32g..32g+31); smallest term first.
+      // they are (row = token c, k = dims 32g..32g+31).  The three query
+      // terms go to independent accumulators (no dependent MFMA chain) and
+      // are summed smallest first.
       const i32x8 ka = {static_cast<int>(k0[0]), static_cast<int>(k0[1]), static_cast<int>(k0[2]),
                         static_cast<int>(k0[3]), static_cast<int>(k1[0]), static_cast<int>(k1[1]),
                         static_cast<int>(k1[2]), static_cast<int>(k1[3])};
-      floatx4 sc = {0.f, 0.f, 0.f, 0.f};
-      sc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, qop.t[2], sc, 0, 0, 0, 0, 0, 0);
-      sc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, qop.t[1], sc, 0, 0, 0, 0, 0, 0);
-      sc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, qop.t[0], sc, 0, 0, 0, 0, 0, 0);
+      const floatx4 zero4 = {0.f, 0.f, 0.f, 0.f};
+      const floatx4 s2 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, qop.t[2], zero4, 0, 0, 0, 0, 0, 0);
+      const floatx4 s1 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, qop.t[1], zero4, 0, 0, 0, 0, 0, 0);
+      const floatx4 s0 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, qop.t[0], zero4, 0, 0, 0, 0, 0, 0);
       // ---- scores in the log2 domain.  Query columns without a query hold
       // q = 0, so their scores are finite and their rows are never written.
       float x[4];
       float vsm[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        x[i] = sc[i] * (ks[i] * qop.colscale);
+        x[i] = ((s2[i] + s1[i]) + s0[i]) * (ks[i] * qop.colscale);
         vsm[i] = vs[i];
       }
       // Only a sequence's last tile can reach past its end (uniform branch).
       // Masked slots get score -inf (weight 0) and v scale 0, and their V
       // bytes are zeroed: rows past the end may hold anything, and the MFMA
       // would turn 0 * NaN into NaN.
-      if (t0 + kTTok > n_eff) {
-        // row 4g + i of this wave's slot is token t0 + tpr * (4g + i) + h / Hkv
-        const int tok_g = t0 + TPR * 4 * g + h / (kSKv / TPR);
+      if (nv < kTTok) {
         uint32_t keep = 0;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const bool tv = tok_g + TPR * i < n_eff;
+          const bool tv = tok_lane + TPR * i < nv;
           x[i] = tv ? x[i] : -INFINITY;
           vsm[i] = tv ? vsm[i] : 0.f;
           keep |= tv ? (0xFFu << (8 * i)) : 0u;
@@ -1566,11 +1806,11 @@ paged_decode_stream_kernel(const DecodeArgs a) {
         for (int j = 0; j < 8; ++j) acc[j] *= up;
       }
     }
+    cstage = cstage == kSStages - 1 ? 0 : cstage + 1;
 
-    // ---- advance the compute iterator; flush at the end of a stream entry
-    const bool more = done + 1 < count;
-    const bool seq_ends = !more || lt + 1 == ntl;
-    if (seq_ends) {
+    // ---- flush at the end of a stream entry (or of this workgroup's range)
+    if (--cleft == 0 || done + 1 == count) {
+      const bool more = done + 1 < count;
       float l_tot = l_run + __shfl_xor(l_run, 16);
       l_tot += __shfl_xor(l_tot, 32);
       // partial rows: real entry b at (wg + b) * 8G + slot * G + column; virtual entry v
@@ -1588,10 +1828,10 @@ paged_decode_stream_kernel(const DecodeArgs a) {
           const int64_t row = row0 + qr;
           float* dst = a.part_acc + row * kHeadDim + c;
 #pragma unroll
-          for (int j = 0; j < 8; ++j) dst[16 * j] = acc[j][i];
+          for (int j = 0; j < 8; ++j) store_coherent(dst + 16 * j, acc[j][i]);
           if (c == 0) {
-            a.part_ml[row * 2 + 0] = mi;
-            a.part_ml[row * 2 + 1] = li;
+            store_coherent(a.part_ml + row * 2 + 0, mi);
+            store_coherent(a.part_ml + row * 2 + 1, li);
           }
         }
       }
@@ -1602,167 +1842,27 @@ paged_decode_stream_kernel(const DecodeArgs a) {
         l_run = 0.f;
         do {
           ++b;
-          ntl = __builtin_amdgcn_readfirstlane(tstart[b + 1] - tstart[b]);
-        } while (ntl == 0 && b + 1 < NS);
+        } while (tstart[b + 1] == tstart[b] && b + 1 < NS);
         b = __builtin_amdgcn_readfirstlane(b);
-        lt = 0;
-        cpage = -1;
-        stream_seq<TPR>(a, tstart, V, b, cbt_row, ctok0, n_eff, crot);
+        cleft = min(__builtin_amdgcn_readfirstlane(tstart[b + 1] - tstart[b]), count - done - 1);
         int qrow, qhead;
         stream_column<TPR>(a, V, b, h, c, qrow, qhead, colv);
         stream_load_q8<QDT, QVEC>(a, qrow, qhead, colv, g, qop);
       }
-    } else {
-      ++lt;
     }
   }
-  if ((PRISM_DBG(a) & 8) && threadIdx.x == 0) {  // measurement aid: start and end (100 MHz clock)
+
+  // ---- completion: count this range's flushes, merge completed sequences
+  __syncthreads();  // every wave is done with the stages (reused as scratch)
+  const uint64_t t_loop = (PRISM_DBG(a) & 8) ? __builtin_amdgcn_s_memrealtime() : 0;
+  stream_finish<QDT, TPR>(a, V, tstart, __builtin_amdgcn_readfirstlane(wr0.x), b - wr0.x + 1,
+                          reinterpret_cast<int*>(stages));
+  if ((PRISM_DBG(a) & 8) && threadIdx.x == 0) {  // measurement aid: start, loop end, end (100 MHz clock)
     const uint64_t t_end = __builtin_amdgcn_s_memrealtime();
     a.plan[kPlanWgTime + 2 * blockIdx.x] = static_cast<int>(t_begin & 0x7FFFFFFF);
     a.plan[kPlanWgTime + 2 * blockIdx.x + 1] = static_cast<int>(t_end & 0x7FFFFFFF);
+    a.plan[kPlanCnt + kSMaxBatch + blockIdx.x] = static_cast<int>((t_end - t_loop) & 0x7FFFFFFF);
   }
-}
-
-// Merge the streaming partials: grid (batch, num_heads), one wave each.
-// A sequence's partials come from the workgroups whose tile ranges meet its
-// own tiles (its private tail) and, when it belongs to a virtual sequence,
-// from those that walked its shared pages.  Every such (workgroup, entry)
-// pair wrote a partial (m = -inf when nothing was attended), so candidates
-// are enumerated by arithmetic.  Up to eight candidates (the usual case) have
-// their (m, l) and accumulators loaded together: two rounds of dependent
-// loads (the sequence's plan record, then the partials).  More candidates
-// are read lane-parallel first.
-template <int QDT, int TPR>
-__global__ void __launch_bounds__(64) paged_decode_stream_combine_kernel(const DecodeArgs a) {
-  // the tail's and the virtual sequence's tile ranges are disjoint, so at
-  // most one workgroup meets both: at most (nwg + 1) * TPR candidates
-  __shared__ float m_s[(kSMaxWg + 1) * TPR];
-  __shared__ float l_s[(kSMaxWg + 1) * TPR];
-  __shared__ int rows[(kSMaxWg + 1) * TPR];
-  const int b = blockIdx.x;
-  const int hq = blockIdx.y;
-  const int lane = threadIdx.x;
-  const int4 r0 = *reinterpret_cast<const int4*>(a.plan + kPlanRec + 8 * b);
-  const int vend = a.plan[kPlanRec + 8 * b + 4];
-  const int V = ld_meta(a.plan);
-  const StreamSplit sp = stream_split(a, ld_meta(a.plan + 1));
-  const int first = r0.x, end = r0.y, vslot = r0.z, vfirst = r0.w;
-  int lo0 = 0, cnt0 = 0, lo1 = 0, cnt1 = 0;
-  if (end > first) {
-    lo0 = static_cast<int>(split_owner(sp, first));
-    cnt0 = static_cast<int>(split_owner(sp, end - 1)) - lo0 + 1;
-  }
-  // Candidates are (workgroup w, token slot s < 8 / Hkv) pairs: the waves of
-  // slots hk + Hkv * s of w each streamed a share of the tokens.  Rows: real
-  // (w + V + b) * 8G + (hk + Hkv s) * G + qh; virtual
-  // vrow0 + ((w + v) * 8 + hk + Hkv s) * 16 + m * G + qh.
-  constexpr int tl = TPR == 1 ? 0 : (TPR == 2 ? 1 : (TPR == 4 ? 2 : 3));  // log2 of the token slots
-  constexpr int hkv = kSKv / TPR;
-  const int64_t rbase0 = static_cast<int64_t>(V + b) * (kSKv * a.groups) + hq;
-  int64_t rbase1 = 0;
-  if (vslot >= 0) {
-    const int v = vslot / kSCols;
-    const int m = vslot - v * kSCols;
-    const int hk = hq / a.groups;
-    rbase1 = a.vrow0 + (static_cast<int64_t>(v) * kSKv + hk) * kSCols + m * a.groups + (hq - hk * a.groups);
-    lo1 = static_cast<int>(split_owner(sp, vfirst));
-    cnt1 = static_cast<int>(split_owner(sp, vend - 1)) - lo1 + 1;
-  }
-  const int cnt = (cnt0 + cnt1) << tl;
-  // candidate i: its row and whether its workgroup had a range at all
-  auto cand = [&](int i, int64_t& row, bool& ok) {
-    const int wi = i >> tl;
-    const int sl = i & ((1 << tl) - 1);
-    const bool second = wi >= cnt0;
-    const int64_t w = second ? lo1 + (wi - cnt0) : lo0 + wi;
-    row = second ? rbase1 + w * (kSKv * kSCols) + sl * (hkv * kSCols)
-                 : rbase0 + w * (kSKv * a.groups) + sl * a.num_heads;
-    ok = split_begin(sp, w) < split_begin(sp, w + 1);
-  };
-  float l_sum = 0.f, o0 = 0.f, o1 = 0.f;
-  if (cnt <= 8) {  // (uniform) a few candidates: their loads in one round
-    constexpr int kU = 8;
-    float m_run = -INFINITY;
-    for (int base = 0; base < cnt; base += kU) {
-      float mv[kU], lv[kU], v0[kU], v1[kU];
-#pragma unroll
-      for (int u = 0; u < kU; ++u) {
-        int64_t row;
-        bool ok;
-        cand(min(base + u, cnt - 1), row, ok);
-        // a workgroup with an empty range (fewer tiles than workgroups) wrote
-        // nothing: its row is never read into the sums
-        ok = ok && base + u < cnt;
-        const float2 ml = *reinterpret_cast<const float2*>(a.part_ml + row * 2);
-        const float x0 = a.part_acc[row * kHeadDim + lane];
-        const float x1 = a.part_acc[row * kHeadDim + lane + 64];
-        mv[u] = ok ? ml.x : -INFINITY;  // -inf: weighs nothing
-        lv[u] = ok ? ml.y : 0.f;
-        v0[u] = ok ? x0 : 0.f;
-        v1[u] = ok ? x1 : 0.f;
-      }
-      float mx = m_run;
-#pragma unroll
-      for (int u = 0; u < kU; ++u) mx = fmaxf(mx, mv[u]);
-      if (mx == -INFINITY) continue;  // nothing attended so far (uniform)
-      const float alpha = exp2f(m_run - mx);  // 0 when m_run = -inf
-      l_sum *= alpha;
-      o0 *= alpha;
-      o1 *= alpha;
-#pragma unroll
-      for (int u = 0; u < kU; ++u) {
-        const float wgt = mv[u] == -INFINITY ? 0.f : exp2f(mv[u] - mx);  // rows with m = -inf hold zeros
-        l_sum += wgt * lv[u];
-        o0 += wgt * v0[u];
-        o1 += wgt * v1[u];
-      }
-      m_run = mx;
-    }
-  } else {
-    // many candidates (a long sequence over few others): lane i reads the
-    // (m, l) of candidate i (+64k), those that attended something are
-    // compacted into LDS, then every lane accumulates two output dims
-    int nvalid = 0;
-    float m_max = -INFINITY;
-    for (int base = 0; base < cnt; base += 64) {
-      const int i = base + lane;
-      int64_t row;
-      bool ok;
-      cand(min(i, cnt - 1), row, ok);
-      ok = ok && i < cnt;
-      float2 ml = {-INFINITY, 0.f};
-      if (ok) ml = *reinterpret_cast<const float2*>(a.part_ml + row * 2);
-      ok = ok && ml.x != -INFINITY;  // a partial with nothing attended weighs 0
-      const uint64_t mask = __builtin_amdgcn_ballot_w64(ok);
-      const int pos = nvalid + __builtin_amdgcn_mbcnt_hi(static_cast<uint32_t>(mask >> 32),
-                                                         __builtin_amdgcn_mbcnt_lo(static_cast<uint32_t>(mask), 0));
-      if (ok) {
-        m_s[pos] = ml.x;
-        l_s[pos] = ml.y;
-        rows[pos] = static_cast<int>(row);
-        m_max = fmaxf(m_max, ml.x);
-      }
-      nvalid += __builtin_popcountll(mask);
-    }
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) m_max = fmaxf(m_max, __shfl_xor(m_max, off));
-    __syncthreads();
-    l_sum = 0.f;
-    o0 = 0.f;
-    o1 = 0.f;
-#pragma unroll 4
-    for (int i = 0; i < nvalid; ++i) {
-      const float wgt = exp2f(m_s[i] - m_max);
-      const float* src = a.part_acc + static_cast<int64_t>(rows[i]) * kHeadDim;
-      l_sum += wgt * l_s[i];
-      o0 += wgt * src[lane];
-      o1 += wgt * src[lane + 64];
-    }
-  }
-  const float inv = l_sum > 0.f ? 1.f / l_sum : 0.f;
-  const int64_t obase = static_cast<int64_t>(b) * a.o_sb + static_cast<int64_t>(hq) * a.o_sh;
-  store_out<QDT>(a.out, obase + lane * a.o_sd, o0 * inv);
-  store_out<QDT>(a.out, obase + (lane + 64) * a.o_sd, o1 * inv);
 }
 
 // ---------------------------------------------------------------- generic path
@@ -2016,18 +2116,9 @@ int launch_stream(int stage, const DecodeArgs& args, const Geometry& geo, hipStr
       else PRISM_LAUNCH_STREAM(false, 1);
     }
 #undef PRISM_LAUNCH_STREAM
-    const int rc = check_launch("paged_decode_stream_kernel launch");
-    if (rc) return rc;
+    return check_launch("paged_decode_stream_kernel launch");
   }
-  if (stage != 1) {
-    const dim3 grid(args.batch, args.num_heads);
-    if (args.s_tpr == 8) hipLaunchKernelGGL((paged_decode_stream_combine_kernel<QDT, 8>), grid, dim3(64), 0, stream, args);
-    else if (args.s_tpr == 4) hipLaunchKernelGGL((paged_decode_stream_combine_kernel<QDT, 4>), grid, dim3(64), 0, stream, args);
-    else if (args.s_tpr == 2) hipLaunchKernelGGL((paged_decode_stream_combine_kernel<QDT, 2>), grid, dim3(64), 0, stream, args);
-    else hipLaunchKernelGGL((paged_decode_stream_combine_kernel<QDT, 1>), grid, dim3(64), 0, stream, args);
-    return check_launch("paged_decode_stream_combine_kernel launch");
-  }
-  return PRISM_OK;
+  return PRISM_OK;  // stage 2: the streaming kernel merges its own partials
 }
 
 template <int QDT>
