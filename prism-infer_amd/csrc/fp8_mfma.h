@@ -88,6 +88,16 @@ __device__ __forceinline__ float wave_max_across_groups(float v) {
   return fmaxf(__uint_as_float(q[0]), __uint_as_float(q[1]));
 }
 
+// The same with IEEE-754 maximum (NaN-propagating, v_maximum_f32): unlike
+// fmaxf it needs no canonicalisation of values that arrive through lane
+// swaps, so a kernel compiled in IEEE mode pays one instruction per step.
+__device__ __forceinline__ float wave_maximum_across_groups(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __builtin_elementwise_maximum(__uint_as_float(r[0]), __uint_as_float(r[1]));
+  const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __builtin_elementwise_maximum(__uint_as_float(q[0]), __uint_as_float(q[1]));
+}
+
 typedef short shortx4 __attribute__((ext_vector_type(4)));
 
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));

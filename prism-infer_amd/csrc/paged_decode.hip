@@ -611,12 +611,11 @@ constexpr int kSThreads = 64 * kSKv;
 constexpr int kSWaves = kSKv;  // waves per streaming workgroup
 constexpr int kSLoadsPerStage = 5;                      // per lane: 2 K, 2 V, 1 scale
 constexpr float kSRescaleThreshold = 8.0f;              // log2 domain
-// PV is one f16 MFMA per N-tile, with P * v_scale as f16 (2^-11 relative).
-// P <= 2^8 with the lazy rescaling, so P * v_scale fits f16 while every v
-// scale is <= kSF16MaxVScale; a tile with a larger one (|V| > 1.1e5) scales
-// P * v_scale by 2^-k and the accumulators by 2^-k before its MFMAs and by
-// 2^k after them, exact powers of two.
-constexpr float kSF16MaxVScale = 255.0f;
+// PV is one bf16 MFMA per N-tile with P * v_scale as one bf16 (8 significant
+// bits, RNE: 2^-9 relative per weight, the precision of the bf16 output
+// itself).  bf16 has fp32's exponent range, so P * v_scale needs no range
+// handling for any v scale (a tile may mix rows at the 1e-6 scale floor with
+// rows at 1e4), and V's E4M3FN bytes convert to bf16 exactly.
 
 // 16-byte LDS reads at a byte address of the LDS aperture.
 __device__ __forceinline__ u32x4 lds_load_b128(uint32_t addr) {
@@ -705,8 +704,20 @@ __device__ __forceinline__ StreamLanePlan stream_plan(int wave, int lane) {
 
 // kb / vb: the tile's first K / V byte; sb: its first scale of this lane's
 // kind (k or v); stage_lds: the stage's LDS address.
+// A pointer the compiler must keep in scalar registers (the asm's `saddr`).
+template <typename T>
+__device__ __forceinline__ T* scalar_ptr(T* p) {
+  const uint64_t v = reinterpret_cast<uint64_t>(p);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v));
+  const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(v >> 32));
+  return reinterpret_cast<T*>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
 __device__ __forceinline__ void stream_issue(const StreamLanePlan& pl, const uint8_t* kb, const uint8_t* vb,
                                              const float* sb, uint32_t stage_lds, bool nt) {
+  kb = scalar_ptr(kb);
+  vb = scalar_ptr(vb);
+  sb = scalar_ptr(sb);
   const uint32_t lk0 = stage_lds + pl.lk[0];
   const uint32_t lk1 = stage_lds + pl.lk[1];
   const uint32_t lv0 = lk0 + kSKBytes;
@@ -854,7 +865,8 @@ __device__ __forceinline__ void stream_load_q8(const DecodeArgs& a, int qrow, in
   mx = wave_max_across_groups(mx);
   // 2^e puts the column's largest |q| in [128, 256); clamped so that 2^-e
   // stays a normal fp32 number (columns of zeros keep e = 0).
-  const int e = (mx > 0.f && mx <= 3.0e38f) ? min(max(7 - ilogbf(mx), -120), 120) : 0;
+  // ilogb(mx) = frexp exponent - 1 (exact for subnormals too, no library call)
+  const int e = (mx > 0.f && mx <= 3.0e38f) ? min(max(8 - __builtin_amdgcn_frexp_expf(mx), -120), 120) : 0;
   qop.colscale = ldexpf(a.scale_log2, -e);
 #pragma unroll
   for (int w = 0; w < 8; ++w) {
@@ -1715,23 +1727,21 @@ paged_decode_stream_kernel(const DecodeArgs a) {
       uint64_t vt[4];
       lds_read_tr8_x4(ad, vt);
       // ---- QK over 16 tokens: the K bytes are the fp8 MFMA's A operand as
-      // they are (row = token c, k = dims 32g..32g+31).  The three query
-      // terms go to independent accumulators (no dependent MFMA chain) and
-      // are summed smallest first.
+      // they are (row = token c, k = dims 32g..32g+31); smallest term first.
       const i32x8 ka = {static_cast<int>(k0[0]), static_cast<int>(k0[1]), static_cast<int>(k0[2]),
                         static_cast<int>(k0[3]), static_cast<int>(k1[0]), static_cast<int>(k1[1]),
                         static_cast<int>(k1[2]), static_cast<int>(k1[3])};
-      const floatx4 zero4 = {0.f, 0.f, 0.f, 0.f};
-      const floatx4 s2 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, qop.t[2], zero4, 0, 0, 0, 0, 0, 0);
-      const floatx4 s1 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, qop.t[1], zero4, 0, 0, 0, 0, 0, 0);
-      const floatx4 s0 = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, qop.t[0], zero4, 0, 0, 0, 0, 0, 0);
+      floatx4 sc = {0.f, 0.f, 0.f, 0.f};
+      sc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, qop.t[2], sc, 0, 0, 0, 0, 0, 0);
+      sc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, qop.t[1], sc, 0, 0, 0, 0, 0, 0);
+      sc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, qop.t[0], sc, 0, 0, 0, 0, 0, 0);
       // ---- scores in the log2 domain.  Query columns without a query hold
       // q = 0, so their scores are finite and their rows are never written.
       float x[4];
       float vsm[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        x[i] = ((s2[i] + s1[i]) + s0[i]) * (ks[i] * qop.colscale);
+        x[i] = sc[i] * (ks[i] * qop.colscale);
         vsm[i] = vs[i];
       }
       // Only a sequence's last tile can reach past its end (uniform branch).
@@ -1752,8 +1762,9 @@ paged_decode_stream_kernel(const DecodeArgs a) {
         for (int jp = 0; jp < 4; ++jp) vt[jp] &= keep2;
       }
       // ---- online softmax with lazy rescaling
-      float tmax = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
-      tmax = wave_max_across_groups(tmax);
+      // (IEEE maximum: no canonicalising of masked or swapped values)
+      float tmax = nan_max(nan_max(x[0], x[1]), nan_max(x[2], x[3]));
+      tmax = wave_maximum_across_groups(tmax);
       const bool raise = tmax > m_run + kSRescaleThreshold;
       if (__builtin_amdgcn_ballot_w64(raise) != 0) {  // wave-uniform branch
         const float m_new = raise ? tmax : m_run;
@@ -1778,32 +1789,16 @@ paged_decode_stream_kernel(const DecodeArgs a) {
         pv[i] = p * vsm[i];
       }
       // ---- PV: one transposed read feeds N-tiles 2jp and 2jp+1.
-      const float vmax4 = fmaxf(fmaxf(vsm[0], vsm[1]), fmaxf(vsm[2], vsm[3]));
-      int vexp = 0;  // wave-uniform power-of-two shift of this tile's P * v_scale
-      if (__builtin_amdgcn_ballot_w64(vmax4 > kSF16MaxVScale) != 0) {
-        float vmax = vmax4;
-#pragma unroll
-        for (int off = 32; off >= 1; off >>= 1) vmax = fmaxf(vmax, __shfl_xor(vmax, off));
-        vexp = __builtin_amdgcn_readfirstlane(ilogbf(vmax / kSF16MaxVScale) + 1);
-        const float down = ldexpf(1.f, -vexp);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[j] *= down;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) pv[i] *= down;
-      }
-      const f16x4 pa = {static_cast<_Float16>(pv[0]), static_cast<_Float16>(pv[1]), static_cast<_Float16>(pv[2]),
-                        static_cast<_Float16>(pv[3])};
+      const shortx4 pa = {__builtin_bit_cast(short, static_cast<__bf16>(pv[0])),
+                          __builtin_bit_cast(short, static_cast<__bf16>(pv[1])),
+                          __builtin_bit_cast(short, static_cast<__bf16>(pv[2])),
+                          __builtin_bit_cast(short, static_cast<__bf16>(pv[3]))};
 #pragma unroll
       for (int jp = 0; jp < 4; ++jp) {
-        const f16x4 b0 = fp8x4_to_f16x4(static_cast<uint32_t>(vt[jp]));
-        const f16x4 b1 = fp8x4_to_f16x4(static_cast<uint32_t>(vt[jp] >> 32));
-        acc[2 * jp] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, b0, acc[2 * jp], 0, 0, 0);
-        acc[2 * jp + 1] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, b1, acc[2 * jp + 1], 0, 0, 0);
-      }
-      if (vexp != 0) {
-        const float up = ldexpf(1.f, vexp);
-#pragma unroll
-        for (int j = 0; j < 8; ++j) acc[j] *= up;
+        const shortx4 b0 = fp8x4_to_bf16x4_bits(static_cast<uint32_t>(vt[jp]));
+        const shortx4 b1 = fp8x4_to_bf16x4_bits(static_cast<uint32_t>(vt[jp] >> 32));
+        acc[2 * jp] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, b0, acc[2 * jp], 0, 0, 0);
+        acc[2 * jp + 1] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, b1, acc[2 * jp + 1], 0, 0, 0);
       }
     }
     cstage = cstage == kSStages - 1 ? 0 : cstage + 1;
