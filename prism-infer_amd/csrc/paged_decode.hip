@@ -993,8 +993,9 @@ __device__ __forceinline__ int stream_owner_count(int first, int end, int total,
   return static_cast<int>(split_owner(sp, end - 1) - split_owner(sp, first)) + 1;
 }
 
-// Inclusive prefix sum over the workgroup (every thread calls it): shuffles
-// within each wave, one pass over the wave totals.
+// Inclusive prefix sum over the workgroup of NT threads (every thread calls
+// it): shuffles within each wave, one pass over the wave totals.
+template <int NT>
 __device__ __forceinline__ int plan_scan(int v, int* wsum_s, int& total) {
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -1008,7 +1009,7 @@ __device__ __forceinline__ int plan_scan(int v, int* wsum_s, int& total) {
   __syncthreads();
   int before = 0, tot = 0;
 #pragma unroll
-  for (int i = 0; i < kPlanThreads / 64; ++i) {
+  for (int i = 0; i < NT / 64; ++i) {
     const int ws = wsum_s[i];
     before += i < wave ? ws : 0;
     tot += ws;
@@ -1018,120 +1019,144 @@ __device__ __forceinline__ int plan_scan(int v, int* wsum_s, int& total) {
   return x + before;
 }
 
-__global__ void __launch_bounds__(kPlanThreads) paged_decode_stream_plan_kernel(const DecodeArgs a) {
-  __shared__ int eff_s[kSMaxBatch];
-  __shared__ int cap_s[kSMaxBatch];    // whole pages covered by the attended length (<= kPlanMaxPages)
-  __shared__ int full_s[kSMaxBatch];   // leading whole pages with valid block ids
-  __shared__ int lead_s[kSMaxBatch];   // group leader
-  __shared__ int sh_s[kSMaxBatch];     // leading pages equal to the leader's
-  __shared__ int cnt_s[kSMaxBatch];    // at a leader: members besides itself
-  __shared__ int smax_s[kSMaxBatch];   // at a leader: longest member share
-  __shared__ int vb_s[kSMaxBatch];     // at a leader: first virtual sequence
-  __shared__ int skip_s[kSMaxBatch];
-  __shared__ int vslot_s[kSMaxBatch];
-  __shared__ int vlen_s[kSMaxVirt];    // pages of virtual sequence v
-  __shared__ int vk_s[kSMaxVirt];      // chunk index of v in its group
-  __shared__ int vn_s[kSMaxVirt];      // virtual sequences of v's group
-  __shared__ int vsrc_s[kSMaxVirt];
-  __shared__ int vmem_s[kSMaxVirt * kSCols];
-  __shared__ int hkey[kPlanHash];
-  __shared__ int hmin[kPlanHash];
-  __shared__ int bt_s[kSShareMaxBatch * kPlanMaxPages];  // compared part of the block tables
-  __shared__ int tst_s[kSMaxBatch + kSMaxVirt + 1];
-  __shared__ int wsum_s[kPlanThreads / 64];
-  __shared__ __attribute__((aligned(16))) int cnt_rank_s[kSShareMaxBatch];  // group of each member or -1
+// LDS of the plan computation (the streaming kernel lays it over its stage
+// buffers, which are idle until the plan is known).
+struct PlanLds {
+  int eff_s[kSMaxBatch];
+  int cap_s[kSMaxBatch];    // whole pages covered by the attended length (<= kPlanMaxPages)
+  int full_s[kSMaxBatch];   // leading whole pages with valid block ids
+  int lead_s[kSMaxBatch];   // group leader
+  int sh_s[kSMaxBatch];     // leading pages equal to the leader's
+  int cnt_s[kSMaxBatch];    // at a leader: members besides itself
+  int smax_s[kSMaxBatch];   // at a leader: longest member share
+  int vb_s[kSMaxBatch];     // at a leader: first virtual sequence
+  int skip_s[kSMaxBatch];
+  int vslot_s[kSMaxBatch];
+  int vlen_s[kSMaxVirt];    // pages of virtual sequence v
+  int vk_s[kSMaxVirt];      // chunk index of v in its group
+  int vn_s[kSMaxVirt];      // virtual sequences of v's group
+  int vsrc_s[kSMaxVirt];
+  int vmem_s[kSMaxVirt * kSCols];
+  int hkey[kPlanHash];
+  int hmin[kPlanHash];
+  int bt_s[kSShareMaxBatch * kPlanMaxPages];  // compared part of the block tables
+  int wsum_s[kPlanThreads / 64];
+  __attribute__((aligned(16))) int cnt_rank_s[kSShareMaxBatch];  // group of each member or -1
+};
+
+// Whether prefix sharing is analysed for this call.
+__device__ __forceinline__ bool plan_share(const DecodeArgs& a) {
+  const int Wc = min(a.width, kPlanMaxPages);
+  return a.share && a.batch <= kSShareMaxBatch && (kSCols / a.groups) >= 2 && Wc >= 1;
+}
+
+__device__ __forceinline__ void plan_key_params(const DecodeArgs& a, bool share, int (&kp)[kPlanKeyParams]) {
+  const int vals[kPlanKeyParams] = {kPlanMagic, a.batch, a.width, a.page_size, a.groups,
+                                    static_cast<int>(a.num_blocks & 0x7FFFFFFF),
+                                    static_cast<int>(a.num_blocks >> 31), share ? 1 : 0, a.stream_nwg,
+                                    a.num_kv_heads, 0, 0};
+#pragma unroll
+  for (int i = 0; i < kPlanKeyParams; ++i) kp[i] = vals[i];
+}
+
+// Compares the inputs of this call with the key stored next to the plan
+// (geometry, attended lengths, compared block-table prefix, plan header)
+// and stages the lengths and the compared block-table prefix into L for a
+// rebuild.  Returns this thread's verdict; the workgroup ANDs them.  All
+// loads of the check go out before anything is compared (one round).  Key
+// words are read with device-scope loads: within one launch of the
+// streaming kernel the key may be rewritten by workgroup 0, and a reader
+// then sees either the old key (and waits for the new plan) or the new one.
+template <int NT>
+__device__ __forceinline__ bool plan_key_check(const DecodeArgs& a, PlanLds& L) {
+  const int tid = threadIdx.x;
+  const int B = a.batch;
+  const int P = a.page_size;
+  const int Wc = min(a.width, kPlanMaxPages);
+  const bool share = plan_share(a);
+  const int* key = a.plan + kPlanKey;
+  auto kld = [](const int* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+  int kp[kPlanKeyParams];
+  plan_key_params(a, share, kp);
+  bool same = true;
+  if (tid < kPlanKeyParams - 2) {
+#pragma unroll
+    for (int i = 0; i < kPlanKeyParams - 2; ++i)
+      if (i == tid) same = kld(key + i) == kp[i];
+  }
+  if (tid == 0)
+    same = same && kld(key + kPlanKeyParams - 2) == kld(a.plan) && kld(key + kPlanKeyParams - 1) == kld(a.plan + 1);
+  for (int b = tid; b < B; b += NT) {
+    const int n = effective_len(a, b);
+    same = same && kld(key + kPlanKeyEff - kPlanKey + b) == n;
+    L.eff_s[b] = n;
+    const int cap = min(n / P, Wc);
+    L.cap_s[b] = cap;
+  }
+  const int items = share ? B * Wc : 0;
+  constexpr int kU = 8;
+  for (int base = 0; base < items; base += kU * NT) {
+    int val[kU], old[kU];
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int idx = base + u * NT + tid;
+      const int b = idx / Wc;
+      const int j = idx - b * Wc;
+      val[u] = idx < items ? a.bt[static_cast<int64_t>(b) * a.bt_sb + static_cast<int64_t>(j) * a.bt_sn] : -1;
+      old[u] = idx < items ? kld(key + kPlanKeyBt - kPlanKey + idx) : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int idx = base + u * NT + tid;
+      if (idx < items) L.bt_s[idx] = val[u];
+      same = same && old[u] == val[u];
+    }
+  }
+  return same;
+}
+
+// Builds the plan from L (filled by plan_key_check) with NT threads and
+// writes it, its key and zeroed merge counters to the workspace.  tst_s
+// receives the tile prefix sums (NS + 1 entries).
+template <int NT>
+__device__ void plan_build(const DecodeArgs& a, PlanLds& L, int* tst_s) {
   int* plan = a.plan;
   const int tid = threadIdx.x;
   const int B = a.batch;
   const int P = a.page_size;
   const int Wc = min(a.width, kPlanMaxPages);
   const int M = kSCols / a.groups;  // members per virtual sequence
-  const bool share = a.share && B <= kSShareMaxBatch && M >= 2 && Wc >= 1;
-  const uint64_t t_start = __builtin_amdgcn_s_memtime();
-  auto stamp = [&](int k) {  // measurement aid: cycles since start of each phase (debug bit 4)
-    if ((PRISM_DBG(a) & 4) && tid == 0) plan[4 + k] = static_cast<int>(__builtin_amdgcn_s_memtime() - t_start);
-  };
-
-  // Global memory is only read until the final write-out: a barrier after
-  // global stores would wait for them to complete.
-  const int* key = plan + kPlanKey;
-  const int key_params[kPlanKeyParams] = {kPlanMagic, B, a.width, P, a.groups,
-                                          static_cast<int>(a.num_blocks & 0x7FFFFFFF),
-                                          static_cast<int>(a.num_blocks >> 31), share ? 1 : 0, a.stream_nwg,
-                                          a.num_kv_heads, 0, 0};
-  // The compared block-table prefix: its first eight loads per thread go out
-  // before anything is compared, so the whole check is one round of loads.
+  const bool share = plan_share(a);
   const int items = share ? B * Wc : 0;
-  int val0[8], old0[8];
-#pragma unroll
-  for (int u = 0; u < 8; ++u) {
-    const int idx = u * kPlanThreads + tid;
-    const int b = idx / Wc;
-    const int j = idx - b * Wc;
-    val0[u] = idx < items ? a.bt[static_cast<int64_t>(b) * a.bt_sb + static_cast<int64_t>(j) * a.bt_sn] : -1;
-    old0[u] = idx < items ? key[kPlanKeyBt - kPlanKey + idx] : -1;
-  }
-  bool same = true;
-  if (tid < kPlanKeyParams - 2) same = key[tid] == key_params[tid];
-  if (tid == 0) same = same && key[kPlanKeyParams - 2] == plan[0] && key[kPlanKeyParams - 1] == plan[1];
-  if (tid < B) {
-    const int n = effective_len(a, tid);
-    same = same && key[kPlanKeyEff - kPlanKey + tid] == n;
-    eff_s[tid] = n;
-    const int cap = min(n / P, Wc);
-    cap_s[tid] = cap;
-    full_s[tid] = cap;
-    sh_s[tid] = cap;
-    lead_s[tid] = tid;
-    cnt_s[tid] = 0;
-    smax_s[tid] = 0;
-    skip_s[tid] = 0;
-    vslot_s[tid] = -1;
+  for (int b = tid; b < B; b += NT) {
+    const int cap = L.cap_s[b];
+    L.full_s[b] = cap;
+    L.sh_s[b] = cap;
+    L.lead_s[b] = b;
+    L.cnt_s[b] = 0;
+    L.smax_s[b] = 0;
+    L.skip_s[b] = 0;
+    L.vslot_s[b] = -1;
   }
   int V = 0;
-  stamp(0);
-  // stage the compared block-table prefix, eight loads in flight per thread
-  for (int base = 0; base < items; base += 8 * kPlanThreads) {
-    int val[8], old[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int idx = base + u * kPlanThreads + tid;
-      const int b = idx / Wc;
-      const int j = idx - b * Wc;
-      if (base == 0) {
-        val[u] = val0[u];
-        old[u] = old0[u];
-      } else {
-        val[u] = idx < items ? a.bt[static_cast<int64_t>(b) * a.bt_sb + static_cast<int64_t>(j) * a.bt_sn] : -1;
-        old[u] = idx < items ? key[kPlanKeyBt - kPlanKey + idx] : -1;
-      }
+  __syncthreads();
+  if (share) {  // B <= kSShareMaxBatch <= NT here: one thread per sequence
+    for (int i = tid; i < kPlanHash; i += NT) {
+      L.hkey[i] = -1;
+      L.hmin[i] = INT_MAX;
     }
-#pragma unroll
-    for (int u = 0; u < 8; ++u) {
-      const int idx = base + u * kPlanThreads + tid;
-      if (idx < items) bt_s[idx] = val[u];
-      same = same && old[u] == val[u];
-    }
-  }
-  if (__syncthreads_and(same ? 1 : 0)) return;  // the previous plan still holds
-  if (share) {
-    for (int i = tid; i < kPlanHash; i += kPlanThreads) {
-      hkey[i] = -1;
-      hmin[i] = INT_MAX;
-    }
-    for (int i = tid; i < kSMaxVirt * kSCols; i += kPlanThreads) vmem_s[i] = -1;
+    for (int i = tid; i < kSMaxVirt * kSCols; i += NT) L.vmem_s[i] = -1;
     __syncthreads();
-    stamp(1);
     // group by first page: open addressing, the lowest index wins the slot
     int slot = -1;
-    if (tid < B && cap_s[tid] >= 1) {
-      const int raw = bt_s[tid * Wc];
+    if (tid < B && L.cap_s[tid] >= 1) {
+      const int raw = L.bt_s[tid * Wc];
       if (raw >= 0 && raw < a.num_blocks) {
         uint32_t hsh = (static_cast<uint32_t>(raw) * 2654435761u) >> (32 - kPlanHashBits);
         for (;;) {
-          const int prev = atomicCAS(&hkey[hsh], -1, raw);
+          const int prev = atomicCAS(&L.hkey[hsh], -1, raw);
           if (prev == -1 || prev == raw) {
-            atomicMin(&hmin[hsh], tid);
+            atomicMin(&L.hmin[hsh], tid);
             slot = static_cast<int>(hsh);
             break;
           }
@@ -1140,138 +1165,138 @@ __global__ void __launch_bounds__(kPlanThreads) paged_decode_stream_plan_kernel(
       }
     }
     __syncthreads();
-    if (slot >= 0) lead_s[tid] = hmin[slot];
+    if (slot >= 0) L.lead_s[tid] = L.hmin[slot];
     __syncthreads();
-    stamp(2);
     // page by page: validity of each whole page, equality with the leader's
-    for (int idx = tid; idx < items; idx += kPlanThreads) {
+    for (int idx = tid; idx < items; idx += NT) {
       const int b = idx / Wc;
       const int j = idx - b * Wc;
-      if (j >= cap_s[b]) continue;
-      const int raw = bt_s[idx];
+      if (j >= L.cap_s[b]) continue;
+      const int raw = L.bt_s[idx];
       const bool valid = raw >= 0 && raw < a.num_blocks;
-      if (!valid) atomicMin(&full_s[b], j);
-      const int L = lead_s[b];
-      if (L != b) {
-        const int lraw = j < cap_s[L] ? bt_s[L * Wc + j] : -1;
-        if (!valid || lraw != raw) atomicMin(&sh_s[b], j);
+      if (!valid) atomicMin(&L.full_s[b], j);
+      const int ld = L.lead_s[b];
+      if (ld != b) {
+        const int lraw = j < L.cap_s[ld] ? L.bt_s[ld * Wc + j] : -1;
+        if (!valid || lraw != raw) atomicMin(&L.sh_s[b], j);
       }
     }
     __syncthreads();
-    stamp(3);
-    if (tid < B && lead_s[tid] != tid) {
-      const int sv = min(sh_s[tid], full_s[tid]);
-      sh_s[tid] = sv;
+    if (tid < B && L.lead_s[tid] != tid) {
+      const int sv = min(L.sh_s[tid], L.full_s[tid]);
+      L.sh_s[tid] = sv;
       if (sv >= 1) {
-        atomicAdd(&cnt_s[lead_s[tid]], 1);
-        atomicMax(&smax_s[lead_s[tid]], sv);
+        atomicAdd(&L.cnt_s[L.lead_s[tid]], 1);
+        atomicMax(&L.smax_s[L.lead_s[tid]], sv);
       }
     }
     __syncthreads();
     // virtual sequences per group: chunks of M members in index order, kept
     // only when a chunk has at least two members
     int nv = 0;
-    if (tid < B && lead_s[tid] == tid && cnt_s[tid] >= 1) {
-      const int n = cnt_s[tid] + 1;
+    if (tid < B && L.lead_s[tid] == tid && L.cnt_s[tid] >= 1) {
+      const int n = L.cnt_s[tid] + 1;
       nv = n / M + ((n % M) >= 2 ? 1 : 0);
     }
-    const int incl = plan_scan(nv, wsum_s, V);
-    if (tid < B) vb_s[tid] = incl - nv;
-    for (int i = tid; i < V; i += kPlanThreads) vlen_s[i] = INT_MAX;
+    const int incl = plan_scan<NT>(nv, L.wsum_s, V);
+    if (tid < B) L.vb_s[tid] = incl - nv;
+    for (int i = tid; i < V; i += NT) L.vlen_s[i] = INT_MAX;
     // group of each member (-1 for non-members), for the rank count below
     if (tid < kSShareMaxBatch) {
       int ml = -1;
       if (tid < B) {
-        const int L = lead_s[tid];
-        ml = ((L == tid) ? cnt_s[tid] >= 1 : sh_s[tid] >= 1) ? L : -1;
+        const int ld = L.lead_s[tid];
+        ml = ((ld == tid) ? L.cnt_s[tid] >= 1 : L.sh_s[tid] >= 1) ? ld : -1;
       }
-      cnt_rank_s[tid] = ml;
+      L.cnt_rank_s[tid] = ml;
     }
     __syncthreads();
-    stamp(4);
     if (tid < B) {
-      const int L = lead_s[tid];
-      const bool member = cnt_rank_s[tid] >= 0;
+      const int ld = L.lead_s[tid];
+      const bool member = L.cnt_rank_s[tid] >= 0;
       if (member) {
         // rank = members of the group with a lower index (the leader is rank 0);
         // independent 16-byte LDS reads so the latencies overlap
         int rank = 0;
-        const int4* ml4 = reinterpret_cast<const int4*>(cnt_rank_s);
+        const int4* ml4 = reinterpret_cast<const int4*>(L.cnt_rank_s);
 #pragma unroll 8
         for (int q = 0; q < (tid + 3) / 4; ++q) {
           const int4 x = ml4[q];
           const int b0 = 4 * q;
-          rank += (b0 + 0 < tid && x.x == L) + (b0 + 1 < tid && x.y == L) + (b0 + 2 < tid && x.z == L) +
-                  (b0 + 3 < tid && x.w == L);
+          rank += (b0 + 0 < tid && x.x == ld) + (b0 + 1 < tid && x.y == ld) + (b0 + 2 < tid && x.z == ld) +
+                  (b0 + 3 < tid && x.w == ld);
         }
-        const int n = cnt_s[L] + 1;
+        const int n = L.cnt_s[ld] + 1;
         const int k = rank / M;
         const int chunk = min(M, n - k * M);
         if (chunk >= 2) {
-          const int v = vb_s[L] + k;
+          const int v = L.vb_s[ld] + k;
           const int m = rank - k * M;
-          vmem_s[v * kSCols + m] = tid;
-          vslot_s[tid] = v * kSCols + m;
-          atomicMin(&vlen_s[v], L == tid ? smax_s[tid] : sh_s[tid]);
+          L.vmem_s[v * kSCols + m] = tid;
+          L.vslot_s[tid] = v * kSCols + m;
+          atomicMin(&L.vlen_s[v], ld == tid ? L.smax_s[tid] : L.sh_s[tid]);
           if (m == 0) {
-            vsrc_s[v] = L;
-            vk_s[v] = k;
-            vn_s[v] = n / M + ((n % M) >= 2 ? 1 : 0);
+            L.vsrc_s[v] = ld;
+            L.vk_s[v] = k;
+            L.vn_s[v] = n / M + ((n % M) >= 2 ? 1 : 0);
           }
         }
       }
     }
     __syncthreads();
-    stamp(5);
-    if (tid < B && vslot_s[tid] >= 0) skip_s[tid] = vlen_s[vslot_s[tid] / kSCols] * P;
+    if (tid < B && L.vslot_s[tid] >= 0) L.skip_s[tid] = L.vlen_s[L.vslot_s[tid] / kSCols] * P;
     __syncthreads();
   }
-  stamp(6);
   // tile prefix sums in stream order: virtual sequences, then real ones
   const int NS = B + V;
   int carry = 0;
   if (tid == 0) tst_s[0] = 0;
-  for (int base = 0; base < NS; base += kPlanThreads) {
+  for (int base = 0; base < NS; base += NT) {
     const int i = base + tid;
     int n = 0;
-    if (i < V) n = vlen_s[i] * (P / a.s_ttok);
-    else if (i < NS) n = (eff_s[i - V] - skip_s[i - V] + a.s_ttok - 1) / a.s_ttok;
+    if (i < V) n = L.vlen_s[i] * (P / a.s_ttok);
+    else if (i < NS) n = (L.eff_s[i - V] - L.skip_s[i - V] + a.s_ttok - 1) / a.s_ttok;
     int chunk_total;
-    const int incl = plan_scan(n, wsum_s, chunk_total);
+    const int incl = plan_scan<NT>(n, L.wsum_s, chunk_total);
     if (i < NS) tst_s[i + 1] = carry + incl;
     carry += chunk_total;
   }
   __syncthreads();
-  stamp(7);
   // ---- write-out
-  for (int i = tid; i <= NS; i += kPlanThreads) plan[kPlanTstart + i] = tst_s[i];
-  if (tid < B) {
-    plan[kPlanSkip + tid] = skip_s[tid];
-    plan[kPlanVslot + tid] = vslot_s[tid];
-    const int vs = vslot_s[tid];
+  for (int i = tid; i <= NS; i += NT) plan[kPlanTstart + i] = tst_s[i];
+  for (int b = tid; b < B; b += NT) {
+    plan[kPlanSkip + b] = L.skip_s[b];
+    plan[kPlanVslot + b] = L.vslot_s[b];
+    const int vs = L.vslot_s[b];
     const int v = vs >= 0 ? vs / kSCols : 0;
-    const int first = tst_s[V + tid], end = tst_s[V + tid + 1];
+    const int first = tst_s[V + b], end = tst_s[V + b + 1];
     const int vfirst = vs >= 0 ? tst_s[v] : 0, vend = vs >= 0 ? tst_s[v + 1] : 0;
     const int expect = stream_owner_count(first, end, carry, a.stream_nwg) +
                        stream_owner_count(vfirst, vend, carry, a.stream_nwg);
-    int4* rec = reinterpret_cast<int4*>(plan + kPlanRec + 8 * tid);
+    int4* rec = reinterpret_cast<int4*>(plan + kPlanRec + 8 * b);
     rec[0] = int4{first, end, vs, vfirst};
     rec[1] = int4{vend, expect, 0, 0};
-    plan[kPlanCnt + tid] = 0;
+    plan[kPlanCnt + b] = 0;
   }
-  for (int i = tid; i < V * kSCols; i += kPlanThreads) plan[kPlanVmem + i] = vmem_s[i];
-  if (tid < V) {
-    plan[kPlanVsrc + tid] = vsrc_s[tid];
-    plan[kPlanVrot + tid] = (vk_s[tid] * vlen_s[tid] / vn_s[tid]) * (P / a.s_ttok);
+  for (int i = tid; i < V * kSCols; i += NT) plan[kPlanVmem + i] = L.vmem_s[i];
+  for (int v = tid; v < V; v += NT) {
+    plan[kPlanVsrc + v] = L.vsrc_s[v];
+    plan[kPlanVrot + v] = (L.vk_s[v] * L.vlen_s[v] / L.vn_s[v]) * (P / a.s_ttok);
   }
-  if (tid < kPlanKeyParams - 2) plan[kPlanKey + tid] = key_params[tid];
+  int kp[kPlanKeyParams];
+  plan_key_params(a, share, kp);
+  if (tid < kPlanKeyParams - 2) {
+#pragma unroll
+    for (int i = 0; i < kPlanKeyParams - 2; ++i)
+      if (i == tid) plan[kPlanKey + i] = kp[i];
+  }
   if (tid == 0) {  // copies of the plan header, checked before the plan is reused
     plan[kPlanKey + kPlanKeyParams - 2] = V;
     plan[kPlanKey + kPlanKeyParams - 1] = carry;
   }
-  if (tid < B) plan[kPlanKeyEff + tid] = eff_s[tid];
-  for (int i = tid; i < items; i += kPlanThreads) plan[kPlanKeyBt + i] = bt_s[i];
-  for (int w = tid; w < a.stream_nwg; w += kPlanThreads) {
+  for (int b = tid; b < B; b += NT) plan[kPlanKeyEff + b] = L.eff_s[b];
+  for (int i = tid; i < items; i += NT) plan[kPlanKeyBt + i] = L.bt_s[i];
+  for (int w = tid; w < a.stream_nwg; w += NT) {
     const int64_t s0 = static_cast<int64_t>(w) * carry / a.stream_nwg;
     const int64_t s1 = static_cast<int64_t>(w + 1) * carry / a.stream_nwg;
     int4 r0 = {-1, 0, 0, 0}, r1 = {0, 0, 0, kNoBlock};
@@ -1289,30 +1314,38 @@ __global__ void __launch_bounds__(kPlanThreads) paged_decode_stream_plan_kernel(
       int bt_row, tok0, n_end, rot;
       if (i >= V) {
         bt_row = i - V;
-        tok0 = skip_s[bt_row];
-        n_end = eff_s[bt_row];
+        tok0 = L.skip_s[bt_row];
+        n_end = L.eff_s[bt_row];
         rot = 0;
       } else {
-        bt_row = vsrc_s[i];
+        bt_row = L.vsrc_s[i];
         tok0 = 0;
         n_end = intl * a.s_ttok;
-        rot = (vk_s[i] * vlen_s[i] / vn_s[i]) * (P / a.s_ttok);
+        rot = (L.vk_s[i] * L.vlen_s[i] / L.vn_s[i]) * (P / a.s_ttok);
       }
       const int lr = ilt + rot;
       const int t0 = tok0 + (lr >= intl ? lr - intl : lr) * a.s_ttok;
       const int page = t0 / P;
       r0 = int4{i, ilt, intl, bt_row};
-      r1 = int4{tok0, n_end, rot, (share && page < Wc) ? bt_s[bt_row * Wc + page] : kNoBlock};
+      r1 = int4{tok0, n_end, rot, (share && page < Wc) ? L.bt_s[bt_row * Wc + page] : kNoBlock};
     }
     int4* rec = reinterpret_cast<int4*>(plan + kPlanWgRec + 8 * w);
     rec[0] = r0;
     rec[1] = r1;
   }
-  stamp(8);
   if (tid == 0) {
     plan[0] = V;
     plan[1] = carry;
   }
+}
+
+// The plan on its own (stage 3): check the key, rebuild when it differs.
+__global__ void __launch_bounds__(kPlanThreads) paged_decode_stream_plan_kernel(const DecodeArgs a) {
+  __shared__ PlanLds L;
+  __shared__ int tst_s[kSMaxBatch + kSMaxVirt + 1];
+  const bool same = plan_key_check<kPlanThreads>(a, L);
+  if (__syncthreads_and(same ? 1 : 0)) return;  // the previous plan still holds
+  plan_build<kPlanThreads>(a, L, tst_s);
 }
 
 // Walk parameters of stream entry i (i < V: virtual sequence i, else real
