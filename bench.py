@@ -96,13 +96,12 @@ def _time_queued(fn, calls: int, torch, *, reps: int = 5, flush=None) -> float:
     return times[len(times) // 2]
 
 
-def _cpu_baseline(w, budget_s: float, torch) -> dict:
-    """Time the CPU restatement of the reference decode path on a bounded sample."""
+def _cpu_decode_sample(w, budget_s: float, torch) -> dict:
+    """The CPU restatement of the reference decode path (paged_attention_reference.py:249-320)
+    over the first sequences of a decode workload, until ``budget_s`` of CPU time."""
 
     import oracle  # noqa: PLC0415  (checker/baseline only)
 
-    threads = len(os.sched_getaffinity(0))
-    torch.set_num_threads(threads)
     tables = w.block_tables.cpu()
     lens = w.context_lens.cpu()
     done_bytes = 0
@@ -126,14 +125,109 @@ def _cpu_baseline(w, budget_s: float, torch) -> dict:
         seqs += 1
         if elapsed >= budget_s:
             break
+    return {"GBps": round(done_bytes / elapsed / 1e9, 4), "seconds": round(elapsed, 2), "sequences": seqs,
+            "us_per_layer_equiv": round(elapsed / seqs * w.batch * 1e6, 1)}
+
+
+def _cpu_config1(dev, budget_s: float, torch, workloads) -> dict:
+    """Config 1 as the reference runs it on the CPU: B = 1, 2048 tokens in 8
+    pages of a 64-page pool, decode_reference_qdtype repeated for ``budget_s``."""
+
+    import oracle  # noqa: PLC0415
+
+    w = workloads.decode_single(dev)
+    q = w.q.cpu()
+    k = w.k_cache.view(torch.uint8).cpu().view(torch.float8_e4m3fn)
+    v = w.v_cache.view(torch.uint8).cpu().view(torch.float8_e4m3fn)
+    ks, vs = w.k_scale.cpu(), w.v_scale.cpu()
+    tables, lens = w.block_tables.cpu(), w.context_lens.cpu()
+    reps, elapsed = 0, 0.0
+    while elapsed < budget_s or reps < 3:
+        t0 = time.perf_counter()
+        oracle.decode_reference_qdtype(q, k, v, tables, lens, w.scale, k_scale_cache=ks, v_scale_cache=vs)
+        elapsed += time.perf_counter() - t0
+        reps += 1
+    s = elapsed / reps
+    return {"us_per_layer": round(s * 1e6, 1), "GBps": round(w.algorithmic_bytes() / s / 1e9, 4), "reps": reps,
+            "sample": "config 1 in full (B=1, 2048 tokens), reference CPU path (page gather, bf16 dequant, GQA "
+                      "expand, SDPA)"}
+
+
+def _cpu_store(dev, budget_s: float, torch, workloads) -> dict:
+    """Config 2's store as the reference's CPU path runs it (a per-token torch loop,
+    kv_cache_store.py:170-230) over the first tokens of the 8192-token chunk until
+    ``budget_s``; the whole chunk's time is extrapolated from the tokens done."""
+
+    import oracle  # noqa: PLC0415
+
+    sw = workloads.store_prefill(dev)
+    key, value, slots = sw.key.cpu(), sw.value.cpu(), sw.slot_mapping.cpu()
+    kc = torch.zeros(sw.num_pages, 256, 8, 128, dtype=torch.uint8).view(torch.float8_e4m3fn)
+    vc = torch.zeros_like(kc.view(torch.uint8)).view(torch.float8_e4m3fn)
+    ksc = torch.zeros(sw.num_pages, 256, 8)
+    vsc = torch.zeros_like(ksc)
+    done, elapsed, chunk = 0, 0.0, 256
+    while done < key.shape[0] and elapsed < budget_s:
+        sl = slice(done, done + chunk)
+        t0 = time.perf_counter()
+        oracle.store_scaled_torch_loop(key[sl], value[sl], kc, vc, slots[sl], ksc, vsc)
+        elapsed += time.perf_counter() - t0
+        done += key[sl].shape[0]
+    per_token = sw.algorithmic_bytes() / key.shape[0]
+    return {"us_chunk_equiv": round(elapsed / done * key.shape[0] * 1e6, 1),
+            "GBps": round(done * per_token / elapsed / 1e9, 5), "tokens": done,
+            "sample": f"first {done} of {key.shape[0]} tokens of config 2, reference CPU path (per-token loop)"}
+
+
+def _cpu_compaction(budget_s: float, torch, workloads) -> dict:
+    """Config 5's compaction as the reference's CPU path runs it
+    (index_select + index_copy_, kv_compaction.py:111-112) on payload and scale
+    caches at L = 1 (payload moved as bytes), whole plan, one call each."""
+
+    cw = workloads.compaction_plans()
+    slots = cw.num_pages * 256
+    src = torch.tensor([x for p in cw.plans for x in p.source_slots], dtype=torch.long)
+    dst = torch.tensor([x for p in cw.plans for x in p.destination_slots], dtype=torch.long)
+    payload = torch.zeros(2, 1, slots, 8, 128, dtype=torch.uint8)
+    scales = torch.zeros(2, 1, slots, 8, dtype=torch.float32)
+    import oracle  # noqa: PLC0415
+
+    reps, elapsed = 0, 0.0
+    while elapsed < budget_s or reps < 1:
+        t0 = time.perf_counter()
+        oracle.compact_slots_torch(payload, src, dst)
+        oracle.compact_slots_torch(scales, src, dst)
+        elapsed += time.perf_counter() - t0
+        reps += 1
+    s = elapsed / reps
+    del payload, scales
+    return {"us": round(s * 1e6, 1), "GBps": round(cw.algorithmic_bytes() / s / 1e9, 4), "reps": reps,
+            "kept_tokens": cw.kept, "sample": "config 5 compaction in full (64 prefixes, out of place, payload + "
+                                              "scales, L = 1), index_select + index_copy_"}
+
+
+def _cpu_baseline(w, budget_s: float, torch, dev, workloads) -> dict:
+    """CPU baselines on the GPU box's host cores: the headline decode sample
+    (``value``) and configs 1, 2 (store) and 5 (compaction) as the reference's
+    CPU paths run them, restated in ``oracle/``."""
+
+    threads = len(os.sched_getaffinity(0))
+    torch.set_num_threads(threads)
+    dec = _cpu_decode_sample(w, 0.4 * budget_s, torch)
+    configs = {
+        "config1_decode_b1": _cpu_config1(dev, 0.15 * budget_s, torch, workloads),
+        "config2_store": _cpu_store(dev, 0.25 * budget_s, torch, workloads),
+        "config5_compaction": _cpu_compaction(0.2 * budget_s, torch, workloads),
+    }
     return {
-        "value": round(done_bytes / elapsed / 1e9, 4),
+        "value": dec["GBps"],
         "unit": "GB/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"first {seqs} of {w.batch} decode_mixed sequences, reference CPU path "
-                  f"(page gather + bf16 dequant + GQA expand + SDPA), {elapsed:.1f} s",
-        "us_per_layer_equiv": round(elapsed / seqs * w.batch * 1e6, 1),
+        "sample": f"first {dec['sequences']} of {w.batch} decode_mixed sequences, reference CPU path "
+                  f"(page gather + bf16 dequant + GQA expand + SDPA), {dec['seconds']} s",
+        "us_per_layer_equiv": dec["us_per_layer_equiv"],
+        "configs": configs,
     }
 
 
@@ -143,7 +237,7 @@ def main() -> int:
     parser.add_argument("--steps", type=int, default=50)
     parser.add_argument("--warmup", type=int, default=100)
     parser.add_argument("--layers", type=int, default=4, help="independent KV pools the steps rotate over")
-    parser.add_argument("--cpu-budget", type=float, default=15.0, help="seconds of CPU baseline work")
+    parser.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU baseline work")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-extras", action="store_true", help="skip store/compaction/single-sequence extras")
     parser.add_argument("--copy-probe", action="store_true",
@@ -293,7 +387,7 @@ def main() -> int:
 
     if not args.no_cpu_baseline:
         _log("cpu baseline")
-        result["cpu_baseline"] = _cpu_baseline(base, args.cpu_budget, torch)
+        result["cpu_baseline"] = _cpu_baseline(base, args.cpu_budget, torch, dev, workloads)
     else:
         result["cpu_baseline"] = None
     print(json.dumps(result), flush=True)

@@ -33,6 +33,7 @@ __all__ = [
     "e4m3fn_encode_bit_range",
     "e4m3fn_decode_table",
     "store_scaled",
+    "store_scaled_torch_loop",
     "store_unit",
     "compact_slots",
     "compact_slots_torch",
@@ -150,6 +151,33 @@ def store_scaled(key, value, k_cache, v_cache, slot_mapping, k_scale_cache, v_sc
         kc.data_ptr(), vc.data_ptr(), k_scale_cache.data_ptr(), v_scale_cache.data_ptr(),
         slots.data_ptr(), num_tokens, num_heads, head_dim, kc.numel() // (num_heads * head_dim),
     )
+
+
+def store_scaled_torch_loop(key, value, k_cache, v_cache, slot_mapping, k_scale_cache, v_scale_cache) -> None:
+    """The reference's CPU store path as it runs: a Python loop over tokens with
+    torch ops per token (``_store_kvcache_eager``, ops/kv_cache_store.py:170-227).
+
+    Per token with slot >= 0 and per head: s = max(amax|x| / 448, 1e-6) in
+    fp32, payload = clamp(x / s, -448, 448) cast to E4M3FN (torch's RNE cast).
+    It is what ``bench.py``'s CPU baseline times for the store; the tests pin
+    it to the C restatement above byte for byte.
+    """
+
+    _check_cpu(key, value, k_cache, v_cache, slot_mapping, k_scale_cache, v_scale_cache)
+    heads, dim = k_cache.shape[-2], k_cache.shape[-1]
+    kc = k_cache.view(-1, heads, dim)
+    vc = v_cache.view(-1, heads, dim)
+    ksc = k_scale_cache.view(-1, heads)
+    vsc = v_scale_cache.view(-1, heads)
+    slots = slot_mapping.tolist()
+    for t, slot in enumerate(slots):
+        if slot < 0:
+            continue
+        for src, payload, scales in ((key[t], kc, ksc), (value[t], vc, vsc)):
+            xf = src.float()
+            s = (xf.abs().amax(dim=-1) / 448.0).clamp(min=1.0e-6)
+            payload[slot] = (xf / s[:, None]).clamp(-448.0, 448.0).to(payload.dtype)
+            scales[slot] = s
 
 
 def store_unit(key, value, k_cache, v_cache, slot_mapping) -> None:

@@ -159,3 +159,32 @@ def test_strided_input_and_out_of_range_slots():
     for slot in range(8):
         if slot not in written:
             assert torch.all(ks[slot] == -1.0)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_torch_loop_store_equals_c_restatement(dtype):
+    """The per-token torch loop (the CPU path bench.py times as the store baseline)
+    writes the same bytes and scales as the C restatement, outliers, zero rows,
+    skipped (-1) slots and untouched slots included."""
+
+    from oracle import store_scaled_torch_loop
+
+    g = torch.Generator().manual_seed(20260903)
+    tokens, heads, dim, pages, page = 64, 8, 128, 3, 32
+    key = torch.randn(tokens, heads, dim, generator=g)
+    key[torch.rand(key.shape, generator=g) < 0.01] *= 20.0
+    key[5] = 0.0
+    value = torch.randn(tokens, heads, dim, generator=g) * 1e-3
+    key, value = key.to(dtype), value.to(dtype)
+    slots = torch.randperm(pages * page, generator=g)[:tokens].to(torch.int32)
+    slots[7] = -1
+    caches = []
+    for fn in (store_scaled, store_scaled_torch_loop):
+        kc = torch.full((pages, page, heads, dim), 0x33, dtype=torch.uint8).view(FP8)
+        vc = torch.full_like(kc.view(torch.uint8), 0x44).view(FP8)
+        ks = torch.full((pages, page, heads), 9.0)
+        vs = torch.full_like(ks, 9.0)
+        fn(key, value, kc, vc, slots, ks, vs)
+        caches.append((kc.view(torch.uint8), vc.view(torch.uint8), ks, vs))
+    for a, b in zip(*caches):
+        assert torch.equal(a, b)
