@@ -394,6 +394,31 @@ def main() -> int:
     return 0
 
 
+def _check_long_sample(lw, out, torch) -> dict:
+    """Compare two sequences of the chained config-5 decode (one starting with
+    a compacted prefix, one private) with the CPU oracle, pages copied only."""
+
+    import oracle  # noqa: PLC0415  (checker only)
+
+    rows = torch.tensor([0, lw.batch - 1])
+    tables = lw.block_tables.cpu().to(torch.int64)[rows]
+    pages = torch.unique(tables[tables >= 0])
+    remap = torch.full((lw.k_cache.shape[0],), -1, dtype=torch.int64)
+    remap[pages] = torch.arange(pages.numel())
+    local = torch.where(tables >= 0, remap[tables.clamp(min=0)], tables).to(torch.int32)
+    idx = pages.to(lw.k_cache.device)
+    k = lw.k_cache.view(torch.uint8).index_select(0, idx).cpu().view(torch.float8_e4m3fn)
+    v = lw.v_cache.view(torch.uint8).index_select(0, idx).cpu().view(torch.float8_e4m3fn)
+    ks, vs = lw.k_scale.index_select(0, idx).cpu(), lw.v_scale.index_select(0, idx).cpu()
+    want = oracle.decode_kernel_semantics(lw.q.cpu()[rows], k, v, local, lw.context_lens.cpu()[rows], lw.scale,
+                                          k_scale_cache=ks, v_scale_cache=vs, compute_dtype=torch.float32)
+    got = out.cpu()[rows].float()
+    err = (got - want.float()).abs()
+    bound = 2e-2 + 1e-2 * want.float().abs()
+    return {"sequences": rows.tolist(), "max_abs_err": round(float(err.max()), 6),
+            "within_tolerance": bool(torch.all(err <= bound))}
+
+
 def _tp_shard(base, torch, tp: int, steps: int = 50) -> dict:
     """One tensor-parallel rank's share of the headline step at TP = tp: the
     same sequences and pages with the first 8 / tp of the 8 kv heads (a
@@ -475,16 +500,29 @@ def _extras(torch, dev, workloads) -> dict:
     scratch = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
     flush = lambda: scratch.fill_(1)
     out = {}
-    # store: 8192 tokens into a 512-page pool
+    # The queued timing of one call has a fixed floor (the start event, then
+    # the launch): measure it with a one-element kernel, to read short calls.
+    tiny = torch.zeros(1, device=dev)
+    out["queued_call_floor_us"] = round(_time_queued(lambda i: tiny.add_(1), 1, torch, flush=flush) * 1e6, 2)
+    # store: 8192 tokens into a 512-page pool; one call cold, and 8 calls back
+    # to back over 8 distinct input chunks (268 MB, more than the MALL), as a
+    # prefill's layers issue them
     sw = workloads.store_prefill(dev)
     kc = torch.empty(sw.num_pages, 256, 8, 128, dtype=torch.float8_e4m3fn, device=dev)
     vc = torch.empty_like(kc)
     ks = torch.empty(sw.num_pages, 256, 8, dtype=torch.float32, device=dev)
     vs = torch.empty_like(ks)
-    s = _time_queued(lambda i: store_kvcache(sw.key, sw.value, kc, vc, sw.slot_mapping, ks, vs), 1, torch, flush=flush)
-    out["store_prefill"] = {"us": round(s * 1e6, 2), "GBps": round(sw.algorithmic_bytes() / s / 1e9, 1),
-                            "bytes": sw.algorithmic_bytes(), "timing": "queued behind a spin, cold"}
-    del kc, vc, ks, vs
+    s1 = _time_queued(lambda i: store_kvcache(sw.key, sw.value, kc, vc, sw.slot_mapping, ks, vs), 1, torch,
+                      flush=flush)
+    keys = [sw.key.roll(i, 0) for i in range(8)]
+    values = [sw.value.roll(i, 0) for i in range(8)]
+    s8 = _time_queued(lambda i: store_kvcache(keys[i], values[i], kc, vc, sw.slot_mapping, ks, vs), 8, torch,
+                      flush=flush)
+    out["store_prefill"] = {"us": round(s8 * 1e6, 2), "GBps": round(sw.algorithmic_bytes() / s8 / 1e9, 1),
+                            "us_single_call": round(s1 * 1e6, 2), "bytes": sw.algorithmic_bytes(),
+                            "timing": "8 calls back to back over 8 distinct cold input chunks, queued behind a "
+                                      "spin (us_single_call: one cold call, including the queued-call floor)"}
+    del kc, vc, ks, vs, keys, values
     # compaction: 64 x 8192-token prefixes, ~30% dropped, out of place, payload + scales (L=1)
     cw = workloads.compaction_plans()
     slots = cw.num_pages * 256
@@ -498,9 +536,18 @@ def _extras(torch, dev, workloads) -> dict:
         compact_kv_slots(scales, src, dst)
 
     s = _time_queued(compact, 1, torch, flush=flush)
+    # the practical ceiling of a gather/scatter copy: a 1 GiB device copy, cold
+    big = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
+    big2 = torch.empty_like(big)
+    sc = _time_queued(lambda i: big2.copy_(big), 1, torch, flush=flush)
+    copy_gbps = 2 * big.numel() / sc / 1e9
+    del big, big2
     out["compaction_out_of_place"] = {"us": round(s * 1e6, 2), "GBps": round(cw.algorithmic_bytes() / s / 1e9, 1),
                                       "bytes": cw.algorithmic_bytes(), "kept_tokens": cw.kept,
-                                      "timing": "queued behind a spin, cold"}
+                                      "copy_probe_GBps": round(copy_gbps, 1),
+                                      "frac_of_copy_probe": round(cw.algorithmic_bytes() / s / 1e9 / copy_gbps, 4),
+                                      "timing": "queued behind a spin, cold (payload and scale calls); copy probe: "
+                                                "1 GiB device-to-device copy, read + write bytes, cold"}
     del payload, scales, src, dst
     # single-sequence decode (latency bound): Qwen3-VL-shaped, B=1, 1800 tokens, 36 layers with their own pools
     layers = [workloads.decode_qwen_vl(dev, seed=20260803 + li) for li in range(36)]
@@ -512,15 +559,21 @@ def _extras(torch, dev, workloads) -> dict:
                                 "GBps": round(layers[0].algorithmic_bytes() / s / 1e9, 1),
                                 "timing": "36 layers back to back, queued behind a spin, cold"}
     del layers
-    # long-context decode (config 5): B = 256 at 32k tokens each, pages scattered in a ~120 GB pool
-    lw = workloads.decode_long(dev, pool_pages=LONG_POOL_PAGES)
-    s = _time_queued(lambda i: paged_decode_attention(
+    # config 5 as a chain: compaction of 64 prefixes into dense pages, then
+    # decode of B = 256 at 32k tokens each (sequences 0..63 start with their
+    # compacted prefix pages), pages scattered in a ~120 GB pool
+    lw = workloads.decode_long_compacted(dev, pool_pages=LONG_POOL_PAGES)
+    call = lambda i: paged_decode_attention(
         lw.q, lw.k_cache, lw.v_cache, lw.block_tables, lw.context_lens, lw.scale, k_scale_cache=lw.k_scale,
-        v_scale_cache=lw.v_scale, max_context_len=lw.max_context_len), 3, torch, flush=flush)
+        v_scale_cache=lw.v_scale, max_context_len=lw.max_context_len)
+    s = _time_queued(call, 3, torch, flush=flush)
+    check = _check_long_sample(lw, call(0), torch)
     pool_bytes = sum(t.numel() * t.element_size() for t in (lw.k_cache, lw.v_cache, lw.k_scale, lw.v_scale))
     out["decode_long_b256"] = {"us": round(s * 1e6, 1), "GBps": round(lw.algorithmic_bytes() / s / 1e9, 1),
                                "pct_of_hbm_peak": round(100.0 * lw.algorithmic_bytes() / s / 1e9 / HBM_PEAK_GBPS, 2),
                                "bytes": lw.algorithmic_bytes(), "pool_GB": round(pool_bytes / 1e9, 1),
+                               "compacted_prefixes": lw.meta["compacted"],
+                               "compacted_kept_tokens": lw.meta["compaction"].kept, "check": check,
                                "timing": "3 calls back to back, queued behind a spin, cold"}
     del lw
     # paged prefill: 4 sequences x (8192 cached + 2048 new tokens), causal

@@ -76,7 +76,7 @@ def _compile(src: Path, build_dir: Path = BUILD_DIR, defines: tuple = ()) -> Pat
     return obj
 
 
-def build(verbose: bool = True, *, out_dir: Path = OUT_DIR, measure: bool = False) -> Path:
+def build(verbose: bool = True, *, out_dir: Path = OUT_DIR, measure: bool = False, defines: tuple = ()) -> Path:
     """Compile all sources and link the shared library; returns its path.
 
     ``measure=True`` builds the measurement variant (PRISM_DECODE_MEASURE:
@@ -84,10 +84,13 @@ def build(verbose: bool = True, *, out_dir: Path = OUT_DIR, measure: bool = Fals
     the product library never has them.
     """
 
-    build_dir = BUILD_DIR / ("measure" if measure else "product")
+    tag = "measure" if measure else "product"
+    if defines:
+        tag += "-" + "-".join(d.replace("=", "") for d in defines)
+    build_dir = BUILD_DIR / tag
     build_dir.mkdir(parents=True, exist_ok=True)
     out_dir.mkdir(parents=True, exist_ok=True)
-    defines = ("PRISM_DECODE_MEASURE",) if measure else ()
+    defines = (("PRISM_DECODE_MEASURE",) if measure else ()) + tuple(defines)
     sources = sorted(CSRC.glob("*.hip"))
     if not sources:
         raise RuntimeError(f"no HIP sources under {CSRC}")

@@ -198,6 +198,100 @@ def decode_long(device, seed: int = 20260805, *, batch: int = 256, context_len: 
                    batch * context_len, fill=fill)
 
 
+def fill_slots(k_cache, v_cache, k_scale, v_scale, slots: torch.Tensor, seed: int, *, chunk: int = 1 << 17) -> None:
+    """Fill individual slots (flat ``block * P + offset``) with quantised bf16 N(0,1) K/V."""
+
+    from prism_infer.ops.kv_cache_store import store_kvcache  # noqa: PLC0415
+
+    device = k_cache.device
+    _, _, kv_heads, dim = k_cache.shape
+    gen = torch.Generator(device=device)
+    gen.manual_seed(seed)
+    slots = slots.to(device=device, dtype=torch.int32)
+    for start in range(0, slots.numel(), chunk):
+        sl = slots[start:start + chunk]
+        key = torch.randn(sl.numel(), kv_heads, dim, generator=gen, device=device, dtype=torch.bfloat16)
+        value = torch.randn(sl.numel(), kv_heads, dim, generator=gen, device=device, dtype=torch.bfloat16)
+        store_kvcache(key, value, k_cache, v_cache, sl, k_scale, v_scale)
+
+
+def decode_long_compacted(device, seed: int = 20260805, *, batch: int = 256, context_len: int = 32768,
+                          compacted: int = 64, pool_pages: int | None = None) -> DecodeWorkload:
+    """Config 5 as one chain: compaction, then long-context decode over its output.
+
+    The 64 prefixes of :func:`compaction_plans` (8192 tokens each, ~30 % of
+    the visual positions dropped) are written into their source pages, then
+    moved with ``compact_kv_slots`` (payload and scales of K and V) into new
+    dense destination pages.  Sequences ``0 .. compacted - 1`` of the decode
+    batch start with those destination pages: their first ``kept`` tokens are
+    the compacted prefix and the following ``context_len - kept`` tokens fill
+    the rest of the last destination page and private pages, as later tokens
+    of a compacted sequence do (kv_compaction_coordinator.py:86-98; the block
+    table keeps the compacted prefix and grows after it).  The other
+    sequences hold ``context_len`` tokens in private pages.  Pages are
+    scattered over a pool of ``pool_pages`` pages.  ``meta`` carries the
+    compaction plans and slot tensors for checking.
+    """
+
+    from prism_infer.ops.kv_compaction import compact_kv_slots  # noqa: PLC0415
+
+    pages_per = math.ceil(context_len / PAGE_SIZE)
+    cw_need = compacted * (8192 // PAGE_SIZE) * 2
+    need = cw_need + batch * pages_per
+    pool_pages = pool_pages or need
+    if pool_pages < need:
+        raise RuntimeError(f"pool of {pool_pages} pages is smaller than the {need} the chain needs")
+    cw = compaction_plans(prefixes=compacted, pool_pages=pool_pages)
+    g = _gen(seed)
+    taken = set()
+    for plan in cw.plans:
+        taken.update(plan.old_block_table)
+        taken.update(plan.new_block_table)
+    free = [p for p in torch.randperm(pool_pages, generator=g).tolist() if p not in taken]
+    k, v, ks, vs = _alloc_pool(pool_pages, device)
+    # 1. the prefixes' K/V in their source pages, then the compaction
+    src_pages = torch.tensor(sorted({p for plan in cw.plans for p in plan.old_block_table}), dtype=torch.int64)
+    fill_pages(k, v, ks, vs, src_pages, seed + 2)
+    src = torch.tensor([x for plan in cw.plans for x in plan.source_slots], dtype=torch.long, device=device)
+    dst = torch.tensor([x for plan in cw.plans for x in plan.destination_slots], dtype=torch.long, device=device)
+    n_slots = pool_pages * PAGE_SIZE
+    compact_kv_slots(k.view(1, 1, n_slots, NUM_KV_HEADS, HEAD_DIM), src, dst)
+    compact_kv_slots(v.view(1, 1, n_slots, NUM_KV_HEADS, HEAD_DIM), src, dst)
+    compact_kv_slots(ks.view(1, 1, n_slots, NUM_KV_HEADS), src, dst)
+    compact_kv_slots(vs.view(1, 1, n_slots, NUM_KV_HEADS), src, dst)
+    # 2. block tables: compacted prefix pages, then private pages
+    tables = torch.full((batch, pages_per), -1, dtype=torch.int32)
+    cursor = 0
+    tail_slots = []
+    private_pages = []
+    for b in range(batch):
+        if b < compacted:
+            plan = cw.plans[b]
+            kept = plan.physical_prompt_len
+            head = list(plan.new_block_table)
+            used_in_last = kept - (len(head) - 1) * PAGE_SIZE
+            last = head[-1]
+            tail_slots.extend(last * PAGE_SIZE + o for o in range(used_in_last, PAGE_SIZE))
+            rest = max(0, math.ceil((context_len - len(head) * PAGE_SIZE) / PAGE_SIZE))
+            row = head + free[cursor:cursor + rest]
+        else:
+            rest = pages_per
+            row = free[cursor:cursor + rest]
+        private_pages.extend(free[cursor:cursor + rest])
+        cursor += rest
+        tables[b, :len(row)] = torch.tensor(row, dtype=torch.int32)
+    if cursor > len(free):
+        raise RuntimeError("pool too small for the decode batch")
+    # 3. the tokens after each compacted prefix, and every private page
+    fill_slots(k, v, ks, vs, torch.tensor(tail_slots, dtype=torch.int64), seed + 3)
+    fill_pages(k, v, ks, vs, torch.tensor(private_pages, dtype=torch.int64), seed + 1)
+    q = torch.randn(batch, NUM_HEADS, HEAD_DIM, generator=g, dtype=torch.bfloat16).to(device)
+    used = torch.unique(tables[tables >= 0].to(torch.int64))
+    meta = {"compaction": cw, "compaction_src": src, "compaction_dst": dst, "compacted": compacted}
+    return _finish("decode_long_compacted", q, (k, v, ks, vs), tables, [context_len] * batch, seed, used,
+                   batch * context_len, meta=meta, fill=False)
+
+
 @dataclass
 class PrefillWorkload:
     q: torch.Tensor                     # [total_q, Hq, D] bf16
@@ -337,9 +431,11 @@ __all__ = [
     "StoreWorkload",
     "compaction_plans",
     "decode_long",
+    "decode_long_compacted",
     "decode_mixed",
     "decode_qwen_vl",
     "decode_single",
     "fill_pages",
+    "fill_slots",
     "store_prefill",
 ]

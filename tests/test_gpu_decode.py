@@ -225,17 +225,28 @@ def test_mixed_batch_north_star_config(decode_path):
 
 
 def test_long_context_b256_config(monkeypatch):
-    """Config 5's decode at full shape: B=256, 32k tokens each, pages scattered in the pool.
+    """Config 5 as a chain: compaction of 64 prefixes into new dense pages, then
+    decode at full shape (B=256, 32k tokens each, pages scattered in the pool)
+    with sequences 0..63 starting with their compacted prefix pages.
 
-    Both kernel families on every sequence, agreeing within the decode
-    tolerance, and the CPU oracle on a sample of sequences (copied pages only).
+    The compaction moved every kept slot (destination bytes equal source bytes,
+    payload and scales of K and V); both kernel families agree on every
+    sequence within the decode tolerance; the CPU oracle matches a sample of
+    compacted and private sequences (copied pages only).
     """
 
     require_gpu()
     from prism_infer.ops.paged_decode import paged_decode_attention
-    from prism_infer.workloads import decode_long
+    from prism_infer.workloads import decode_long_compacted
 
-    w = decode_long(torch.device("cuda"))
+    w = decode_long_compacted(torch.device("cuda"))
+    src, dst = w.meta["compaction_src"], w.meta["compaction_dst"]
+    for cache, row in ((w.k_cache, (8, 128)), (w.v_cache, (8, 128)), (w.k_scale, (8,)), (w.v_scale, (8,))):
+        flat = cache.view(torch.uint8) if cache.dtype == FP8 else cache
+        flat = flat.reshape(-1, *row)
+        assert torch.equal(flat.index_select(0, dst), flat.index_select(0, src)), "compacted prefix differs"
+    kept = [p.physical_prompt_len for p in w.meta["compaction"].plans]
+    print(f"compacted 64 prefixes: kept {sum(kept)} tokens ({min(kept)}..{max(kept)} per prefix)", flush=True)
     run = lambda: paged_decode_attention(w.q, w.k_cache, w.v_cache, w.block_tables, w.context_lens, w.scale,
                                          k_scale_cache=w.k_scale, v_scale_cache=w.v_scale,
                                          max_context_len=w.max_context_len)
@@ -245,7 +256,7 @@ def test_long_context_b256_config(monkeypatch):
     out_split = run()
     torch.cuda.synchronize()
     assert_decode_close(out_stream, out_split, label="decode_long stream vs split")
-    rows = torch.tensor([0, 97, 255])
+    rows = torch.tensor([0, 17, 63, 64, 255])
     pages = torch.unique(w.block_tables[rows.to(w.block_tables.device)].cpu().to(torch.int64))
     q, k, v, ks, vs, tables, lens, mx = compact_to_cpu(w, page_ids=pages)
     want = oracle.decode_kernel_semantics(q[rows], k, v, tables[rows], lens[rows], w.scale, k_scale_cache=ks,
