@@ -114,6 +114,31 @@ int prism_paged_decode(const void* q, int q_dtype, const int64_t q_strides[3], c
                        float scale, void* workspace, int64_t workspace_bytes, void* stream);
 
 /*
+ * Allocation-free paged decode.  NO COUNTERPART IN THE REFERENCE: for callers
+ * that cannot allocate device memory or pass a workspace (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid allocation).
+ * Same arguments, semantics and results as prism_paged_decode minus the
+ * workspace: the library keeps a file-scope 64 MiB (67,108,864-byte) scratch
+ * array per GPU (held until the process ends) and uses it as the workspace.
+ * A geometry whose prism_paged_decode_workspace_bytes() exceeds 64 MiB is
+ * rejected with PRISM_ERR_INVALID (e.g. B = 256 at 32k tokens needs about
+ * 36 MiB and fits).  Calls no hipMalloc, hipFree or allocating library
+ * routine.  Every call on one GPU shares that GPU's scratch: calls that
+ * overlap on one GPU (different streams, or different host threads) race
+ * and must be serialised by the caller.
+ */
+int prism_paged_decode_noalloc(const void* q, int q_dtype, const int64_t q_strides[3],
+                               const void* k_cache, const void* v_cache, int cache_dtype,
+                               const int64_t k_strides[4], const int64_t v_strides[4],
+                               const float* k_scale, const float* v_scale,
+                               const int64_t ks_strides[3], const int64_t vs_strides[3],
+                               const int32_t* block_tables, const int64_t bt_strides[2],
+                               const int32_t* context_lens, const int32_t* max_context_len, void* out,
+                               const int64_t out_strides[3], int batch, int num_heads, int num_kv_heads,
+                               int head_dim, int page_size, int64_t num_blocks, int max_blocks_per_seq,
+                               float scale, void* stream);
+
+/*
  * Stage selector for measurement: the same as prism_paged_decode but runs only
  * one part of it.  stage 0 runs everything and is identical to
  * prism_paged_decode; stage 1 runs only the partial kernel (split-K or

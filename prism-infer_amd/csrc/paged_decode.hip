@@ -28,6 +28,7 @@
 // Generic path (any other supported shape): one wave per (sequence, q head),
 //   lane-per-token scores, lane-per-dim accumulation, no split-K.
 #include <atomic>
+#include <mutex>
 
 #include "common.h"
 #include "fp8_mfma.h"
@@ -2420,5 +2421,84 @@ extern "C" int prism_paged_decode(const void* q, int q_dtype, const int64_t q_st
                                   k_scale, v_scale, ks_strides, vs_strides, block_tables, bt_strides, context_lens,
                                   max_context_len, out, out_strides, batch, num_heads, num_kv_heads, head_dim,
                                   page_size, num_blocks, max_blocks_per_seq, scale, workspace, workspace_bytes,
+                                  stream);
+}
+
+// ------------------------------------------------------- allocation-free entry
+
+namespace prism {
+namespace {
+
+// Scratch of prism_paged_decode_noalloc: the decode workspace (streaming
+// plan, partials, merge counters) of callers that cannot allocate.  Each GPU
+// the library runs on holds its own copy until the process ends.  Host code
+// must not use the array's name as a device address: the address of each
+// device's copy comes from hipGetSymbolAddress, once per device.
+constexpr int64_t kNoAllocScratchBytes = int64_t{64} << 20;
+__device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The current device's copy of `scratch` (looked up on its first use).
+int scratch_for_current_device(void** out) {
+  int dev = 0;
+  if (int rc = check_hip(hipGetDevice(&dev), "prism_paged_decode_noalloc: hipGetDevice")) return rc;
+  if (dev < 0 || dev >= kMaxDevices) {
+    set_error("prism_paged_decode_noalloc: device ordinal %d is out of range", dev);
+    return PRISM_ERR_INVALID;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    if (int rc = check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)),
+                           "prism_paged_decode_noalloc: hipGetSymbolAddress"))
+      return rc;
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return PRISM_OK;
+}
+
+}  // namespace
+}  // namespace prism
+
+extern "C" int prism_paged_decode_noalloc(const void* q, int q_dtype, const int64_t q_strides[3],
+                                          const void* k_cache, const void* v_cache, int cache_dtype,
+                                          const int64_t k_strides[4], const int64_t v_strides[4],
+                                          const float* k_scale, const float* v_scale,
+                                          const int64_t ks_strides[3], const int64_t vs_strides[3],
+                                          const int32_t* block_tables, const int64_t bt_strides[2],
+                                          const int32_t* context_lens, const int32_t* max_context_len, void* out,
+                                          const int64_t out_strides[3], int batch, int num_heads,
+                                          int num_kv_heads, int head_dim, int page_size, int64_t num_blocks,
+                                          int max_blocks_per_seq, float scale, void* stream) {
+  using namespace prism;
+  clear_error();
+  const int64_t need = prism_paged_decode_workspace_bytes(batch, num_heads, num_kv_heads, head_dim, page_size,
+                                                          max_blocks_per_seq, cache_dtype);
+  if (need < 0) {
+    set_error("prism_paged_decode_noalloc: invalid geometry");
+    return PRISM_ERR_INVALID;
+  }
+  if (need > kNoAllocScratchBytes) {
+    set_error("prism_paged_decode_noalloc: this geometry needs %lld bytes of workspace, more than the %lld-byte "
+              "scratch of the allocation-free entry point; use prism_paged_decode with a workspace",
+              static_cast<long long>(need), static_cast<long long>(kNoAllocScratchBytes));
+    return PRISM_ERR_INVALID;
+  }
+  void* ws = nullptr;
+  if (need > 0) {
+    if (int rc = scratch_for_current_device(&ws)) return rc;
+  }
+  // Nothing in the scratch needs clearing: the streaming plan carries the key
+  // of the inputs it was computed from (a stale or zero plan is rebuilt, and
+  // its rebuild zeroes the merge counters), and split partials are written
+  // before they are read.
+  return prism_paged_decode_stage(0, q, q_dtype, q_strides, k_cache, v_cache, cache_dtype, k_strides, v_strides,
+                                  k_scale, v_scale, ks_strides, vs_strides, block_tables, bt_strides, context_lens,
+                                  max_context_len, out, out_strides, batch, num_heads, num_kv_heads, head_dim,
+                                  page_size, num_blocks, max_blocks_per_seq, scale, ws, need > 0 ? need : 0,
                                   stream);
 }

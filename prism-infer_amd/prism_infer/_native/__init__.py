@@ -53,6 +53,11 @@ SIGNATURES: dict[str, tuple] = {
         [_VP, _I, _I64P, _VP, _VP, _I, _I64P, _I64P, _VP, _VP, _I64P, _I64P, _VP, _I64P, _VP, _VP, _VP,
          _I64P, _I, _I, _I, _I, _I, _I64, _I, _F, _VP, _I64, _VP],
     ),
+    "prism_paged_decode_noalloc": (
+        _I,
+        [_VP, _I, _I64P, _VP, _VP, _I, _I64P, _I64P, _VP, _VP, _I64P, _I64P, _VP, _I64P, _VP, _VP, _VP,
+         _I64P, _I, _I, _I, _I, _I, _I64, _I, _F, _VP],
+    ),
     "prism_paged_decode_stage": (
         _I,
         [_I, _VP, _I, _I64P, _VP, _VP, _I, _I64P, _I64P, _VP, _VP, _I64P, _I64P, _VP, _I64P, _VP, _VP, _VP,
