@@ -92,13 +92,14 @@ int prism_kv_store(const void* key, const void* value, int in_dtype, const int64
  * out        : [batch, num_heads, head_dim] of q_dtype, strides out_strides.
  * workspace  : device scratch of at least prism_paged_decode_workspace_bytes()
  *              bytes for the same geometry; may be NULL when that function
- *              returns 0.  It holds split-K partials and, for the streaming
- *              kernel, a work plan (prefix-sharing groups, tile ranges)
- *              together with the inputs it was computed from; a call whose
- *              block tables and context lengths equal those of the previous
- *              call on the same workspace reuses the plan.  Any initial
- *              contents are valid.  Calls that share a workspace must be
- *              ordered on one stream.
+ *              returns 0.  It holds split-K partials with their arrival
+ *              counters (tagged per call, so leftovers of any other call or
+ *              use count as zero) and, for the streaming kernel, a work plan
+ *              (prefix-sharing groups, tile ranges) together with the inputs
+ *              it was computed from; a call whose block tables and context
+ *              lengths equal those of the previous call on the same
+ *              workspace reuses the plan.  Any initial contents are valid.
+ *              Calls that share a workspace must be ordered on one stream.
  */
 int64_t prism_paged_decode_workspace_bytes(int batch, int num_heads, int num_kv_heads, int head_dim,
                                            int page_size, int max_blocks_per_seq, int cache_dtype);
@@ -141,11 +142,12 @@ int prism_paged_decode_noalloc(const void* q, int q_dtype, const int64_t q_strid
 /*
  * Stage selector for measurement: the same as prism_paged_decode but runs only
  * one part of it.  stage 0 runs everything and is identical to
- * prism_paged_decode; stage 1 runs only the partial kernel (split-K or
- * streaming); stage 2 only the merge of the partials; stage 3 only the
- * streaming kernel's plan (nothing for the other kernels).  Stage 1 of the
- * streaming kernel uses the plan already in the workspace: run stage 0 or 3
- * with the same inputs first.
+ * prism_paged_decode; stage 1 runs the decode kernel without the streaming
+ * kernel's plan (both the split-K and the streaming kernel merge their own
+ * partials in the same launch, so stage 1 of those is the whole decode and
+ * stage 2 launches nothing); stage 3 only the streaming kernel's plan
+ * (nothing for the other kernels).  Stage 1 of the streaming kernel uses the
+ * plan already in the workspace: run stage 0 or 3 with the same inputs first.
  */
 int prism_paged_decode_stage(int stage, const void* q, int q_dtype, const int64_t q_strides[3],
                              const void* k_cache, const void* v_cache, int cache_dtype,

@@ -7,11 +7,10 @@
 // K and V are dequantised with their per-token, per-head fp32 scales; online
 // softmax in fp32; a sequence with no attended token outputs zeros.
 //
-// Fast path (FP8 cache, head_dim 128, <= 8 kv heads, G <= 16):
-//   grid (batch, splits); one workgroup per (sequence, split of SPLIT tokens)
-//   with one wave per kv head, so the workgroup streams a contiguous
-//   [32 tokens x Hkv x 128 B] slab of K and of V per tile.  Per 32-token tile
-//   and wave:
+// Split-K path (FP8 cache, head_dim 128, <= 8 kv heads, G <= 16):
+//   grid (batch, kv heads, chunks); one workgroup per (sequence, kv head,
+//   chunk of SPLIT tokens), its eight waves on neighbouring 32-token tiles of
+//   that head.  Per tile and wave:
 //     QK: 2 x 4 MFMA f32_16x16x32_bf16, A = K rows (fp8 -> bf16 exact),
 //         B = Q^T (G valid columns of 16).  Lane (g, c) receives the scores of
 //         q head c for tokens 4g+i and 16+4g+i.
@@ -23,8 +22,9 @@
 //         output column c of N-tile j mapped to dim 8c + j, so each lane loads
 //         8 contiguous bytes per token and the byte transpose is one v_perm
 //         plus two native fp8 -> bf16 conversions per 4 values.
-//   Sequences longer than SPLIT write (m, l, acc) partials and a combine
-//   kernel merges them; single-split sequences are written directly.
+//   The waves merge through LDS.  A sequence with one chunk writes its output
+//   directly; otherwise each chunk writes an (m, l, acc) partial and the last
+//   chunk of (sequence, kv head) to finish merges them in the same launch.
 // Generic path (any other supported shape): one wave per (sequence, q head),
 //   lane-per-token scores, lane-per-dim accumulation, no split-K.
 #include <atomic>
@@ -77,8 +77,10 @@ struct DecodeArgs {
   int batch, num_heads, num_kv_heads, groups, page_size, width, head_dim;
   int64_t num_blocks;
   int q_vec;     // q rows are 16-byte aligned with unit dim stride
-  int split;     // tokens per split (multiple of kTile)
-  int max_splits;
+  int split;     // split-K path: tokens per chunk (multiple of 8 tiles)
+  int max_splits;  // split-K path: chunks per (sequence, kv head)
+  unsigned long long* split_cnt;  // split-K path: arrival counters, [batch][kv heads]
+  unsigned int epoch;             // split-K path: this call's counter tag (nonzero)
   float scale_log2;  // sm_scale * log2(e)
   int cache_dtype;
   int debug;         // measurement aid for the stream kernel (0 in normal use)
@@ -132,7 +134,7 @@ __device__ __forceinline__ int slot_token(int g, int e) { return (e < 4) ? (4 * 
 
 template <bool SCALED, bool PAGE_ALIGNED>
 __device__ __forceinline__ void load_tile(const DecodeArgs& a, int b, int h, int g, int c, int t0, int t_end,
-                                          TileRegs& r) {
+                                          TileRegs& r, int32_t blk_pre = -1, bool use_pre = false) {
   const int32_t* bt_row = a.bt + static_cast<int64_t>(b) * a.bt_sb;
   r.kvalid = 0;
   if constexpr (PAGE_ALIGNED) {
@@ -141,7 +143,7 @@ __device__ __forceinline__ void load_tile(const DecodeArgs& a, int b, int h, int
     // compiler can keep this prefetch asynchronous.
     const int page = t0 / a.page_size;
     const int off0 = t0 - page * a.page_size;
-    const int32_t blk_raw = bt_row[page * a.bt_sn];
+    const int32_t blk_raw = use_pre ? blk_pre : bt_row[page * a.bt_sn];
     const bool blk_ok = blk_raw >= 0 && blk_raw < a.num_blocks;
     const int64_t blk = blk_ok ? blk_raw : 0;
     const uint8_t* kbase = a.k + blk * a.k_sblk + static_cast<int64_t>(off0) * a.k_stok + h * a.k_sh;
@@ -221,23 +223,108 @@ struct QOperand<PRISM_DTYPE_F16> {
   f16x8 hi[4];
 };
 
+// Partials cross workgroups (and XCDs, whose L2 caches are not coherent with
+// each other) inside one launch.  They are written with device-scope stores
+// (sc1: written through to the device-coherent level) and read back with
+// device-scope loads (sc1 buffer loads), so neither side needs a cache-wide
+// writeback or invalidate.  A partial is counted only after its writer's
+// stores have completed (s_waitcnt vmcnt(0)), and the merging workgroup
+// loads the partials only after the counter told it every one is in.
+__device__ __forceinline__ void store_coherent(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+constexpr int kCoherentLoad = 16;  // buffer-load cache policy: sc1 (device scope)
+
+__device__ __forceinline__ floatx4 load_coherent4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(byte_off), 0, kCoherentLoad);
+  return floatx4{__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3])};
+}
+
+__device__ __forceinline__ float2 load_coherent2(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+  const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(byte_off), 0, kCoherentLoad);
+  return float2{__uint_as_float(v[0]), __uint_as_float(v[1])};
+}
+
+constexpr int kSplitWaves = 8;       // waves per split-K workgroup (tile lanes of one kv head)
+constexpr int kSplitMaxChunks = 64;  // chunks per (sequence, kv head) at most
+
+// Chunk counters of the split-K path, one 64-bit word per (sequence, kv
+// head): (epoch << 32) | arrivals.  Every call carries its own nonzero epoch,
+// so a word holding anything of another call (or bytes of another use of the
+// workspace) counts as zero arrivals and the workspace needs no clearing.
+// Every chunk of the launch claims the word for its call: an exchange
+// 0 -> (epoch, 0) issued first thing, whose answer only a live chunk reads,
+// when it arrives (the round trip hides behind the chunk's tiles); if the
+// word held neither 0 nor this call's tag, the arriving chunk repeats the
+// exchange with the value seen until the word carries the tag.  The arrival
+// is then a single add.  An exchange succeeds only on 0 or a foreign value,
+// so no claim disturbs a word this call has tagged; every live chunk has
+// claimed the word before its own add, so the count starts from this call's
+// zero.  The completing chunk resets the word to 0 (a chunk without tokens
+// that claims after that leaves (epoch, 0): a replay of the same launch
+// counts from it, any other call sees a foreign tag).
+__device__ __forceinline__ unsigned long long split_claim_issue(unsigned long long* cnt, unsigned int epoch) {
+  unsigned long long seen = 0;
+  __hip_atomic_compare_exchange_strong(cnt, &seen, static_cast<unsigned long long>(epoch) << 32, __ATOMIC_RELAXED,
+                                       __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return seen;  // 0 when the exchange succeeded, else the word's value
+}
+
+// Completes the claim (from the first exchange's answer) and arrives; true
+// for the chunk that completes the word.
+__device__ __forceinline__ bool split_arrive(unsigned long long* cnt, unsigned int epoch, unsigned long long seen,
+                                             int n_live) {
+  const unsigned long long tag = static_cast<unsigned long long>(epoch) << 32;
+  // a failed exchange leaves the word's current value in `seen`
+  while (seen != 0 && (seen >> 32) != epoch) {
+    if (__hip_atomic_compare_exchange_strong(cnt, &seen, tag, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                             __HIP_MEMORY_SCOPE_AGENT))
+      break;
+  }
+  const unsigned long long now = __hip_atomic_fetch_add(cnt, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) + 1;
+  const bool last = static_cast<int>(now & 0xFFFFFFFFull) == n_live;
+  if (last) __hip_atomic_store(cnt, 0ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  return last;
+}
+
+// Split-K kernel: grid (batch, num_kv_heads, chunks), eight waves per
+// workgroup, all on kv head h = blockIdx.y.  Chunk z covers tokens
+// [z * split, (z + 1) * split) of its sequence; wave w takes the chunk's
+// tiles w, w + 8, w + 16, ... (the eight waves read eight neighbouring
+// 32-token tiles of the same head together).  The waves' (m, l, acc) are
+// merged through LDS; a sequence with one live chunk writes its output there
+// and then, otherwise the chunk writes a partial and the last chunk of
+// (sequence, kv head) to arrive merges all of them: no second launch.
 template <int QDT, bool SCALED, bool PAGE_ALIGNED, bool QVEC>
 __global__ void __launch_bounds__(512)
 paged_decode_split_kernel(const DecodeArgs a) {
   const int lane = threadIdx.x & 63;
-  const int h = threadIdx.x >> 6;  // kv head of this wave
+  const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // tile lane of this wave (uniform)
   const int g = lane >> 4;
   const int c = lane & 15;
   const int b = blockIdx.x;
-  const int s = blockIdx.y;
+  const int h = blockIdx.y;
+  const int z = blockIdx.z;
   const int G = a.groups;
+  const int nkv = a.num_kv_heads;
 
+  unsigned long long* const cnt = a.split_cnt + static_cast<int64_t>(b) * nkv + h;
+  unsigned long long claim_seen = 0;  // thread 0: the claim exchange's answer
+  const int c_begin = z * a.split;
+  int t0 = c_begin + wv * kTile;
+  // The block id of this wave's first tile is requested together with the
+  // context length (both scalar loads, one round trip), so the first K/V
+  // loads do not wait for two dependent trips.
+  int32_t blk0 = 0;
+  if constexpr (PAGE_ALIGNED) {
+    if (t0 < a.width * a.page_size) blk0 = ld_meta(a.bt + static_cast<int64_t>(b) * a.bt_sb + (t0 / a.page_size) * a.bt_sn);
+  }
   const int n_eff = effective_len(a, b);
-  const int t_begin = s * a.split;
-  if (t_begin >= n_eff) {
-    if (s == 0) {
+  if (c_begin >= n_eff) {
+    if (z == 0) {
       // No attended token: zeros (the reference kernel's l == 0 branch).
-      for (int idx = lane; idx < G * kHeadDim; idx += 64) {
+      for (int idx = threadIdx.x; idx < G * kHeadDim; idx += blockDim.x) {
         const int qh = h * G + idx / kHeadDim;
         const int d = idx % kHeadDim;
         store_out<QDT>(a.out, b * a.o_sb + qh * a.o_sh + d * a.o_sd, 0.f);
@@ -245,60 +332,8 @@ paged_decode_split_kernel(const DecodeArgs a) {
     }
     return;
   }
-  const int t_end = min(t_begin + a.split, n_eff);
-
-  // ---- query operand (B of QK): column c = q head h*G + c, k slot 8g+e of
-  // chunk cc <-> dim 32g + 8cc + e.
-  // First tile's loads go out before the query is read and converted.
-  TileRegs ta, tb;
-  load_tile<SCALED, PAGE_ALIGNED>(a, b, h, g, c, t_begin, t_end, ta);
-
-  QOperand<QDT> qop;
-  {
-    // Lanes c >= G read q head h*G (a valid row) and zero their copy, so the
-    // loads carry no branch.
-    const bool qvalid = c < G;
-    const int64_t qbase = static_cast<int64_t>(b) * a.q_sb + static_cast<int64_t>(h * G + (qvalid ? c : 0)) * a.q_sh;
-#pragma unroll
-    for (int cc = 0; cc < 4; ++cc) {
-      float x[8];
-      const int64_t d0 = 32 * g + 8 * cc;
-      if constexpr (QVEC) {
-        if constexpr (QDT == PRISM_DTYPE_F32) {
-          const floatx4* p = reinterpret_cast<const floatx4*>(static_cast<const float*>(a.q) + qbase + d0);
-          const floatx4 lo = p[0], hi = p[1];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) x[e] = lo[e], x[4 + e] = hi[e];
-        } else {
-          const u32x4 w = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.q) + qbase + d0);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            if constexpr (QDT == PRISM_DTYPE_BF16) {
-              x[2 * e] = bf16_bits_to_f32(w[e] & 0xFFFFu);
-              x[2 * e + 1] = bf16_bits_to_f32(w[e] >> 16);
-            } else {
-              x[2 * e] = f16_bits_to_f32(w[e] & 0xFFFFu);
-              x[2 * e + 1] = f16_bits_to_f32(w[e] >> 16);
-            }
-          }
-        }
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) x[e] = load_q<QDT>(a.q, qbase + (d0 + e) * a.q_sd);
-      }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float xv = qvalid ? x[e] : 0.f;
-        if constexpr (QDT == PRISM_DTYPE_F16) {
-          qop.hi[cc][e] = static_cast<_Float16>(xv);
-        } else {
-          const __bf16 hi = static_cast<__bf16>(xv);
-          qop.hi[cc][e] = hi;
-          if constexpr (QDT == PRISM_DTYPE_F32) qop.lo[cc][e] = static_cast<__bf16>(xv - static_cast<float>(hi));
-        }
-      }
-    }
-  }
+  const int c_end = min(c_begin + a.split, n_eff);
+  const int n_live = (n_eff + a.split - 1) / a.split;  // chunks with attended tokens (>= 1)
 
   floatx4 acc[8];
 #pragma unroll
@@ -306,252 +341,315 @@ paged_decode_split_kernel(const DecodeArgs a) {
   float m_run = -INFINITY;  // running max (log2 domain) of q head c
   float l_run = 0.f;        // this lane's share of the running sum
 
-  // One 32-token tile of this wave's kv head: QK, online softmax, PV.
-  auto compute = [&](TileRegs& cur) {
-    // ---- QK
-    floatx4 sc[2];
-#pragma unroll
-    for (int hh = 0; hh < 2; ++hh) {
-      floatx4 accs = {0.f, 0.f, 0.f, 0.f};
+  if (t0 < c_end) {  // wave-uniform; a wave past the chunk's end keeps empty state
+    // First tile's loads go out before the query is read and converted.
+    TileRegs ta, tb;
+    load_tile<SCALED, PAGE_ALIGNED>(a, b, h, g, c, t0, c_end, ta, blk0, true);
+    // The claim goes out behind the first tile's loads (the load counter is
+    // in order: ahead of them it would delay the first tile by its own
+    // round trip) and is not waited for before the arrival.
+    if (n_live > 1 && threadIdx.x == 0) claim_seen = split_claim_issue(cnt, a.epoch);
+
+    // ---- query operand (B of QK): column c = q head h*G + c, k slot 8g+e of
+    // chunk cc <-> dim 32g + 8cc + e.
+    QOperand<QDT> qop;
+    {
+      // Lanes c >= G read q head h*G (a valid row) and zero their copy, so the
+      // loads carry no branch.
+      const bool qvalid = c < G;
+      const int64_t qbase =
+          static_cast<int64_t>(b) * a.q_sb + static_cast<int64_t>(h * G + (qvalid ? c : 0)) * a.q_sh;
 #pragma unroll
       for (int cc = 0; cc < 4; ++cc) {
-        const uint32_t w0 = cur.k[hh][cc >> 1][(cc & 1) * 2];
-        const uint32_t w1 = cur.k[hh][cc >> 1][(cc & 1) * 2 + 1];
-        if constexpr (QDT == PRISM_DTYPE_F16) {
-          accs = __builtin_amdgcn_mfma_f32_16x16x32_f16(fp8x8_to_f16x8(w0, w1), qop.hi[cc], accs, 0, 0, 0);
+        float x[8];
+        const int64_t d0 = 32 * g + 8 * cc;
+        if constexpr (QVEC) {
+          if constexpr (QDT == PRISM_DTYPE_F32) {
+            const floatx4* p = reinterpret_cast<const floatx4*>(static_cast<const float*>(a.q) + qbase + d0);
+            const floatx4 lo = p[0], hi = p[1];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) x[e] = lo[e], x[4 + e] = hi[e];
+          } else {
+            const u32x4 w = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(a.q) + qbase + d0);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              if constexpr (QDT == PRISM_DTYPE_BF16) {
+                x[2 * e] = bf16_bits_to_f32(w[e] & 0xFFFFu);
+                x[2 * e + 1] = bf16_bits_to_f32(w[e] >> 16);
+              } else {
+                x[2 * e] = f16_bits_to_f32(w[e] & 0xFFFFu);
+                x[2 * e + 1] = f16_bits_to_f32(w[e] >> 16);
+              }
+            }
+          }
         } else {
-          const bf16x8 kb = fp8x8_to_bf16x8(w0, w1);
-          accs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qop.hi[cc], accs, 0, 0, 0);
-          if constexpr (QDT == PRISM_DTYPE_F32)
-            accs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qop.lo[cc], accs, 0, 0, 0);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[e] = load_q<QDT>(a.q, qbase + (d0 + e) * a.q_sd);
         }
-      }
-      sc[hh] = accs;
-    }
-
-    // ---- online softmax (log2 domain).  Value e of this lane: half e/4, row e%4.
-    float x[8];
-    float tmax = -INFINITY;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const bool ok = ((cur.kvalid >> e) & 1u) && c < G;
-      const float v = sc[e >> 2][e & 3] * (cur.ksc[e] * a.scale_log2);
-      x[e] = ok ? v : -INFINITY;
-      tmax = fmaxf(tmax, x[e]);
-    }
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
-    tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-    const float m_new = fmaxf(m_run, tmax);
-    const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
-    const float alpha = exp2f(m_run - m_use);
-    m_run = m_new;
-    // P * v_scale as a bf16 hi/lo pair (about 16 significant bits): the PV
-    // product then matches fp32 accumulation closely (V itself is exact).
-    float psum = 0.f;
-    bf16x8 pa, pa_lo;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const float p = exp2f(x[e] - m_use);  // 0 for masked slots
-      psum += p;
-      const float pv = ((cur.kvalid >> e) & 1u) ? p * cur.vsc[e] : 0.f;
-      const __bf16 hi = static_cast<__bf16>(pv);
-      pa[e] = hi;
-      pa_lo[e] = static_cast<__bf16>(pv - static_cast<float>(hi));
-    }
-    l_run = l_run * alpha + psum;
-
-    // Rescale accumulator rows (q heads 4g+i) by their alpha.
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const float ai = __shfl(alpha, 4 * g + i);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) acc[j][i] *= ai;
-    }
-
-    // Rows past the end of the split may hold anything (NaN codes included);
-    // their V bytes are zeroed because the PV MFMA would turn 0 * NaN into NaN.
-    // (Done here, at use, so the prefetch of this tile stays asynchronous.)
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      if (!((cur.kvalid >> e) & 1u)) cur.v[e] = u32x2{0, 0};
-
-    // ---- PV: B operand of N-tile j = byte j of the lane's 8 V rows.
-#pragma unroll
-    for (int jp = 0; jp < 4; ++jp) {  // column pairs (2jp, 2jp+1)
-      const int j = 2 * jp;
-      const int dw = j >> 2;
-      const int jj = j & 3;
-      const uint32_t sel = (jj) | ((4 + jj) << 8) | ((jj + 1) << 16) | ((5 + jj) << 24);
-      bf16x8 b0, b1;
-#pragma unroll
-      for (int ep = 0; ep < 4; ++ep) {  // slot pairs (2ep, 2ep+1)
-        const uint32_t lo = cur.v[2 * ep][dw];
-        const uint32_t hi = cur.v[2 * ep + 1][dw];
-        const uint32_t pr = __builtin_amdgcn_perm(hi, lo, sel);
-        const bf16x2 cj = fp8x2_to_bf16x2<false>(pr);
-        const bf16x2 cj1 = fp8x2_to_bf16x2<true>(pr);
-        b0[2 * ep] = cj[0];
-        b0[2 * ep + 1] = cj[1];
-        b1[2 * ep] = cj1[0];
-        b1[2 * ep + 1] = cj1[1];
-      }
-      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, b0, acc[j], 0, 0, 0);
-      acc[j + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, b1, acc[j + 1], 0, 0, 0);
-      acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa_lo, b0, acc[j], 0, 0, 0);
-      acc[j + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa_lo, b1, acc[j + 1], 0, 0, 0);
-    }
-
-  };
-
-  // Ping-pong prefetch: the next tile's loads are in flight while the current
-  // one is computed.  The loads are unconditional (past the end they re-read
-  // the current tile, a cache hit) so the waitcnt pass can count them exactly.
-  int t0 = t_begin;
-  while (true) {
-    int tn = (t0 + kTile < t_end) ? t0 + kTile : t0;
-    load_tile<SCALED, PAGE_ALIGNED>(a, b, h, g, c, tn, t_end, tb);
-    compute(ta);
-    t0 += kTile;
-    if (t0 >= t_end) break;
-    tn = (t0 + kTile < t_end) ? t0 + kTile : t0;
-    load_tile<SCALED, PAGE_ALIGNED>(a, b, h, g, c, tn, t_end, ta);
-    compute(tb);
-    t0 += kTile;
-    if (t0 >= t_end) break;
-  }
-
-  // ---- finish: total l per q head c, then per accumulator row 4g+i.
-  float l_tot = l_run + __shfl_xor(l_run, 16);
-  l_tot += __shfl_xor(l_tot, 32);
-  if (a.max_splits == 1) {  // no combine launch: write the output
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int qr = 4 * g + i;
-      const float li = __shfl(l_tot, qr);
-      if (qr < G) {
-        const float inv = li > 0.f ? 1.f / li : 0.f;
-        const int64_t base = static_cast<int64_t>(b) * a.o_sb + static_cast<int64_t>(h * G + qr) * a.o_sh;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) store_out<QDT>(a.out, base + (8 * c + j) * a.o_sd, acc[j][i] * inv);
-      }
-    }
-  } else {
-    const int64_t row0 = (static_cast<int64_t>(b) * a.max_splits + s) * a.num_heads;
-    for (int i = 0; i < 4; ++i) {
-      const int qr = 4 * g + i;
-      const float li = __shfl(l_tot, qr);
-      const float mi = __shfl(m_run, qr);
-      if (qr < G) {
-        const int64_t hq = h * G + qr;
-        floatx4* dstp = reinterpret_cast<floatx4*>(a.part_acc + (row0 + hq) * kHeadDim + 8 * c);
-        dstp[0] = floatx4{acc[0][i], acc[1][i], acc[2][i], acc[3][i]};
-        dstp[1] = floatx4{acc[4][i], acc[5][i], acc[6][i], acc[7][i]};
-        if (c == 0) {
-          a.part_ml[(row0 + hq) * 2 + 0] = mi;
-          a.part_ml[(row0 + hq) * 2 + 1] = li;
+        for (int e = 0; e < 8; ++e) {
+          const float xv = qvalid ? x[e] : 0.f;
+          if constexpr (QDT == PRISM_DTYPE_F16) {
+            qop.hi[cc][e] = static_cast<_Float16>(xv);
+          } else {
+            const __bf16 hi = static_cast<__bf16>(xv);
+            qop.hi[cc][e] = hi;
+            if constexpr (QDT == PRISM_DTYPE_F32) qop.lo[cc][e] = static_cast<__bf16>(xv - static_cast<float>(hi));
+          }
         }
       }
     }
-  }
-}
 
-constexpr int kCombineSmallMax = 64;  // split slots the one-round combine takes
 
-// Merge split-K partials when there are at most MS split slots: one round of
-// loads.  Lane s reads split s's (m, l); every lane reads its two output dims
-// of every split; all of it goes out together with the context length.  Rows
-// of splits past the context's last one may hold anything and are never read
-// into the sums.  With more than one split slot the split kernel always
-// writes partials, so this kernel writes every output row (zeros for an
-// empty context).
-template <int QDT, int MS>
-__global__ void __launch_bounds__(64) paged_decode_combine_small_kernel(const DecodeArgs a) {
-  const int b = blockIdx.x;
-  const int hq = blockIdx.y;
-  const int lane = threadIdx.x;
-  const int64_t row0 = static_cast<int64_t>(b) * a.max_splits * a.num_heads + hq;
-  const int ms = a.max_splits;  // <= MS
-  float2 ml = {-INFINITY, 0.f};
-  if (lane < ms) ml = *reinterpret_cast<const float2*>(a.part_ml + (row0 + static_cast<int64_t>(lane) * a.num_heads) * 2);
-  float v0[MS], v1[MS];
+    // One 32-token tile of kv head h: QK, online softmax, PV.
+    auto compute = [&](TileRegs& cur) {
+      // ---- QK
+      floatx4 sc[2];
 #pragma unroll
-  for (int s = 0; s < MS; ++s) {
-    const int64_t r = row0 + static_cast<int64_t>(s < ms ? s : 0) * a.num_heads;
-    v0[s] = a.part_acc[r * kHeadDim + lane];
-    v1[s] = a.part_acc[r * kHeadDim + lane + 64];
-  }
-  const int n_eff = effective_len(a, b);
-  const int nsplit = (n_eff + a.split - 1) / a.split;  // 0 .. ms; no early exit, so the loads stay ahead
-  const float m = lane < nsplit ? ml.x : -INFINITY;
-  float m_max = m;
+      for (int hh = 0; hh < 2; ++hh) {
+        floatx4 accs = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) m_max = fmaxf(m_max, __shfl_xor(m_max, off));
-  const float m_use = (m_max == -INFINITY) ? 0.f : m_max;
-  const float w = lane < nsplit ? exp2f(m - m_use) : 0.f;  // 0 for m = -inf
-  float l_sum = w * (lane < nsplit ? ml.y : 0.f);
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) l_sum += __shfl_xor(l_sum, off);
-  float o0 = 0.f, o1 = 0.f;
-#pragma unroll
-  for (int s = 0; s < MS; ++s) {
-    // selects, not branches: rows past nsplit contribute exactly 0 (their
-    // contents, NaN included, are never multiplied)
-    const bool live = s < nsplit;
-    const float ws = __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, w), s));
-    o0 += live ? ws * v0[s] : 0.f;
-    o1 += live ? ws * v1[s] : 0.f;
-  }
-  const float inv = l_sum > 0.f ? 1.f / l_sum : 0.f;
-  const int64_t base = static_cast<int64_t>(b) * a.o_sb + static_cast<int64_t>(hq) * a.o_sh;
-  store_out<QDT>(a.out, base + lane * a.o_sd, o0 * inv);
-  store_out<QDT>(a.out, base + (lane + 64) * a.o_sd, o1 * inv);
-}
+        for (int cc = 0; cc < 4; ++cc) {
+          const uint32_t w0 = cur.k[hh][cc >> 1][(cc & 1) * 2];
+          const uint32_t w1 = cur.k[hh][cc >> 1][(cc & 1) * 2 + 1];
+          if constexpr (QDT == PRISM_DTYPE_F16) {
+            accs = __builtin_amdgcn_mfma_f32_16x16x32_f16(fp8x8_to_f16x8(w0, w1), qop.hi[cc], accs, 0, 0, 0);
+          } else {
+            const bf16x8 kb = fp8x8_to_bf16x8(w0, w1);
+            accs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qop.hi[cc], accs, 0, 0, 0);
+            if constexpr (QDT == PRISM_DTYPE_F32)
+              accs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qop.lo[cc], accs, 0, 0, 0);
+          }
+        }
+        sc[hh] = accs;
+      }
 
-// Merge split-K partials: grid (batch, num_heads), one wave each.
-template <int QDT>
-__global__ void __launch_bounds__(64) paged_decode_combine_kernel(const DecodeArgs a) {
-  const int b = blockIdx.x;
-  const int hq = blockIdx.y;
-  const int lane = threadIdx.x;
-  const int n_eff = effective_len(a, b);
-  const int nsplit = (n_eff + a.split - 1) / a.split;  // 0 for an empty context: zeros below
-  const int64_t row0 = static_cast<int64_t>(b) * a.max_splits * a.num_heads + hq;
-  float m_max = -INFINITY;
-  for (int s = lane; s < nsplit; s += 64) m_max = fmaxf(m_max, a.part_ml[(row0 + static_cast<int64_t>(s) * a.num_heads) * 2]);
+      // ---- online softmax (log2 domain).  Value e of this lane: half e/4, row e%4.
+      float x[8];
+      float tmax = -INFINITY;
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) m_max = fmaxf(m_max, __shfl_xor(m_max, off));
-  const float m_use = (m_max == -INFINITY) ? 0.f : m_max;
-  float l_sum = 0.f;
-  for (int s = lane; s < nsplit; s += 64) {
-    const int64_t r = (row0 + static_cast<int64_t>(s) * a.num_heads) * 2;
-    l_sum += a.part_ml[r + 1] * exp2f(a.part_ml[r] - m_use);
-  }
+      for (int e = 0; e < 8; ++e) {
+        const bool ok = ((cur.kvalid >> e) & 1u) && c < G;
+        const float v = sc[e >> 2][e & 3] * (cur.ksc[e] * a.scale_log2);
+        x[e] = ok ? v : -INFINITY;
+        tmax = fmaxf(tmax, x[e]);
+      }
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 16));
+      tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
+      const float m_new = fmaxf(m_run, tmax);
+      const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
+      const float alpha = exp2f(m_run - m_use);
+      m_run = m_new;
+      // P * v_scale as a bf16 hi/lo pair (about 16 significant bits): the PV
+      // product then matches fp32 accumulation closely (V itself is exact).
+      float psum = 0.f;
+      bf16x8 pa, pa_lo;
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) l_sum += __shfl_xor(l_sum, off);
-  // eight partials per trip, all their loads issued before the first use
-  float o0 = 0.f, o1 = 0.f;
-  constexpr int kU = 8;
-  for (int s0 = 0; s0 < nsplit; s0 += kU) {
-    float mv[kU], v0[kU], v1[kU];
+      for (int e = 0; e < 8; ++e) {
+        const float p = exp2f(x[e] - m_use);  // 0 for masked slots
+        psum += p;
+        const float pv = ((cur.kvalid >> e) & 1u) ? p * cur.vsc[e] : 0.f;
+        const __bf16 hi = static_cast<__bf16>(pv);
+        pa[e] = hi;
+        pa_lo[e] = static_cast<__bf16>(pv - static_cast<float>(hi));
+      }
+      l_run = l_run * alpha + psum;
+
+      // Rescale accumulator rows (q heads 4g+i) by their alpha.
 #pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      const int s = min(s0 + u, nsplit - 1);
-      const int64_t r = row0 + static_cast<int64_t>(s) * a.num_heads;
-      mv[u] = s0 + u < nsplit ? a.part_ml[r * 2] : -INFINITY;
-      v0[u] = a.part_acc[r * kHeadDim + lane];
-      v1[u] = a.part_acc[r * kHeadDim + lane + 64];
+      for (int i = 0; i < 4; ++i) {
+        const float ai = __shfl(alpha, 4 * g + i);
+#pragma unroll
+        for (int j = 0; j < 8; ++j) acc[j][i] *= ai;
+      }
+
+      // Rows past the end of the chunk may hold anything (NaN codes included);
+      // their V bytes are zeroed because the PV MFMA would turn 0 * NaN into
+      // NaN.  (Done here, at use, so the prefetch of this tile stays
+      // asynchronous.)
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (!((cur.kvalid >> e) & 1u)) cur.v[e] = u32x2{0, 0};
+
+      // ---- PV: B operand of N-tile j = byte j of the lane's 8 V rows.
+#pragma unroll
+      for (int jp = 0; jp < 4; ++jp) {  // column pairs (2jp, 2jp+1)
+        const int j = 2 * jp;
+        const int dw = j >> 2;
+        const int jj = j & 3;
+        const uint32_t sel = (jj) | ((4 + jj) << 8) | ((jj + 1) << 16) | ((5 + jj) << 24);
+        bf16x8 b0, b1;
+#pragma unroll
+        for (int ep = 0; ep < 4; ++ep) {  // slot pairs (2ep, 2ep+1)
+          const uint32_t lo = cur.v[2 * ep][dw];
+          const uint32_t hi = cur.v[2 * ep + 1][dw];
+          const uint32_t pr = __builtin_amdgcn_perm(hi, lo, sel);
+          const bf16x2 cj = fp8x2_to_bf16x2<false>(pr);
+          const bf16x2 cj1 = fp8x2_to_bf16x2<true>(pr);
+          b0[2 * ep] = cj[0];
+          b0[2 * ep + 1] = cj[1];
+          b1[2 * ep] = cj1[0];
+          b1[2 * ep + 1] = cj1[1];
+        }
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, b0, acc[j], 0, 0, 0);
+        acc[j + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, b1, acc[j + 1], 0, 0, 0);
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa_lo, b0, acc[j], 0, 0, 0);
+        acc[j + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa_lo, b1, acc[j + 1], 0, 0, 0);
+      }
+    };
+
+    // Ping-pong prefetch over this wave's tiles (stride 8 tiles): the next
+    // tile's loads are in flight while the current one is computed.  The
+    // loads are unconditional (past the end they re-read the current tile, a
+    // cache hit) so the waitcnt pass can count them exactly.
+    constexpr int kStep = kSplitWaves * kTile;
+    while (true) {
+      int tn = (t0 + kStep < c_end) ? t0 + kStep : t0;
+      load_tile<SCALED, PAGE_ALIGNED>(a, b, h, g, c, tn, c_end, tb);
+      compute(ta);
+      t0 += kStep;
+      if (t0 >= c_end) break;
+      tn = (t0 + kStep < c_end) ? t0 + kStep : t0;
+      load_tile<SCALED, PAGE_ALIGNED>(a, b, h, g, c, tn, c_end, ta);
+      compute(tb);
+      t0 += kStep;
+      if (t0 >= c_end) break;
     }
+  }
+
+  // ---- merge the eight waves through LDS.  Wave w's row r (q head h*G + r)
+  // goes to s_acc[(w * G + r) * 128 + d]; its (m, l) to s_ml[w][r].
+  __shared__ float s_acc[kSplitWaves * 16 * kHeadDim];
+  __shared__ float2 s_ml[kSplitWaves * 16];
+  __shared__ int s_last;
+  {
+    float l_tot = l_run + __shfl_xor(l_run, 16);
+    l_tot += __shfl_xor(l_tot, 32);
+    if (g == 0) s_ml[wv * 16 + c] = float2{m_run, l_tot};
 #pragma unroll
-    for (int u = 0; u < kU; ++u) {
-      const float w = exp2f(mv[u] - m_use);  // 0 past the last split
-      o0 += w * v0[u];
-      o1 += w * v1[u];
+    for (int i = 0; i < 4; ++i) {
+      const int r = 4 * g + i;
+      if (r < G) {
+        floatx4* dst = reinterpret_cast<floatx4*>(s_acc + (wv * G + r) * kHeadDim + 8 * c);
+        dst[0] = floatx4{acc[0][i], acc[1][i], acc[2][i], acc[3][i]};
+        dst[1] = floatx4{acc[4][i], acc[5][i], acc[6][i], acc[7][i]};
+      }
     }
   }
-  const float inv = l_sum > 0.f ? 1.f / l_sum : 0.f;
-  const int64_t base = static_cast<int64_t>(b) * a.o_sb + static_cast<int64_t>(hq) * a.o_sh;
-  store_out<QDT>(a.out, base + lane * a.o_sd, o0 * inv);
-  store_out<QDT>(a.out, base + (lane + 64) * a.o_sd, o1 * inv);
+  // LDS-only barrier: outstanding global operations (the claim) need not
+  // complete here.
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+  const int64_t prow0 = ((static_cast<int64_t>(b) * nkv + h) * a.max_splits + z) * G;  // first partial row
+  for (int e = threadIdx.x; e < G * kHeadDim; e += blockDim.x) {
+    const int r = e / kHeadDim;
+    const int d = e - r * kHeadDim;
+    float mx = -INFINITY;
+#pragma unroll
+    for (int w = 0; w < kSplitWaves; ++w) mx = fmaxf(mx, s_ml[w * 16 + r].x);
+    const float m_use = mx == -INFINITY ? 0.f : mx;
+    float l_sum = 0.f, o = 0.f;
+#pragma unroll
+    for (int w = 0; w < kSplitWaves; ++w) {
+      const float2 ml = s_ml[w * 16 + r];
+      const float wgt = exp2f(ml.x - m_use);  // 0 for a wave without attended tokens
+      l_sum += wgt * ml.y;
+      o += wgt * s_acc[(w * G + r) * kHeadDim + d];
+    }
+    if (n_live == 1) {
+      const float inv = l_sum > 0.f ? 1.f / l_sum : 0.f;
+      store_out<QDT>(a.out, b * a.o_sb + (h * G + r) * a.o_sh + d * a.o_sd, o * inv);
+    } else {
+      store_coherent(a.part_acc + (prow0 + r) * kHeadDim + d, o);
+      if (d == 0) {
+        store_coherent(a.part_ml + (prow0 + r) * 2, mx);
+        store_coherent(a.part_ml + (prow0 + r) * 2 + 1, l_sum);
+      }
+    }
+  }
+  if (n_live == 1) return;
+
+  // ---- arrival; the last chunk of (b, h) merges the n_live partials.
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // this thread's partial stores have completed
+  __syncthreads();
+  if (threadIdx.x == 0) s_last = split_arrive(cnt, a.epoch, claim_seen, n_live);
+  __syncthreads();
+  if (!s_last) return;
+
+  // Thread (cg, u): unit u = float4 u of the G x 128 outputs, chunk group cg
+  // takes chunks cg, cg + NG, ...; the NG groups then meet in LDS.
+  const int units = G * (kHeadDim / 4);
+  const int NG = blockDim.x / units;  // 1 (G = 16) .. 16 (G = 1)
+  const int cg = threadIdx.x / units;
+  const int u = threadIdx.x - cg * units;
+  const int r = u / (kHeadDim / 4);
+  const int d0 = 4 * (u - r * (kHeadDim / 4));
+  const int64_t hrow0 = (static_cast<int64_t>(b) * nkv + h) * a.max_splits * G;  // chunk 0's first row
+  const __amdgpu_buffer_rsrc_t acc_r = __builtin_amdgcn_make_buffer_rsrc(a.part_acc, 0, 0x7FFFFFFF, 0x00020000);
+  const __amdgpu_buffer_rsrc_t ml_r = __builtin_amdgcn_make_buffer_rsrc(a.part_ml, 0, 0x7FFFFFFF, 0x00020000);
+  float m_acc = -INFINITY, l_acc = 0.f;
+  floatx4 o = {0.f, 0.f, 0.f, 0.f};
+  if (cg < NG) {
+    constexpr int kU = 8;
+    for (int k0 = cg; k0 < n_live; k0 += kU * NG) {
+      float mv[kU], lv[kU];
+      floatx4 xv[kU];
+#pragma unroll
+      for (int q = 0; q < kU; ++q) {
+        const int k = k0 + q * NG;
+        const int kk = k < n_live ? k : cg;  // past the end: re-read a live row, weighed 0
+        const int64_t row = hrow0 + static_cast<int64_t>(kk) * G + r;
+        const float2 ml = load_coherent2(ml_r, static_cast<uint32_t>(row * 8));
+        xv[q] = load_coherent4(acc_r, static_cast<uint32_t>((row * kHeadDim + d0) * 4));
+        mv[q] = k < n_live ? ml.x : -INFINITY;
+        lv[q] = k < n_live ? ml.y : 0.f;
+      }
+      float mx = m_acc;
+#pragma unroll
+      for (int q = 0; q < kU; ++q) mx = fmaxf(mx, mv[q]);
+      if (mx == -INFINITY) continue;  // nothing attended so far
+      const float alpha = exp2f(m_acc - mx);  // 0 while m_acc = -inf
+      l_acc *= alpha;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) o[j] *= alpha;
+#pragma unroll
+      for (int q = 0; q < kU; ++q) {
+        const float wgt = mv[q] == -INFINITY ? 0.f : exp2f(mv[q] - mx);  // rows with m = -inf weigh 0
+        l_acc += wgt * lv[q];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) o[j] += wgt * (wgt != 0.f ? xv[q][j] : 0.f);
+      }
+      m_acc = mx;
+    }
+  }
+  // meet in LDS (s_acc is free again: every thread passed the barriers above)
+  floatx4* red = reinterpret_cast<floatx4*>(s_acc);
+  float2* red_ml = reinterpret_cast<float2*>(s_acc + 512 * 4);  // after up to 512 floatx4
+  if (cg < NG) {
+    red[cg * units + u] = o;
+    red_ml[cg * units + u] = float2{m_acc, l_acc};
+  }
+  __syncthreads();
+  if (cg == 0) {
+    float mx = -INFINITY;
+    for (int k = 0; k < NG; ++k) mx = fmaxf(mx, red_ml[k * units + u].x);
+    const float m_use = mx == -INFINITY ? 0.f : mx;
+    float l_sum = 0.f;
+    floatx4 s = {0.f, 0.f, 0.f, 0.f};
+    for (int k = 0; k < NG; ++k) {
+      const float2 ml = red_ml[k * units + u];
+      const float wgt = exp2f(ml.x - m_use);
+      l_sum += wgt * ml.y;
+      const floatx4 x = red[k * units + u];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) s[j] += wgt * x[j];
+    }
+    const float inv = l_sum > 0.f ? 1.f / l_sum : 0.f;
+    const int64_t obase = static_cast<int64_t>(b) * a.o_sb + static_cast<int64_t>(h * G + r) * a.o_sh;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) store_out<QDT>(a.out, obase + (d0 + j) * a.o_sd, s[j] * inv);
+  }
 }
 
 // ---------------------------------------------------------------- streaming path
@@ -1391,29 +1489,6 @@ __device__ __forceinline__ void stream_column(const DecodeArgs& a, int V, int i,
   qhead = h * G + (valid ? qh : 0);
 }
 
-// Partials cross workgroups (and XCDs, whose L2 caches are not coherent with
-// each other) inside one launch.  They are written with device-scope stores
-// (sc1: written through to the device-coherent level) and read back with
-// device-scope loads (sc1 buffer loads), so neither side needs a cache-wide
-// writeback or invalidate.  A flush is counted only after the writer's
-// stores have completed (s_waitcnt vmcnt(0)), and the merging workgroup
-// loads the partials only after the counter told it every flush is in.
-__device__ __forceinline__ void store_coherent(float* p, float v) {
-  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-constexpr int kCoherentLoad = 16;  // buffer-load cache policy: sc1 (device scope)
-
-__device__ __forceinline__ floatx4 load_coherent4(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
-  const u32x4 v = __builtin_amdgcn_raw_buffer_load_b128(r, static_cast<int>(byte_off), 0, kCoherentLoad);
-  return floatx4{__uint_as_float(v[0]), __uint_as_float(v[1]), __uint_as_float(v[2]), __uint_as_float(v[3])};
-}
-
-__device__ __forceinline__ float2 load_coherent2(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
-  const u32x2 v = __builtin_amdgcn_raw_buffer_load_b64(r, static_cast<int>(byte_off), 0, kCoherentLoad);
-  return float2{__uint_as_float(v[0]), __uint_as_float(v[1])};
-}
-
 // Output of real sequence b from the streaming partials, by the whole
 // workgroup: thread t owns q head t / 16 and dims 8 (t % 16) .. + 7 (the
 // partial layout is covered for up to 32 q heads per pass).  The candidates
@@ -2002,7 +2077,7 @@ struct Geometry {
   int split;
   int max_splits;
   int64_t ws_bytes;
-  int64_t acc_off, ml_off;
+  int64_t acc_off, ml_off, cnt_off;
   // streaming path (canonical layout only; chosen per call from the strides)
   bool stream_shape;
   int stream_nwg;
@@ -2040,6 +2115,15 @@ EnvOverrides& env_overrides() {
 
 int forced_path() { return env_overrides().path.load(); }
 
+// Tag of one split-K call's chunk counters: process-wide, nonzero, and
+// different from the previous 2^32 - 2 calls'.
+unsigned int next_split_epoch() {
+  static std::atomic<unsigned int> counter{0};
+  unsigned int e = counter.fetch_add(1, std::memory_order_relaxed) + 1;
+  if (e == 0) e = counter.fetch_add(1, std::memory_order_relaxed) + 1;
+  return e;
+}
+
 bool stream_disabled() { return forced_path() == 1; }
 
 bool fast_geometry(int num_heads, int num_kv_heads, int head_dim, int cache_dtype) {
@@ -2048,27 +2132,23 @@ bool fast_geometry(int num_heads, int num_kv_heads, int head_dim, int cache_dtyp
   return num_heads / num_kv_heads <= 16;
 }
 
+// Tokens per chunk of the split-K path (a multiple of 8 tiles, one per
+// wave): aim for about two workgroups per CU over batch x kv heads x chunks,
+// with at least one tile per wave and at most kSplitMaxChunks chunks.
 int choose_split(int batch, int num_kv_heads, int page_size, int width) {
+  constexpr int64_t kChunkTok = static_cast<int64_t>(kSplitWaves) * kTile;
   {
     const int v = env_overrides().split.load();
-    if (v >= kTile) return static_cast<int>(align_up(v, kTile));
+    if (v >= kTile) return static_cast<int>(align_up(v, kChunkTok));
   }
   const int64_t cap = static_cast<int64_t>(width) * page_size;
-  const int64_t tiles = static_cast<int64_t>(batch) * ceil_div(cap, kTile);
-  const int64_t target = static_cast<int64_t>(device_cu_count()) * 8;
-  int64_t per = tiles / (target > 0 ? target : 1);
-  // at least two tiles per split, or one when every split slot of the table
-  // fits the one-round combine (a short table: shorter splits, same merge cost)
-  const int64_t min_per = ceil_div(cap, kTile) <= kCombineSmallMax ? 1 : 2;
-  if (per < min_per) per = min_per;
-  // round down to a power of two number of tiles
-  int64_t p2 = 1;
-  while (p2 * 2 <= per) p2 *= 2;
-  int64_t split = p2 * kTile;
-  const int64_t cap_tiles = align_up(cap, kTile);
-  if (split > cap_tiles) split = cap_tiles > 0 ? cap_tiles : kTile;
-  (void)num_kv_heads;
-  return static_cast<int>(split);
+  const int64_t slots = std::max<int64_t>(1, static_cast<int64_t>(batch) * num_kv_heads);
+  const int64_t target = static_cast<int64_t>(device_cu_count()) * 2;
+  int64_t chunks = ceil_div(target, slots);
+  chunks = std::min<int64_t>(chunks, std::min<int64_t>(kSplitMaxChunks, std::max<int64_t>(1, ceil_div(cap, kChunkTok))));
+  if (chunks < 1) chunks = 1;
+  const int64_t per_wave = std::max<int64_t>(1, ceil_div(cap, chunks * kChunkTok));  // tiles per wave
+  return static_cast<int>(per_wave * kChunkTok);
 }
 
 Geometry geometry(int batch, int num_heads, int num_kv_heads, int head_dim, int page_size, int width,
@@ -2078,6 +2158,10 @@ Geometry geometry(int batch, int num_heads, int num_kv_heads, int head_dim, int 
   if (!geo.fast) return geo;
   geo.split = choose_split(batch, num_kv_heads, page_size, width);
   const int64_t cap = static_cast<int64_t>(width) * page_size;
+  // the in-kernel merge addresses the partials with 32-bit byte offsets
+  while (cap > geo.split &&
+         static_cast<int64_t>(batch) * ceil_div(cap, geo.split) * num_heads * head_dim * 4 >= (1LL << 31))
+    geo.split *= 2;
   geo.max_splits = static_cast<int>(cap > 0 ? ceil_div(cap, geo.split) : 1);
   // Every fast-path workspace starts with the streaming kernel's plan region,
   // which only the plan kernel writes (a workspace shared by calls of
@@ -2089,7 +2173,8 @@ Geometry geometry(int batch, int num_heads, int num_kv_heads, int head_dim, int 
     const int64_t rows = static_cast<int64_t>(batch) * geo.max_splits * num_heads;
     geo.acc_off = plan_bytes;
     geo.ml_off = geo.acc_off + align_up(rows * head_dim * 4, 256);
-    geo.ws_bytes = geo.ml_off + align_up(rows * 2 * 4, 256);
+    geo.cnt_off = geo.ml_off + align_up(rows * 2 * 4, 256);
+    geo.ws_bytes = geo.cnt_off + align_up(static_cast<int64_t>(batch) * num_kv_heads * 8, 256);
   }
   const int ttok = (num_kv_heads > 0 && num_kv_heads <= kSKv && (kSKv % num_kv_heads) == 0 &&
                     (num_kv_heads & (num_kv_heads - 1)) == 0)
@@ -2162,9 +2247,10 @@ int launch_all(int stage, const DecodeArgs& args, const Geometry& geo, bool page
                        args);
     return check_launch("paged_decode_generic_kernel launch");
   }
-  if (stage != 2) {
-    dim3 grid(args.batch, geo.max_splits);
-    dim3 block(64 * args.num_kv_heads);
+  if (stage == 2) return PRISM_OK;  // the split-K kernel merges its own chunks
+  {
+    const dim3 grid(args.batch, args.num_kv_heads, geo.max_splits);
+    const dim3 block(64 * kSplitWaves);
 #define PRISM_LAUNCH_SPLIT(S, A)                                                                   \
   do {                                                                                             \
     if (args.q_vec)                                                                                \
@@ -2177,22 +2263,8 @@ int launch_all(int stage, const DecodeArgs& args, const Geometry& geo, bool page
     else if (page_aligned) PRISM_LAUNCH_SPLIT(false, true);
     else PRISM_LAUNCH_SPLIT(false, false);
 #undef PRISM_LAUNCH_SPLIT
-    int rc = check_launch("paged_decode_split_kernel launch");
-    if (rc) return rc;
+    return check_launch("paged_decode_split_kernel launch");
   }
-  if (stage != 1 && geo.max_splits > 1) {
-    const dim3 grid(args.batch, args.num_heads);
-    if (geo.max_splits <= 16)
-      hipLaunchKernelGGL((paged_decode_combine_small_kernel<QDT, 16>), grid, dim3(64), 0, stream, args);
-    else if (geo.max_splits <= 32)
-      hipLaunchKernelGGL((paged_decode_combine_small_kernel<QDT, 32>), grid, dim3(64), 0, stream, args);
-    else if (geo.max_splits <= kCombineSmallMax)
-      hipLaunchKernelGGL((paged_decode_combine_small_kernel<QDT, kCombineSmallMax>), grid, dim3(64), 0, stream, args);
-    else
-      hipLaunchKernelGGL(paged_decode_combine_kernel<QDT>, grid, dim3(64), 0, stream, args);
-    return check_launch("paged_decode_combine_kernel launch");
-  }
-  return PRISM_OK;
 }
 
 }  // namespace
@@ -2356,6 +2428,8 @@ extern "C" int prism_paged_decode_stage(
   if (geo.fast && geo.ws_bytes > 0) {
     args.part_acc = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + geo.acc_off);
     args.part_ml = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + geo.ml_off);
+    args.split_cnt = reinterpret_cast<unsigned long long*>(static_cast<uint8_t*>(workspace) + geo.cnt_off);
+    args.epoch = next_split_epoch();
   }
   args.batch = batch;
   args.num_heads = num_heads;
@@ -2494,8 +2568,9 @@ extern "C" int prism_paged_decode_noalloc(const void* q, int q_dtype, const int6
   }
   // Nothing in the scratch needs clearing: the streaming plan carries the key
   // of the inputs it was computed from (a stale or zero plan is rebuilt, and
-  // its rebuild zeroes the merge counters), and split partials are written
-  // before they are read.
+  // its rebuild zeroes the merge counters), split-K chunk counters carry the
+  // epoch of their call (any other value counts as zero arrivals), and
+  // partials are written before they are read.
   return prism_paged_decode_stage(0, q, q_dtype, q_strides, k_cache, v_cache, cache_dtype, k_strides, v_strides,
                                   k_scale, v_scale, ks_strides, vs_strides, block_tables, bt_strides, context_lens,
                                   max_context_len, out, out_strides, batch, num_heads, num_kv_heads, head_dim,

@@ -90,7 +90,7 @@ def test_no_alloc_rejects_oversized_geometry():
     out = torch.empty_like(w.q)
     args = _args(w, out)
     # pretend 1024 sequences of 128 query heads over a 512-page table: about
-    # 130 MiB of split-K partials, beyond the 64 MiB scratch (the call is
+    # 81 MiB of streaming partials, beyond the 64 MiB scratch (the call is
     # rejected before anything is launched, so the small tensors are never read)
     need = lib.prism_paged_decode_workspace_bytes(1024, 128, 8, 128, 256, 512, 3)
     assert need > 64 << 20
