@@ -38,9 +38,13 @@ namespace {
 
 // Measurement aids of the streaming kernel (bit 1: skip compute, 2: skip
 // loads, 4: plan phase stamps, 8: per-workgroup start/end times, 16: default
-// cache policy for private pages) exist only in a build that defines
-// PRISM_DECODE_MEASURE (read from PRISM_STREAM_DEBUG there).  The product
-// library compiles them out: it always loads and computes every tile.
+// cache policy for private pages, 32: per-workgroup stamps of the kernel's
+// phases and merge counts, 64: per-wave cycles spent waiting, issuing,
+// computing and flushing) exist only in a build that defines
+// PRISM_DECODE_MEASURE (read from PRISM_STREAM_DEBUG there).  Bits 32 and 64
+// write into the plan's key area, so the call after a stamped one rebuilds
+// its plan.  The product library compiles them out: it always loads and
+// computes every tile.
 #ifdef PRISM_DECODE_MEASURE
 #define PRISM_DBG(a) ((a).debug)
 #else
@@ -1499,8 +1503,10 @@ __device__ __forceinline__ void stream_column(const DecodeArgs& a, int V, int i,
 // partial with m = -inf attended nothing and weighs 0.  Eight candidates are
 // loaded per round, (m, l) and 32 accumulator bytes each, with a running
 // maximum across rounds; the usual sequence has at most eight, so its merge
-// is one round of loads.  `rec` is b's plan record (first, end, virtual slot,
-// virtual first, virtual end).
+// is one round of loads.  This code runs once per workgroup, from a cold
+// instruction cache, so it is kept small: row arithmetic in 32 bits (the
+// partial region is addressed with 32-bit byte offsets anyway).  `rec` is
+// b's plan record (first, end, virtual slot, virtual first, virtual end).
 template <int QDT, int TPR>
 __device__ __forceinline__ void stream_merge_seq(const DecodeArgs& a, int V, int b, const int* rec,
                                                  const StreamSplit& sp) {
@@ -1519,17 +1525,25 @@ __device__ __forceinline__ void stream_merge_seq(const DecodeArgs& a, int V, int
   }
   const int cnt = (cnt0 + cnt1) << tl;
   const int d0 = 8 * (threadIdx.x & 15);
+  // with at least one tile per workgroup every range is non-empty; otherwise
+  // a workgroup with an empty range wrote nothing (64-bit divisions to tell)
+  const bool all_ranges = sp.total >= sp.nwg;
+  // per candidate: row = base + w * stride + slot * slot_stride, where the
+  // real candidates' (w from lo0) and the virtual ones' (w from lo1) differ
+  const int stride0 = kSKv * a.groups, stride1 = kSKv * kSCols;
+  const int sstride0 = a.num_heads, sstride1 = hkv * kSCols;
   // whole-region resources (the partial region is far below 4 GiB)
   const __amdgpu_buffer_rsrc_t acc_r = __builtin_amdgcn_make_buffer_rsrc(a.part_acc, 0, 0x7FFFFFFF, 0x00020000);
   const __amdgpu_buffer_rsrc_t ml_r = __builtin_amdgcn_make_buffer_rsrc(a.part_ml, 0, 0x7FFFFFFF, 0x00020000);
   for (int hq = threadIdx.x >> 4; hq < a.num_heads; hq += kSThreads / 16) {
-    const int64_t rbase0 = static_cast<int64_t>(V + b) * (kSKv * a.groups) + hq;
-    int64_t rbase1 = 0;
+    const int rbase0 = (V + b) * stride0 + hq + lo0 * stride0;
+    int rbase1 = 0;
     if (vslot >= 0) {
       const int v = vslot / kSCols;
       const int m = vslot - v * kSCols;
       const int hk = hq / a.groups;
-      rbase1 = a.vrow0 + (static_cast<int64_t>(v) * kSKv + hk) * kSCols + m * a.groups + (hq - hk * a.groups);
+      rbase1 = static_cast<int>(a.vrow0) + (v * kSKv + hk) * kSCols + m * a.groups + (hq - hk * a.groups) +
+               lo1 * stride1;
     }
     float m_run = -INFINITY, l_sum = 0.f;
     float o[8];
@@ -1544,13 +1558,16 @@ __device__ __forceinline__ void stream_merge_seq(const DecodeArgs& a, int V, int
         const int wi = i >> tl;
         const int sl = i & ((1 << tl) - 1);
         const bool second = wi >= cnt0;
-        const int64_t w = second ? lo1 + (wi - cnt0) : lo0 + wi;
-        const int64_t row = second ? rbase1 + w * (kSKv * kSCols) + sl * (hkv * kSCols)
-                                   : rbase0 + w * (kSKv * a.groups) + sl * a.num_heads;
-        // a workgroup with an empty range (fewer tiles than workgroups) wrote nothing
-        const bool ok = base + u < cnt && split_begin(sp, w) < split_begin(sp, w + 1);
-        const float2 ml = load_coherent2(ml_r, static_cast<uint32_t>(row * 8));
-        const uint32_t off = static_cast<uint32_t>((row * kHeadDim + d0) * 4);
+        const int wk = second ? wi - cnt0 : wi;  // workgroup offset from lo0 or lo1
+        const int row = (second ? rbase1 : rbase0) + wk * (second ? stride1 : stride0) +
+                        sl * (second ? sstride1 : sstride0);
+        bool ok = base + u < cnt;
+        if (!all_ranges) {
+          const int64_t w = (second ? lo1 : lo0) + wk;
+          ok = ok && split_begin(sp, w) < split_begin(sp, w + 1);
+        }
+        const float2 ml = load_coherent2(ml_r, static_cast<uint32_t>(row) * 8u);
+        const uint32_t off = (static_cast<uint32_t>(row) * kHeadDim + d0) * 4u;
         x0[u] = load_coherent4(acc_r, off);
         x1[u] = load_coherent4(acc_r, off + 16);
         mv[u] = ok ? ml.x : -INFINITY;
@@ -1635,11 +1652,20 @@ __device__ __forceinline__ void stream_finish(const DecodeArgs& a, int V, const 
   }
   __syncthreads();
   const int nm = *n_merge;
+  if ((PRISM_DBG(a) & 32) && threadIdx.x == 0) {  // measurement aid: merges, counted
+    int* d = a.plan + kPlanKeyBt + 8 * blockIdx.x;
+    d[3] = nm;
+    d[4] = static_cast<int>(__builtin_amdgcn_s_memrealtime() & 0x7FFFFFFF);
+  }
   if (nm == 0) return;
   const StreamSplit sp = stream_split(a, a.plan[1]);
   for (int k = 0; k < nm; ++k) {
     const int* e = merge_rec + 8 * k;
     stream_merge_seq<QDT, TPR>(a, V, e[0], e + 1, sp);
+    if ((PRISM_DBG(a) & 32) && k == 0 && threadIdx.x == 0) {  // measurement aid: first merge done
+      int* d = a.plan + kPlanKeyBt + 8 * blockIdx.x;
+      d[6] = static_cast<int>(__builtin_amdgcn_s_memrealtime() & 0x7FFFFFFF);
+    }
   }
   static_assert(kRec + 1 <= 8, "merge record stride");
 }
@@ -1656,6 +1682,7 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   const int g = lane >> 4;
   const int c = lane & 15;
   const int B = a.batch;
+  const uint64_t r_entry = (PRISM_DBG(a) & 32) ? __builtin_amdgcn_s_memrealtime() : 0;
 
   // ---- the plan's tile prefix sums (virtual sequences, then real ones)
   // one round of loads: this workgroup's start record, the plan header and
@@ -1697,6 +1724,7 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   const uint8_t* ivb;
   const float* isb;
   bool ivalid;
+  bool iprivate;          // the entry is a real sequence: its pages stream past the caches
   uint32_t stage_nv = 0;  // byte s: attended tokens of the tile in stage s
   auto ipage_set = [&](int raw_or_load) {
     // raw_or_load: a block id already known, or kNoBlock to read it
@@ -1725,6 +1753,7 @@ paged_decode_stream_kernel(const DecodeArgs a) {
     ipage = it0 / P;
     itip = (it0 - ipage * P) / kTTok;
     ipage0 = itok0 / P;
+    iprivate = ie >= V && !(PRISM_DBG(a) & 16);
     ipage_set(first_raw);
   };
   ientry(__builtin_amdgcn_readfirstlane(wr0.y), __builtin_amdgcn_readfirstlane(wr1.w));
@@ -1734,8 +1763,7 @@ paged_decode_stream_kernel(const DecodeArgs a) {
     const int nv = ivalid ? min(iend - it0, kTTok) : 0;
     stage_nv = (stage_nv & ~(0xFFu << (8 * istage))) | (static_cast<uint32_t>(nv) << (8 * istage));
     if (!(PRISM_DBG(a) & 2))
-      stream_issue(pl, ikb, ivb, isb, stage0 + static_cast<uint32_t>(istage) * kSStage,
-                   ie >= V && !(PRISM_DBG(a) & 16));
+      stream_issue(pl, ikb, ivb, isb, stage0 + static_cast<uint32_t>(istage) * kSStage, iprivate);
     ++issued;
     istage = istage == kSStages - 1 ? 0 : istage + 1;
     if (issued == count) return;  // the range is done (no page past it is read)
@@ -1806,6 +1834,16 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   const int tok_lane = TPR * 4 * g + h / (kSKv / TPR);
 
   int cstage = 0;
+  // measurement aid (bit 64): cycles per section of the loop, per wave
+  uint64_t xs[4] = {0, 0, 0, 0};
+  uint64_t xs_t = (PRISM_DBG(a) & 64) ? __builtin_amdgcn_s_memtime() : 0;
+  auto xs_mark = [&](int k) {
+    if (PRISM_DBG(a) & 64) {
+      const uint64_t n = __builtin_amdgcn_s_memtime();
+      xs[k] += n - xs_t;
+      xs_t = n;
+    }
+  };
   for (int done = 0; done < count; ++done) {
     // Wait for this tile's loads (the younger tiles' loads may stay in flight),
     // then one barrier: every wave's loads have landed and every wave has
@@ -1820,8 +1858,10 @@ paged_decode_stream_kernel(const DecodeArgs a) {
       else __builtin_amdgcn_s_waitcnt(0xF70);
     }
     stream_barrier();
+    xs_mark(0);
     const int nv = __builtin_amdgcn_readfirstlane((stage_nv >> (8 * cstage)) & 0xFF);
     if (issued < count) issue_next();
+    xs_mark(1);
 
     if (nv != 0 && !(PRISM_DBG(a) & 1)) {
       const uint32_t slot = static_cast<uint32_t>(cstage) * kSStage;
@@ -1911,6 +1951,7 @@ paged_decode_stream_kernel(const DecodeArgs a) {
       }
     }
     cstage = cstage == kSStages - 1 ? 0 : cstage + 1;
+    xs_mark(2);
 
     // ---- flush at the end of a stream entry (or of this workgroup's range)
     if (--cleft == 0 || done + 1 == count) {
@@ -1954,13 +1995,26 @@ paged_decode_stream_kernel(const DecodeArgs a) {
         stream_load_q8<QDT, QVEC>(a, qrow, qhead, colv, g, qop);
       }
     }
+    xs_mark(3);
+  }
+  if ((PRISM_DBG(a) & 64) && lane == 0) {
+    int* d = a.plan + kPlanKeyBt + 4096 + 4 * (blockIdx.x * kSKv + h);
+    for (int k = 0; k < 4; ++k) d[k] = static_cast<int>(xs[k] & 0x7FFFFFFF);
   }
 
   // ---- completion: count this range's flushes, merge completed sequences
   __syncthreads();  // every wave is done with the stages (reused as scratch)
-  const uint64_t t_loop = (PRISM_DBG(a) & 8) ? __builtin_amdgcn_s_memrealtime() : 0;
+  const uint64_t t_loop = (PRISM_DBG(a) & (8 | 32)) ? __builtin_amdgcn_s_memrealtime() : 0;
   stream_finish<QDT, TPR>(a, V, tstart, __builtin_amdgcn_readfirstlane(wr0.x), b - wr0.x + 1,
                           reinterpret_cast<int*>(stages));
+  if ((PRISM_DBG(a) & 32) && threadIdx.x == 0) {  // measurement aid: phase stamps (100 MHz clock)
+    int* d = a.plan + kPlanKeyBt + 8 * blockIdx.x;
+    d[0] = static_cast<int>(r_entry & 0x7FFFFFFF);
+    d[1] = static_cast<int>(t_begin & 0x7FFFFFFF);
+    d[2] = static_cast<int>(t_loop & 0x7FFFFFFF);
+    d[5] = static_cast<int>(__builtin_amdgcn_s_memrealtime() & 0x7FFFFFFF);
+    d[7] = (b - wr0.x + 1) | ((wr0.x < V) ? 0x10000 : 0) | (count << 17);  // entries, virtual first, tiles
+  }
   if ((PRISM_DBG(a) & 8) && threadIdx.x == 0) {  // measurement aid: start, loop end, end (100 MHz clock)
     const uint64_t t_end = __builtin_amdgcn_s_memrealtime();
     a.plan[kPlanWgTime + 2 * blockIdx.x] = static_cast<int>(t_begin & 0x7FFFFFFF);
