@@ -1,31 +1,100 @@
-"""No-op profiling facade with the reference's region API.
+"""Profiling boundary of the ops, with the reference's API.
 
-Mirrors ``profile_region(name, cuda=True, metadata=None)`` of
-prism_infer/observability/performance.py:31-42: a context manager that does
-nothing unless a provider is installed with :func:`install_profile_provider`.
-The ops keep the reference's region names (``attention.kv_store.*``,
-``attention.decode.*``) so existing trace tooling keeps working.
+The API follows prism_infer/observability/performance.py:13-47:
+``profile_region(name, *, cuda=True, metadata=None)`` returns a context
+manager, a no-op until a provider pair is installed with
+:func:`install_performance_provider` (non-callables raise TypeError), and
+:func:`get_performance_profile_session` returns the installed session
+provider's current session (None without one).  The ops keep the reference's
+region names (``attention.kv_store.*``) so trace tooling keyed on them keeps
+working.
+
+Two ready-made region providers are included:
+
+* :func:`record_function_region` -- a ``torch.profiler.record_function`` range,
+  visible in ``torch.profiler`` traces;
+* :func:`roctx_region` -- a ROCTX range (``torch.cuda.nvtx`` is ROCTX on
+  ROCm), visible in ``rocprofv3 --marker-trace``; metadata is appended to the
+  range name as ``key=value`` pairs.
 """
 
 from __future__ import annotations
 
-from contextlib import nullcontext
-from typing import Any, Callable
+from contextlib import AbstractContextManager, contextmanager, nullcontext
+from typing import Any, Callable, Iterator, Optional
 
-_PROVIDER: Callable[..., Any] | None = None
+ProfileRegionProvider = Callable[..., AbstractContextManager]
+ProfileSessionProvider = Callable[[], Optional[Any]]
 
-
-def install_profile_provider(provider: Callable[..., Any] | None) -> None:
-    """Install (or clear with ``None``) a callable returning a context manager."""
-
-    global _PROVIDER
-    _PROVIDER = provider
+_region_provider: Optional[ProfileRegionProvider] = None
+_session_provider: Optional[ProfileSessionProvider] = None
 
 
-def profile_region(name: str, cuda: bool = True, metadata: dict | None = None):
-    if _PROVIDER is None:
+def install_performance_provider(*, profile_region_provider: Optional[ProfileRegionProvider],
+                                 profile_session_provider: Optional[ProfileSessionProvider]) -> None:
+    """Install both providers, or remove them by passing ``None`` for both."""
+
+    global _region_provider, _session_provider
+    if profile_region_provider is None and profile_session_provider is None:
+        _region_provider = _session_provider = None
+        return
+    if not callable(profile_region_provider) or not callable(profile_session_provider):
+        raise TypeError("install_performance_provider: both providers must be callables "
+                        f"(got {type(profile_region_provider).__name__} and "
+                        f"{type(profile_session_provider).__name__})")
+    _region_provider = profile_region_provider
+    _session_provider = profile_session_provider
+
+
+def profile_region(name: str, *, cuda: bool = True, metadata: Optional[dict] = None) -> AbstractContextManager:
+    """A region of the installed provider, or a no-op context."""
+
+    provider = _region_provider
+    if provider is None:
         return nullcontext()
-    return _PROVIDER(name, cuda=cuda, metadata=metadata)
+    return provider(name, cuda=cuda, metadata=metadata)
 
 
-__all__ = ["install_profile_provider", "profile_region"]
+def get_performance_profile_session() -> Optional[Any]:
+    provider = _session_provider
+    return None if provider is None else provider()
+
+
+def _label(name: str, metadata: Optional[dict]) -> str:
+    if not metadata:
+        return name
+    return name + " " + " ".join(f"{k}={metadata[k]}" for k in sorted(metadata))
+
+
+@contextmanager
+def record_function_region(name: str, *, cuda: bool = True, metadata: Optional[dict] = None) -> Iterator[None]:
+    """Region provider: a ``torch.profiler.record_function`` range."""
+
+    import torch  # noqa: PLC0415
+
+    with torch.profiler.record_function(_label(name, metadata)):
+        yield
+
+
+@contextmanager
+def roctx_region(name: str, *, cuda: bool = True, metadata: Optional[dict] = None) -> Iterator[None]:
+    """Region provider: a ROCTX range around the block (host-side markers;
+    ``cuda`` is accepted for API compatibility, the range does not wait for
+    the device)."""
+
+    import torch  # noqa: PLC0415
+
+    torch.cuda.nvtx.range_push(_label(name, metadata))
+    try:
+        yield
+    finally:
+        torch.cuda.nvtx.range_pop()
+
+
+__all__ = [
+    "get_performance_profile_session",
+    "install_performance_provider",
+    "profile_region",
+    "record_function_region",
+    "roctx_region",
+]
