@@ -242,6 +242,12 @@ def main() -> int:
     parser.add_argument("--no-extras", action="store_true", help="skip store/compaction/single-sequence extras")
     parser.add_argument("--copy-probe", action="store_true",
                         help="only run a plain 1 GiB device copy (reference for rocprof FETCH/WRITE_SIZE scaling)")
+    parser.add_argument("--store-probe", action="store_true",
+                        help="only run the config-2 store, 8 calls over 8 distinct input chunks (target for rocprof "
+                             "FETCH/WRITE_SIZE of the store kernel)")
+    parser.add_argument("--compaction-probe", action="store_true",
+                        help="only run the config-5 compaction (payload and scale calls) 3 times (target for rocprof "
+                             "FETCH/WRITE_SIZE of the compaction kernels)")
     parser.add_argument("--prefill-probe", action="store_true",
                         help="only run the paged-prefill extra warm, 3 + 10 calls (target for rocprof statistics "
                              "and SQ counters of the prefill kernel)")
@@ -273,6 +279,41 @@ def main() -> int:
             dst.copy_(src)
         torch.cuda.synchronize()
         print(json.dumps({"copy_probe_bytes_read": src.numel(), "copy_probe_bytes_written": dst.numel(), "calls": 5}))
+        return 0
+
+    if args.store_probe:
+        from prism_infer.ops.kv_cache_store import store_kvcache  # noqa: PLC0415
+
+        sw = workloads.store_prefill(dev)
+        kc = torch.empty(sw.num_pages, 256, 8, 128, dtype=torch.float8_e4m3fn, device=dev)
+        vc = torch.empty_like(kc)
+        ks = torch.empty(sw.num_pages, 256, 8, dtype=torch.float32, device=dev)
+        vs = torch.empty_like(ks)
+        keys = [sw.key.roll(i, 0) for i in range(8)]
+        values = [sw.value.roll(i, 0) for i in range(8)]
+        torch.cuda.synchronize()
+        for i in range(8):
+            store_kvcache(keys[i], values[i], kc, vc, sw.slot_mapping, ks, vs)
+        torch.cuda.synchronize()
+        print(json.dumps({"store_probe_calls": 8, "algorithmic_bytes_per_call": sw.algorithmic_bytes()}))
+        return 0
+
+    if args.compaction_probe:
+        from prism_infer.ops.kv_compaction import compact_kv_slots  # noqa: PLC0415
+
+        cw = workloads.compaction_plans()
+        slots = cw.num_pages * 256
+        payload = torch.zeros(2, 1, slots, 8, 128, dtype=torch.uint8, device=dev).view(torch.float8_e4m3fn)
+        scales = torch.zeros(2, 1, slots, 8, dtype=torch.float32, device=dev)
+        src = torch.tensor([x for p in cw.plans for x in p.source_slots], dtype=torch.long, device=dev)
+        dst = torch.tensor([x for p in cw.plans for x in p.destination_slots], dtype=torch.long, device=dev)
+        torch.cuda.synchronize()
+        for _ in range(3):
+            compact_kv_slots(payload, src, dst)
+            compact_kv_slots(scales, src, dst)
+        torch.cuda.synchronize()
+        print(json.dumps({"compaction_probe_calls": 3, "algorithmic_bytes_per_call": cw.algorithmic_bytes(),
+                          "kept_tokens": cw.kept}))
         return 0
 
     if args.prefill_probe:

@@ -45,6 +45,15 @@ const char* prism_last_error(void);
 int prism_device_cu_count(void);
 
 /*
+ * Load every kernel's code object on the current device now (HIP otherwise
+ * loads a code object at the first launch of one of its kernels, which stalls
+ * that call for tens of milliseconds).  No counterpart in the reference (its
+ * Triton kernels compile on first call); for hosts that want the first
+ * decode step to run at speed.  Returns PRISM_OK or PRISM_ERR_HIP.
+ */
+int prism_preload(void);
+
+/*
  * KV store.  Replaces the kernels behind
  *   store_kvcache(key, value, k_cache, v_cache, slot_mapping,
  *                 k_scale_cache=None, v_scale_cache=None)

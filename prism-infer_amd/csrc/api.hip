@@ -54,6 +54,18 @@ const char* prism_last_error(void) { return prism::g_last_error.c_str(); }
 
 int prism_device_cu_count(void) { return prism::device_cu_count(); }
 
+int prism_preload(void) {
+  prism::clear_error();
+  hipFuncAttributes attr;
+  if (int rc = prism::check_hip(hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&prism::fp8_encode_kernel)),
+                                "prism_preload"))
+    return rc;
+  if (int rc = prism::preload_kv_store()) return rc;
+  if (int rc = prism::preload_kv_compaction()) return rc;
+  if (int rc = prism::preload_paged_prefill()) return rc;
+  return prism::preload_paged_decode();
+}
+
 int prism_debug_fp8_encode(const float* in, uint8_t* out, int64_t n, void* stream) {
   prism::clear_error();
   if (n < 0 || (n % 4) != 0) {

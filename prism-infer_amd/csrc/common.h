@@ -23,6 +23,12 @@ int check_hip(hipError_t err, const char* what);
 // Launch-error check after a kernel launch.
 inline int check_launch(const char* what) { return check_hip(hipGetLastError(), what); }
 
+// Per source file: load its code object on the current device (see prism_preload).
+int preload_kv_store();
+int preload_kv_compaction();
+int preload_paged_prefill();
+int preload_paged_decode();
+
 int device_cu_count();
 
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }

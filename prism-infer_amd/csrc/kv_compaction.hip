@@ -203,6 +203,13 @@ int launch_moves(uint8_t* cache, int64_t rows, int64_t num_slots, int64_t vec_by
 }
 
 }  // namespace
+
+// Loads this file's code object now rather than at its first kernel launch.
+int preload_kv_compaction() {
+  hipFuncAttributes attr;
+  return check_hip(hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&clear_words_kernel)), "preload_kv_compaction");
+}
+
 }  // namespace prism
 
 extern "C" int64_t prism_compact_slots_workspace_bytes(int64_t rows, int64_t num_slots, int64_t vec_bytes,

@@ -410,6 +410,13 @@ int dispatch_lanes(int lanes, const void* key, const void* value, int64_t kb, in
 }
 
 }  // namespace
+
+// Loads this file's code object now rather than at its first kernel launch.
+int preload_kv_store() {
+  hipFuncAttributes attr;
+  return check_hip(hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&kv_store_scalar_kernel)), "preload_kv_store");
+}
+
 }  // namespace prism
 
 extern "C" int prism_kv_store(const void* key, const void* value, int in_dtype,

@@ -2322,6 +2322,14 @@ int launch_all(int stage, const DecodeArgs& args, const Geometry& geo, bool page
 }
 
 }  // namespace
+
+// Loads this file's code object now rather than at its first kernel launch.
+int preload_paged_decode() {
+  hipFuncAttributes attr;
+  return check_hip(hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&paged_decode_stream_plan_kernel)),
+                   "preload_paged_decode");
+}
+
 }  // namespace prism
 
 extern "C" int prism_paged_decode_set_overrides(int path, int split_tokens, int share) {

@@ -548,6 +548,13 @@ int dispatch_tile(const PrefillArgs& a, bool scaled, int total_q, hipStream_t st
 }
 
 }  // namespace
+
+// Loads this file's code object now rather than at its first kernel launch.
+int preload_paged_prefill() {
+  hipFuncAttributes attr;
+  return check_hip(hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&paged_prefill_kernel<PRISM_DTYPE_BF16, 64, 4, true>)), "preload_paged_prefill");
+}
+
 }  // namespace prism
 
 extern "C" int prism_paged_prefill(const void* q, int q_dtype, const int64_t q_strides[3], const void* k_cache,

@@ -39,6 +39,7 @@ SIGNATURES: dict[str, tuple] = {
     "prism_abi_version": (_I, []),
     "prism_last_error": (ctypes.c_char_p, []),
     "prism_device_cu_count": (_I, []),
+    "prism_preload": (_I, []),
     "prism_kv_store": (
         _I,
         [_VP, _VP, _I, _I64P, _I64P, _VP, _VP, _I, _VP, _VP, _VP, _I64, _I, _I, _I64, _VP],
@@ -110,7 +111,22 @@ def lib() -> ctypes.CDLL:
     if version != ABI_VERSION:
         raise RuntimeError(f"{LIB_NAME} ABI version {version} != expected {ABI_VERSION}; rebuild it")
     _LIB = handle
+    _preload(handle)
     return handle
+
+
+def _preload(handle: ctypes.CDLL) -> None:
+    """Load the kernels' code objects on the current GPU now (a code object
+    otherwise loads at its first kernel's launch and stalls that call).
+    Nothing to do without a GPU; a failure on a GPU is an error."""
+
+    import torch  # noqa: PLC0415
+
+    if not torch.cuda.is_available():
+        return
+    status = handle.prism_preload()
+    if status != 0:
+        raise RuntimeError(f"prism_preload failed ({status}): {handle.prism_last_error().decode(errors='replace')}")
 
 
 def available() -> bool:
