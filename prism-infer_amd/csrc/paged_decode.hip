@@ -1493,27 +1493,45 @@ __device__ __forceinline__ void stream_column(const DecodeArgs& a, int V, int i,
   qhead = h * G + (valid ? qh : 0);
 }
 
-// Output of real sequence b from the streaming partials, by the whole
-// workgroup: thread t owns q head t / 16 and dims 8 (t % 16) .. + 7 (the
-// partial layout is covered for up to 32 q heads per pass).  The candidates
-// are the (workgroup, token slot) pairs whose workgroups met b's own tiles or
-// its virtual sequence's tiles; their rows follow the layout the streaming
-// kernel writes (real entry e of workgroup w at (w + e) * 8G + slot * G +
+constexpr int kMergeRedOffset = 4096;  // floats: the merge's LDS scratch starts 16 KiB into the stages
+
+// Outputs of a batch of nb merged sequences from the streaming partials, by
+// the whole workgroup.  A unit is (q head, 8 dims): 16 units per head.  When
+// the heads fill fewer units than threads (fewer q heads than 32, as on a
+// tensor-parallel rank), the threads form ng = threads / units slots of
+// `units` threads; the batch's nb <= ng sequences get ng / nb slots each,
+// slot cg of a sequence merging its candidates cg, cg + ng / nb, ..., and a
+// sequence's slots meet in LDS (`red`, 10 floats per thread), so the batch's
+// loads are in flight together.  Otherwise (nb = 1) one slot covers the heads
+// in passes of 32.  The candidates are the (workgroup, token slot) pairs
+// whose workgroups met b's own tiles or its virtual sequence's tiles (one per
+// workgroup: with fewer kv heads the workgroup merged its token slots before
+// writing); their rows follow the layout the streaming kernel writes (real entry e of workgroup w at (w + e) * 8G + slot * G +
 // column; virtual entry v at vrow0 + ((w + v) * 8 + slot) * 16 + column).  A
 // partial with m = -inf attended nothing and weighs 0.  Eight candidates are
-// loaded per round, (m, l) and 32 accumulator bytes each, with a running
-// maximum across rounds; the usual sequence has at most eight, so its merge
-// is one round of loads.  This code runs once per workgroup, from a cold
-// instruction cache, so it is kept small: row arithmetic in 32 bits (the
-// partial region is addressed with 32-bit byte offsets anyway).  `rec` is
-// b's plan record (first, end, virtual slot, virtual first, virtual end).
+// loaded per round and slot, (m, l) and 32 accumulator bytes each, with a
+// running maximum across rounds; the usual sequence needs one round.  This
+// code runs once per workgroup, from a cold instruction cache, so it is kept
+// small: row arithmetic in 32 bits (the partial region is addressed with
+// 32-bit byte offsets anyway).  `recs` holds per sequence b and its plan
+// record (first, end, virtual slot, virtual first, virtual end), stride 8.
 template <int QDT, int TPR>
-__device__ __forceinline__ void stream_merge_seq(const DecodeArgs& a, int V, int b, const int* rec,
-                                                 const StreamSplit& sp) {
-  constexpr int tl = TPR == 1 ? 0 : (TPR == 2 ? 1 : (TPR == 4 ? 2 : 3));  // log2 of the token slots
+__device__ __forceinline__ void stream_merge_batch(const DecodeArgs& a, int V, const int* recs, int nb,
+                                                   const StreamSplit& sp, float* red) {
+  constexpr int tl = 0;  // one partial per kv head and workgroup entry: the token slots met at the flush
   constexpr int hkv = kSKv / TPR;
   constexpr int kU = 8;
-  const int first = rec[0], end = rec[1], vslot = rec[2], vfirst = rec[3], vend = rec[4];
+  const int units = a.num_heads * 16;
+  const int ng = units >= kSThreads ? 1 : kSThreads / units;  // slots (nb <= ng)
+  const int gpm = ng / nb;                                     // slots per sequence
+  const int slot = ng > 1 ? static_cast<int>(threadIdx.x) / units : 0;
+  const int u0 = ng > 1 ? static_cast<int>(threadIdx.x) - slot * units : static_cast<int>(threadIdx.x);
+  const int kseq = min(slot / gpm, nb - 1);                    // this slot's sequence in the batch
+  const int cg = slot - kseq * gpm;                            // candidate group within it
+  const bool active = slot < nb * gpm;  // other threads only take part in the barriers
+  const int* rec = recs + 8 * kseq;
+  const int b = rec[0];
+  const int first = rec[1], end = rec[2], vslot = rec[3], vfirst = rec[4], vend = rec[5];
   int lo0 = 0, cnt0 = 0, lo1 = 0, cnt1 = 0;
   if (end > first) {
     lo0 = static_cast<int>(split_owner(sp, first));
@@ -1524,7 +1542,7 @@ __device__ __forceinline__ void stream_merge_seq(const DecodeArgs& a, int V, int
     cnt1 = static_cast<int>(split_owner(sp, vend - 1)) - lo1 + 1;
   }
   const int cnt = (cnt0 + cnt1) << tl;
-  const int d0 = 8 * (threadIdx.x & 15);
+  const int d0 = 8 * (u0 & 15);
   // with at least one tile per workgroup every range is non-empty; otherwise
   // a workgroup with an empty range wrote nothing (64-bit divisions to tell)
   const bool all_ranges = sp.total >= sp.nwg;
@@ -1535,7 +1553,8 @@ __device__ __forceinline__ void stream_merge_seq(const DecodeArgs& a, int V, int
   // whole-region resources (the partial region is far below 4 GiB)
   const __amdgpu_buffer_rsrc_t acc_r = __builtin_amdgcn_make_buffer_rsrc(a.part_acc, 0, 0x7FFFFFFF, 0x00020000);
   const __amdgpu_buffer_rsrc_t ml_r = __builtin_amdgcn_make_buffer_rsrc(a.part_ml, 0, 0x7FFFFFFF, 0x00020000);
-  for (int hq = threadIdx.x >> 4; hq < a.num_heads; hq += kSThreads / 16) {
+  for (int u = u0; u < units; u += (ng > 1 ? units : kSThreads)) {  // one pass when ng > 1
+    const int hq = u >> 4;
     const int rbase0 = (V + b) * stride0 + hq + lo0 * stride0;
     int rbase1 = 0;
     if (vslot >= 0) {
@@ -1549,49 +1568,77 @@ __device__ __forceinline__ void stream_merge_seq(const DecodeArgs& a, int V, int
     float o[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) o[j] = 0.f;
-    for (int base = 0; base < cnt; base += kU) {
+    const int mine = active ? (cnt - cg + gpm - 1) / gpm : 0;  // candidates cg, cg + gpm, ...
+    for (int base = 0; base < mine; base += kU) {
       float mv[kU], lv[kU];
       floatx4 x0[kU], x1[kU];
 #pragma unroll
-      for (int u = 0; u < kU; ++u) {
-        const int i = min(base + u, cnt - 1);
+      for (int k = 0; k < kU; ++k) {
+        const int i = min(base + k, mine - 1) * gpm + cg;
         const int wi = i >> tl;
         const int sl = i & ((1 << tl) - 1);
         const bool second = wi >= cnt0;
         const int wk = second ? wi - cnt0 : wi;  // workgroup offset from lo0 or lo1
         const int row = (second ? rbase1 : rbase0) + wk * (second ? stride1 : stride0) +
                         sl * (second ? sstride1 : sstride0);
-        bool ok = base + u < cnt;
+        bool ok = base + k < mine;
         if (!all_ranges) {
           const int64_t w = (second ? lo1 : lo0) + wk;
           ok = ok && split_begin(sp, w) < split_begin(sp, w + 1);
         }
         const float2 ml = load_coherent2(ml_r, static_cast<uint32_t>(row) * 8u);
         const uint32_t off = (static_cast<uint32_t>(row) * kHeadDim + d0) * 4u;
-        x0[u] = load_coherent4(acc_r, off);
-        x1[u] = load_coherent4(acc_r, off + 16);
-        mv[u] = ok ? ml.x : -INFINITY;
-        lv[u] = ok ? ml.y : 0.f;
+        x0[k] = load_coherent4(acc_r, off);
+        x1[k] = load_coherent4(acc_r, off + 16);
+        mv[k] = ok ? ml.x : -INFINITY;
+        lv[k] = ok ? ml.y : 0.f;
       }
       float mx = m_run;
 #pragma unroll
-      for (int u = 0; u < kU; ++u) mx = fmaxf(mx, mv[u]);
+      for (int k = 0; k < kU; ++k) mx = fmaxf(mx, mv[k]);
       if (mx == -INFINITY) continue;  // nothing attended so far
       const float alpha = exp2f(m_run - mx);  // 0 while m_run = -inf
       l_sum *= alpha;
 #pragma unroll
       for (int j = 0; j < 8; ++j) o[j] *= alpha;
 #pragma unroll
-      for (int u = 0; u < kU; ++u) {
-        const float wgt = mv[u] == -INFINITY ? 0.f : exp2f(mv[u] - mx);  // rows with m = -inf weigh 0
-        l_sum += wgt * lv[u];
+      for (int k = 0; k < kU; ++k) {
+        const float wgt = mv[k] == -INFINITY ? 0.f : exp2f(mv[k] - mx);  // rows with m = -inf weigh 0
+        l_sum += wgt * lv[k];
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
-          o[j] += wgt * (wgt != 0.f ? x0[u][j] : 0.f);
-          o[4 + j] += wgt * (wgt != 0.f ? x1[u][j] : 0.f);
+          o[j] += wgt * (wgt != 0.f ? x0[k][j] : 0.f);
+          o[4 + j] += wgt * (wgt != 0.f ? x1[k][j] : 0.f);
         }
       }
       m_run = mx;
+    }
+    if (gpm > 1) {  // a sequence's slots meet in LDS; its slot 0 finishes the unit
+      __syncthreads();  // `red` is free (the previous batch may still read it)
+      if (active) {
+        float* r = red + 10 * threadIdx.x;
+        r[0] = m_run;
+        r[1] = l_sum;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) r[2 + j] = o[j];
+      }
+      __syncthreads();
+      if (!active || cg != 0) continue;
+      float mx = -INFINITY;
+      for (int k = 0; k < gpm; ++k) mx = fmaxf(mx, red[10 * ((kseq * gpm + k) * units + u0)]);
+      const float m_use = mx == -INFINITY ? 0.f : mx;
+      l_sum = 0.f;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) o[j] = 0.f;
+      for (int k = 0; k < gpm; ++k) {
+        const float* r = red + 10 * ((kseq * gpm + k) * units + u0);
+        const float wgt = exp2f(r[0] - m_use);  // 0 for a slot that attended nothing
+        l_sum += wgt * r[1];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) o[j] += wgt * r[2 + j];
+      }
+    } else if (!active) {
+      continue;
     }
     const float inv = l_sum > 0.f ? 1.f / l_sum : 0.f;
     const int64_t obase = static_cast<int64_t>(b) * a.o_sb + static_cast<int64_t>(hq) * a.o_sh;
@@ -1613,6 +1660,7 @@ __device__ __forceinline__ void stream_finish(const DecodeArgs& a, int V, const 
   constexpr int kRec = 5;
   int* n_merge = scratch;
   int* merge_rec = scratch + 4;  // per merged sequence: b, then its 5-int plan record (stride 8)
+  static_assert(kMergeRedOffset * 4 + 10 * 4 * kSThreads <= kSStages * kSStage, "merge scratch fits the stages");
   // this wave's partial stores have completed (device scope): the flushes may be counted
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   if (threadIdx.x == 0) *n_merge = 0;
@@ -1659,10 +1707,14 @@ __device__ __forceinline__ void stream_finish(const DecodeArgs& a, int V, const 
   }
   if (nm == 0) return;
   const StreamSplit sp = stream_split(a, a.plan[1]);
-  for (int k = 0; k < nm; ++k) {
-    const int* e = merge_rec + 8 * k;
-    stream_merge_seq<QDT, TPR>(a, V, e[0], e + 1, sp);
-    if ((PRISM_DBG(a) & 32) && k == 0 && threadIdx.x == 0) {  // measurement aid: first merge done
+  // merges in batches: as many at once as the workgroup has slots (one at a
+  // time when the q heads fill the workgroup)
+  const int units = a.num_heads * 16;
+  const int slots = units >= kSThreads ? 1 : kSThreads / units;
+  for (int k = 0; k < nm; k += slots) {
+    stream_merge_batch<QDT, TPR>(a, V, merge_rec + 8 * k, min(slots, nm - k), sp,
+                                 reinterpret_cast<float*>(scratch) + kMergeRedOffset);
+    if ((PRISM_DBG(a) & 32) && k == 0 && threadIdx.x == 0) {  // measurement aid: first batch done
       int* d = a.plan + kPlanKeyBt + 8 * blockIdx.x;
       d[6] = static_cast<int>(__builtin_amdgcn_s_memrealtime() & 0x7FFFFFFF);
     }
@@ -1950,6 +2002,7 @@ paged_decode_stream_kernel(const DecodeArgs a) {
         acc[2 * jp + 1] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, b1, acc[2 * jp + 1], 0, 0, 0);
       }
     }
+    const int cdone = cstage;  // the stage just consumed (refilled only after the next barrier)
     cstage = cstage == kSStages - 1 ? 0 : cstage + 1;
     xs_mark(2);
 
@@ -1958,8 +2011,62 @@ paged_decode_stream_kernel(const DecodeArgs a) {
       const bool more = done + 1 < count;
       float l_tot = l_run + __shfl_xor(l_run, 16);
       l_tot += __shfl_xor(l_tot, 32);
+      if constexpr (TPR > 1) {
+        // With fewer kv heads a row holds TPR tokens per head and the waves
+        // h, h + Hkv, ... hold token slots of the same kv head: their states
+        // meet (tree of log2 TPR levels) in the stage just consumed, which no
+        // load refills before the next barrier, so the head slots below Hkv
+        // write one partial per kv head and entry.  LDS-only barriers: the
+        // younger tiles' loads stay in flight.
+        constexpr int kHk = kSKv / TPR;
+        constexpr int kState = kSCols * kHeadDim + 2 * kSCols;  // floats of one wave's state
+        static_assert(kSKv / 2 * kState * 4 <= kSStage, "half the waves' states fit one stage");
+        float* buf = reinterpret_cast<float*>(stages + cdone * kSStage);
+        const int sub = h / kHk;
+        const int hk = h - sub * kHk;
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        stream_barrier();  // every wave is done reading the stage
+#pragma unroll
+        for (int span = TPR / 2; span >= 1; span /= 2) {
+          if (sub >= span && sub < 2 * span) {
+            float* st = buf + ((sub - span) * kHk + hk) * kState;
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+              for (int j = 0; j < 8; ++j) st[(4 * g + i) * kHeadDim + c + 16 * j] = acc[j][i];
+            if (g == 0) {
+              st[kSCols * kHeadDim + c] = m_run;
+              st[kSCols * kHeadDim + kSCols + c] = l_tot;
+            }
+          }
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          stream_barrier();
+          if (sub < span) {
+            const float* st = buf + (sub * kHk + hk) * kState;
+            const float pm = st[kSCols * kHeadDim + c];
+            const float pl = st[kSCols * kHeadDim + kSCols + c];
+            const float mx = fmaxf(m_run, pm);
+            const float mu = mx == -INFINITY ? 0.f : mx;
+            l_tot = l_tot * exp2f(m_run - mu) + pl * exp2f(pm - mu);  // exp2(-inf) = 0
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int qr = 4 * g + i;
+              const float mo = __shfl(m_run, qr);
+              const float mp = st[kSCols * kHeadDim + qr];
+              const float mxi = fmaxf(mo, mp);
+              const float mui = mxi == -INFINITY ? 0.f : mxi;
+              const float ao = exp2f(mo - mui), ap = exp2f(mp - mui);
+#pragma unroll
+              for (int j = 0; j < 8; ++j) acc[j][i] = acc[j][i] * ao + st[qr * kHeadDim + c + 16 * j] * ap;
+            }
+            m_run = mx;
+          }
+          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+          stream_barrier();  // the next level reuses the buffer
+        }
+      }
       // partial rows: real entry b at (wg + b) * 8G + slot * G + column; virtual entry v
-      // at vrow0 + ((wg + v) * 8 + h) * 16 + column
+      // at vrow0 + ((wg + v) * 8 + h) * 16 + column (head slots below Hkv only)
       const bool virt = b < V;
       const int ncols = virt ? kSCols : a.groups;
       const int64_t row0 = virt ? a.vrow0 + ((static_cast<int64_t>(blockIdx.x) + b) * kSKv + h) * kSCols
@@ -1969,7 +2076,7 @@ paged_decode_stream_kernel(const DecodeArgs a) {
         const int qr = 4 * g + i;
         const float li = __shfl(l_tot, qr);
         const float mi = __shfl(m_run, qr);
-        if (qr < ncols) {
+        if (qr < ncols && h < kSKv / TPR) {
           const int64_t row = row0 + qr;
           float* dst = a.part_acc + row * kHeadDim + c;
 #pragma unroll
