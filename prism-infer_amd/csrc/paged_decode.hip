@@ -29,6 +29,7 @@
 //   lane-per-token scores, lane-per-dim accumulation, no split-K.
 #include <atomic>
 #include <mutex>
+#include <type_traits>
 
 #include "common.h"
 #include "fp8_mfma.h"
@@ -214,6 +215,76 @@ __device__ __forceinline__ void load_tile(const DecodeArgs& a, int b, int h, int
   }
 }
 
+// The same tile of a 16-bit (bf16 or f16) cache: lane (g, c) holds 64 bytes of
+// K rows c and c + 16 (dims 32g .. 32g + 31) and 16 bytes of the V rows of its
+// 8 slot tokens (dims 8c .. 8c + 7).  No scales (16-bit caches are unscaled).
+struct TileRegs16 {
+  u32x4 k[2][4];   // [half][dims 8q .. 8q + 7 of the lane's 32]
+  u32x4 v[8];      // V rows of tokens {4g+i, 16+4g+i}, dims 8c..8c+7
+  uint32_t kvalid; // bit e: token of slot e is attended
+};
+
+template <bool PAGE_ALIGNED>
+__device__ __forceinline__ void load_tile16(const DecodeArgs& a, int b, int h, int g, int c, int t0, int t_end,
+                                            TileRegs16& r, int32_t blk_pre = -1, bool use_pre = false) {
+  const int32_t* bt_row = a.bt + static_cast<int64_t>(b) * a.bt_sb;
+  r.kvalid = 0;
+  if constexpr (PAGE_ALIGNED) {
+    // The whole tile lies in one page; an absent block reads page 0 and is masked.
+    const int page = t0 / a.page_size;
+    const int off0 = t0 - page * a.page_size;
+    const int32_t blk_raw = use_pre ? blk_pre : bt_row[page * a.bt_sn];
+    const bool blk_ok = blk_raw >= 0 && blk_raw < a.num_blocks;
+    const int64_t blk = blk_ok ? blk_raw : 0;
+    const uint8_t* kbase = a.k + blk * a.k_sblk + static_cast<int64_t>(off0) * a.k_stok + h * a.k_sh;
+    const uint8_t* vbase = a.v + blk * a.v_sblk + static_cast<int64_t>(off0) * a.v_stok + h * a.v_sh;
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const u32x4* p = reinterpret_cast<const u32x4*>(kbase + (c + 16 * hh) * a.k_stok + 64 * g);
+#pragma unroll
+      for (int q = 0; q < 4; ++q) r.k[hh][q] = p[q];
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int tk = slot_token(g, e);
+      r.v[e] = *reinterpret_cast<const u32x4*>(vbase + tk * a.v_stok + 16 * c);
+      r.kvalid |= (blk_ok && t0 + tk < t_end) ? (1u << e) : 0u;
+    }
+  } else {
+#pragma unroll
+    for (int hh = 0; hh < 2; ++hh) {
+      const int tok = t0 + c + 16 * hh;
+#pragma unroll
+      for (int q = 0; q < 4; ++q) r.k[hh][q] = u32x4{0, 0, 0, 0};
+      if (tok < t_end) {
+        const int page = tok / a.page_size;
+        const int32_t blk = bt_row[page * a.bt_sn];
+        if (blk >= 0 && blk < a.num_blocks) {
+          const u32x4* p = reinterpret_cast<const u32x4*>(
+              a.k + blk * a.k_sblk + static_cast<int64_t>(tok - page * a.page_size) * a.k_stok + h * a.k_sh + 64 * g);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) r.k[hh][q] = p[q];
+        }
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int tok = t0 + slot_token(g, e);
+      r.v[e] = u32x4{0, 0, 0, 0};
+      if (tok < t_end) {
+        const int page = tok / a.page_size;
+        const int off = tok - page * a.page_size;
+        const int32_t blk = bt_row[page * a.bt_sn];
+        if (blk >= 0 && blk < a.num_blocks) {
+          r.v[e] = *reinterpret_cast<const u32x4*>(a.v + blk * a.v_sblk + static_cast<int64_t>(off) * a.v_stok +
+                                                   h * a.v_sh + 16 * c);
+          r.kvalid |= 1u << e;
+        }
+      }
+    }
+  }
+}
+
 // Query operand type per q dtype: bf16 MFMA for bf16 (and the hi/lo split of
 // fp32), f16 MFMA for fp16.
 template <int QDT>
@@ -300,9 +371,13 @@ __device__ __forceinline__ bool split_arrive(unsigned long long* cnt, unsigned i
 // merged through LDS; a sequence with one live chunk writes its output there
 // and then, otherwise the chunk writes a partial and the last chunk of
 // (sequence, kv head) to arrive merges all of them: no second launch.
-template <int QDT, bool SCALED, bool PAGE_ALIGNED, bool QVEC>
+template <int QDT, bool SCALED, bool PAGE_ALIGNED, bool QVEC, int CB>
 __global__ void __launch_bounds__(512)
 paged_decode_split_kernel(const DecodeArgs a) {
+  // CB: bytes per cache element, 1 (FP8, scaled or unit) or 2 (a bf16 / f16
+  // cache of the query's dtype, unscaled)
+  static_assert(CB == 1 || (CB == 2 && !SCALED && QDT != PRISM_DTYPE_F32), "16-bit caches: unscaled, 16-bit q");
+  using Tile = typename std::conditional<CB == 1, TileRegs, TileRegs16>::type;
   const int lane = threadIdx.x & 63;
   const int wv = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // tile lane of this wave (uniform)
   const int g = lane >> 4;
@@ -347,8 +422,12 @@ paged_decode_split_kernel(const DecodeArgs a) {
 
   if (t0 < c_end) {  // wave-uniform; a wave past the chunk's end keeps empty state
     // First tile's loads go out before the query is read and converted.
-    TileRegs ta, tb;
-    load_tile<SCALED, PAGE_ALIGNED>(a, b, h, g, c, t0, c_end, ta, blk0, true);
+    Tile ta, tb;
+    auto load = [&](int t, Tile& r, int32_t pre, bool use_pre) {
+      if constexpr (CB == 1) load_tile<SCALED, PAGE_ALIGNED>(a, b, h, g, c, t, c_end, r, pre, use_pre);
+      else load_tile16<PAGE_ALIGNED>(a, b, h, g, c, t, c_end, r, pre, use_pre);
+    };
+    load(t0, ta, blk0, true);
     // The claim goes out behind the first tile's loads (the load counter is
     // in order: ahead of them it would delay the first tile by its own
     // round trip) and is not waited for before the arrival.
@@ -406,7 +485,7 @@ paged_decode_split_kernel(const DecodeArgs a) {
 
 
     // One 32-token tile of kv head h: QK, online softmax, PV.
-    auto compute = [&](TileRegs& cur) {
+    auto compute = [&](Tile& cur) {
       // ---- QK
       floatx4 sc[2];
 #pragma unroll
@@ -414,6 +493,15 @@ paged_decode_split_kernel(const DecodeArgs a) {
         floatx4 accs = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int cc = 0; cc < 4; ++cc) {
+          if constexpr (CB == 2) {  // the cache rows are already MFMA operands
+            if constexpr (QDT == PRISM_DTYPE_F16)
+              accs = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, cur.k[hh][cc]), qop.hi[cc],
+                                                            accs, 0, 0, 0);
+            else
+              accs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, cur.k[hh][cc]), qop.hi[cc],
+                                                             accs, 0, 0, 0);
+            continue;
+          } else {
           const uint32_t w0 = cur.k[hh][cc >> 1][(cc & 1) * 2];
           const uint32_t w1 = cur.k[hh][cc >> 1][(cc & 1) * 2 + 1];
           if constexpr (QDT == PRISM_DTYPE_F16) {
@@ -423,6 +511,7 @@ paged_decode_split_kernel(const DecodeArgs a) {
             accs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qop.hi[cc], accs, 0, 0, 0);
             if constexpr (QDT == PRISM_DTYPE_F32)
               accs = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb, qop.lo[cc], accs, 0, 0, 0);
+          }
           }
         }
         sc[hh] = accs;
@@ -434,7 +523,9 @@ paged_decode_split_kernel(const DecodeArgs a) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const bool ok = ((cur.kvalid >> e) & 1u) && c < G;
-        const float v = sc[e >> 2][e & 3] * (cur.ksc[e] * a.scale_log2);
+        float ksc = 1.f;
+        if constexpr (CB == 1) ksc = cur.ksc[e];
+        const float v = sc[e >> 2][e & 3] * (ksc * a.scale_log2);
         x[e] = ok ? v : -INFINITY;
         tmax = fmaxf(tmax, x[e]);
       }
@@ -444,18 +535,29 @@ paged_decode_split_kernel(const DecodeArgs a) {
       const float m_use = (m_new == -INFINITY) ? 0.f : m_new;
       const float alpha = exp2f(m_run - m_use);
       m_run = m_new;
-      // P * v_scale as a bf16 hi/lo pair (about 16 significant bits): the PV
-      // product then matches fp32 accumulation closely (V itself is exact).
+      // P * v_scale as a hi/lo pair of the PV MFMA's 16-bit type (about 16
+      // significant bits): the PV product then matches fp32 accumulation
+      // closely (V itself is exact).  bf16 for FP8 and bf16 caches, f16 for
+      // an f16 cache (P <= 1 there: no scale).
+      using PvT = typename std::conditional<CB == 2 && QDT == PRISM_DTYPE_F16, f16x8, bf16x8>::type;
       float psum = 0.f;
-      bf16x8 pa, pa_lo;
+      PvT pa, pa_lo;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const float p = exp2f(x[e] - m_use);  // 0 for masked slots
         psum += p;
-        const float pv = ((cur.kvalid >> e) & 1u) ? p * cur.vsc[e] : 0.f;
-        const __bf16 hi = static_cast<__bf16>(pv);
-        pa[e] = hi;
-        pa_lo[e] = static_cast<__bf16>(pv - static_cast<float>(hi));
+        float vsc = 1.f;
+        if constexpr (CB == 1) vsc = cur.vsc[e];
+        const float pv = ((cur.kvalid >> e) & 1u) ? p * vsc : 0.f;
+        if constexpr (CB == 2 && QDT == PRISM_DTYPE_F16) {
+          const _Float16 hi = static_cast<_Float16>(pv);
+          pa[e] = hi;
+          pa_lo[e] = static_cast<_Float16>(pv - static_cast<float>(hi));
+        } else {
+          const __bf16 hi = static_cast<__bf16>(pv);
+          pa[e] = hi;
+          pa_lo[e] = static_cast<__bf16>(pv - static_cast<float>(hi));
+        }
       }
       l_run = l_run * alpha + psum;
 
@@ -472,33 +574,63 @@ paged_decode_split_kernel(const DecodeArgs a) {
       // NaN.  (Done here, at use, so the prefetch of this tile stays
       // asynchronous.)
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        if (!((cur.kvalid >> e) & 1u)) cur.v[e] = u32x2{0, 0};
+      for (int e = 0; e < 8; ++e) {
+        if (!((cur.kvalid >> e) & 1u)) {
+          if constexpr (CB == 1) cur.v[e] = u32x2{0, 0};
+          else cur.v[e] = u32x4{0, 0, 0, 0};
+        }
+      }
 
-      // ---- PV: B operand of N-tile j = byte j of the lane's 8 V rows.
+      // ---- PV: B operand of N-tile j = element j of the lane's 8 V rows.
 #pragma unroll
       for (int jp = 0; jp < 4; ++jp) {  // column pairs (2jp, 2jp+1)
         const int j = 2 * jp;
-        const int dw = j >> 2;
-        const int jj = j & 3;
-        const uint32_t sel = (jj) | ((4 + jj) << 8) | ((jj + 1) << 16) | ((5 + jj) << 24);
-        bf16x8 b0, b1;
+        PvT b0, b1;
+        if constexpr (CB == 2) {
+          // dims 8c + 2jp and 8c + 2jp + 1 are the low and high halves of
+          // dword jp of each token's row: pair them across slot pairs
 #pragma unroll
-        for (int ep = 0; ep < 4; ++ep) {  // slot pairs (2ep, 2ep+1)
-          const uint32_t lo = cur.v[2 * ep][dw];
-          const uint32_t hi = cur.v[2 * ep + 1][dw];
-          const uint32_t pr = __builtin_amdgcn_perm(hi, lo, sel);
-          const bf16x2 cj = fp8x2_to_bf16x2<false>(pr);
-          const bf16x2 cj1 = fp8x2_to_bf16x2<true>(pr);
-          b0[2 * ep] = cj[0];
-          b0[2 * ep + 1] = cj[1];
-          b1[2 * ep] = cj1[0];
-          b1[2 * ep + 1] = cj1[1];
+          for (int ep = 0; ep < 4; ++ep) {  // slot pairs (2ep, 2ep+1)
+            const uint32_t lo = cur.v[2 * ep][jp];
+            const uint32_t hi = cur.v[2 * ep + 1][jp];
+            const uint32_t w0 = __builtin_amdgcn_perm(hi, lo, 0x05040100u);  // low halves
+            const uint32_t w1 = __builtin_amdgcn_perm(hi, lo, 0x07060302u);  // high halves
+            using Pair = typename std::conditional<QDT == PRISM_DTYPE_F16, f16x2, bf16x2>::type;
+            const Pair c0 = __builtin_bit_cast(Pair, w0);
+            const Pair c1 = __builtin_bit_cast(Pair, w1);
+            b0[2 * ep] = c0[0];
+            b0[2 * ep + 1] = c0[1];
+            b1[2 * ep] = c1[0];
+            b1[2 * ep + 1] = c1[1];
+          }
+        } else {
+          const int dw = j >> 2;
+          const int jj = j & 3;
+          const uint32_t sel = (jj) | ((4 + jj) << 8) | ((jj + 1) << 16) | ((5 + jj) << 24);
+#pragma unroll
+          for (int ep = 0; ep < 4; ++ep) {  // slot pairs (2ep, 2ep+1)
+            const uint32_t lo = cur.v[2 * ep][dw];
+            const uint32_t hi = cur.v[2 * ep + 1][dw];
+            const uint32_t pr = __builtin_amdgcn_perm(hi, lo, sel);
+            const bf16x2 cj = fp8x2_to_bf16x2<false>(pr);
+            const bf16x2 cj1 = fp8x2_to_bf16x2<true>(pr);
+            b0[2 * ep] = cj[0];
+            b0[2 * ep + 1] = cj[1];
+            b1[2 * ep] = cj1[0];
+            b1[2 * ep + 1] = cj1[1];
+          }
         }
-        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, b0, acc[j], 0, 0, 0);
-        acc[j + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, b1, acc[j + 1], 0, 0, 0);
-        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa_lo, b0, acc[j], 0, 0, 0);
-        acc[j + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa_lo, b1, acc[j + 1], 0, 0, 0);
+        if constexpr (CB == 2 && QDT == PRISM_DTYPE_F16) {
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, b0, acc[j], 0, 0, 0);
+          acc[j + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa, b1, acc[j + 1], 0, 0, 0);
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa_lo, b0, acc[j], 0, 0, 0);
+          acc[j + 1] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa_lo, b1, acc[j + 1], 0, 0, 0);
+        } else {
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, b0, acc[j], 0, 0, 0);
+          acc[j + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa, b1, acc[j + 1], 0, 0, 0);
+          acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa_lo, b0, acc[j], 0, 0, 0);
+          acc[j + 1] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa_lo, b1, acc[j + 1], 0, 0, 0);
+        }
       }
     };
 
@@ -509,12 +641,12 @@ paged_decode_split_kernel(const DecodeArgs a) {
     constexpr int kStep = kSplitWaves * kTile;
     while (true) {
       int tn = (t0 + kStep < c_end) ? t0 + kStep : t0;
-      load_tile<SCALED, PAGE_ALIGNED>(a, b, h, g, c, tn, c_end, tb);
+      load(tn, tb, -1, false);
       compute(ta);
       t0 += kStep;
       if (t0 >= c_end) break;
       tn = (t0 + kStep < c_end) ? t0 + kStep : t0;
-      load_tile<SCALED, PAGE_ALIGNED>(a, b, h, g, c, tn, c_end, ta);
+      load(tn, ta, -1, false);
       compute(tb);
       t0 += kStep;
       if (t0 >= c_end) break;
@@ -2287,8 +2419,12 @@ unsigned int next_split_epoch() {
 
 bool stream_disabled() { return forced_path() == 1; }
 
+// FP8 caches (scaled or unit scale) and 16-bit caches (bf16, f16; the split-K
+// kernel takes them when the query has the cache's dtype).
 bool fast_geometry(int num_heads, int num_kv_heads, int head_dim, int cache_dtype) {
-  if (cache_dtype != PRISM_DTYPE_FP8_E4M3FN || head_dim != kHeadDim) return false;
+  const bool dtype_ok = cache_dtype == PRISM_DTYPE_FP8_E4M3FN || cache_dtype == PRISM_DTYPE_BF16 ||
+                        cache_dtype == PRISM_DTYPE_F16;
+  if (!dtype_ok || head_dim != kHeadDim) return false;
   if (num_kv_heads <= 0 || num_kv_heads > 8 || num_heads % num_kv_heads) return false;
   return num_heads / num_kv_heads <= 16;
 }
@@ -2341,7 +2477,8 @@ Geometry geometry(int batch, int num_heads, int num_kv_heads, int head_dim, int 
                     (num_kv_heads & (num_kv_heads - 1)) == 0)
                        ? kSTile * (kSKv / num_kv_heads)
                        : 0;  // 8, 4, 2 or 1 kv heads
-  geo.stream_shape = ttok > 0 && page_size % ttok == 0 && batch <= kSMaxBatch && !stream_disabled() &&
+  geo.stream_shape = cache_dtype == PRISM_DTYPE_FP8_E4M3FN && ttok > 0 && page_size % ttok == 0 &&
+                     batch <= kSMaxBatch && !stream_disabled() &&
                      device_cu_count() * kSWgPerCu <= kSMaxWg;
   if (geo.stream_shape && forced_path() != 2) {
     const int64_t cap_tiles = static_cast<int64_t>(batch) * ceil_div(static_cast<int64_t>(width) * page_size, ttok);
@@ -2412,17 +2549,22 @@ int launch_all(int stage, const DecodeArgs& args, const Geometry& geo, bool page
   {
     const dim3 grid(args.batch, args.num_kv_heads, geo.max_splits);
     const dim3 block(64 * kSplitWaves);
-#define PRISM_LAUNCH_SPLIT(S, A)                                                                   \
-  do {                                                                                             \
-    if (args.q_vec)                                                                                \
-      hipLaunchKernelGGL((paged_decode_split_kernel<QDT, S, A, true>), grid, block, 0, stream, args);  \
-    else                                                                                           \
-      hipLaunchKernelGGL((paged_decode_split_kernel<QDT, S, A, false>), grid, block, 0, stream, args); \
+#define PRISM_LAUNCH_SPLIT(S, A, CB)                                                                   \
+  do {                                                                                                 \
+    if (args.q_vec)                                                                                    \
+      hipLaunchKernelGGL((paged_decode_split_kernel<QDT, S, A, true, CB>), grid, block, 0, stream, args);  \
+    else                                                                                               \
+      hipLaunchKernelGGL((paged_decode_split_kernel<QDT, S, A, false, CB>), grid, block, 0, stream, args); \
   } while (0)
-    if (scaled && page_aligned) PRISM_LAUNCH_SPLIT(true, true);
-    else if (scaled) PRISM_LAUNCH_SPLIT(true, false);
-    else if (page_aligned) PRISM_LAUNCH_SPLIT(false, true);
-    else PRISM_LAUNCH_SPLIT(false, false);
+    if (args.cache_dtype != PRISM_DTYPE_FP8_E4M3FN) {  // 16-bit cache of the query's dtype, unscaled
+      if constexpr (QDT != PRISM_DTYPE_F32) {
+        if (page_aligned) PRISM_LAUNCH_SPLIT(false, true, 2);
+        else PRISM_LAUNCH_SPLIT(false, false, 2);
+      }
+    } else if (scaled && page_aligned) PRISM_LAUNCH_SPLIT(true, true, 1);
+    else if (scaled) PRISM_LAUNCH_SPLIT(true, false, 1);
+    else if (page_aligned) PRISM_LAUNCH_SPLIT(false, true, 1);
+    else PRISM_LAUNCH_SPLIT(false, false, 1);
 #undef PRISM_LAUNCH_SPLIT
     return check_launch("paged_decode_split_kernel launch");
   }
@@ -2547,7 +2689,9 @@ extern "C" int prism_paged_decode_stage(
                     k_strides[2] % 16 == 0 && v_strides[0] % 16 == 0 && v_strides[1] % 16 == 0 &&
                     v_strides[2] % 16 == 0;
     // The branch-free tile loader reads page 0 for absent blocks: needs >= 1 page.
-    if (!ok || num_blocks < 1) geo.fast = false, geo.ws_bytes = 0, geo.max_splits = 1;
+    // A 16-bit cache feeds the MFMAs as it is, so the query must have its dtype.
+    const bool dtype_ok = cache_dtype == PRISM_DTYPE_FP8_E4M3FN || q_dtype == cache_dtype;
+    if (!ok || num_blocks < 1 || !dtype_ok) geo.fast = false, geo.ws_bytes = 0, geo.max_splits = 1;
   }
   if (geo.fast && geo.ws_bytes > 0) {
     if (!workspace || workspace_bytes < geo.ws_bytes) {
