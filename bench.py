@@ -528,10 +528,11 @@ def _graph_steps(step, n_layers: int, outs, alg_bytes: int, torch, reps: int = 2
 
 def _extras(torch, dev, workloads) -> dict:
     """GPU time of the other configurations: store (config 2), compaction
-    (config 5), B = 1 decode over 36 layers (config 3) and a batch of
-    copy-on-write block copies.  Each runs after a 1 GiB write that evicts the
-    MALL and L2 ("cold"), queued behind a GPU spin so that only GPU time is
-    measured (``_time_queued``)."""
+    (config 5), B = 1 decode over 36 layers (config 3), the config-5 chain,
+    paged prefill, a batch of copy-on-write block copies and config 4's
+    decode over unit-scale FP8 and bf16 caches.  Each runs after a 1 GiB
+    write that evicts the MALL and L2 ("cold"), queued behind a GPU spin so
+    that only GPU time is measured (``_time_queued``)."""
 
     from prism_infer.engine.kv_block_ops import copy_kv_blocks  # noqa: PLC0415
     from prism_infer.ops.kv_cache_store import store_kvcache  # noqa: PLC0415
@@ -648,6 +649,25 @@ def _extras(torch, dev, workloads) -> dict:
     s = _time_queued(cow, 1, torch, flush=flush)
     out["copy_on_write_blocks"] = {"us": round(s * 1e6, 2), "GBps": round(nbytes / s / 1e9, 1), "bytes": nbytes,
                                    "pairs": len(pairs), "layers": 4, "timing": "queued behind a spin, cold"}
+    del scache
+    # the dense variants of config 4's decode (same sequences, tables and
+    # pages): a unit-scale FP8 cache (no scale caches) and a bf16 cache (the
+    # dequantised pages), both on the split-K kernel, which reads each
+    # sequence's pages (shared ones included) once per sequence
+    w = workloads.decode_mixed(dev)
+    attended = int(w.context_lens.sum().item())
+    variants = {}
+    for name, k, v, row in (("unit_scale_fp8", w.k_cache, w.v_cache, 2 * 8 * 128),
+                            ("bf16", (w.k_cache.float() * w.k_scale.unsqueeze(-1)).to(torch.bfloat16),
+                             (w.v_cache.float() * w.v_scale.unsqueeze(-1)).to(torch.bfloat16), 2 * 8 * 128 * 2)):
+        call = lambda i, k=k, v=v: paged_decode_attention(  # noqa: E731
+            w.q, k, v, w.block_tables, w.context_lens, w.scale, max_context_len=w.max_context_len)
+        s = _time_queued(call, 3, torch, flush=flush)
+        variants[name] = {"us": round(s * 1e6, 1), "GBps_attended": round(attended * row / s / 1e9, 1),
+                          "bytes_attended": attended * row}
+        del k, v
+    out["decode_mixed_dense_variants"] = {**variants, "timing": "3 calls back to back, queued behind a spin, cold"}
+    del w
     return out
 
 
