@@ -17,9 +17,10 @@
 // v_mfma_f32_16x16x32_{bf16,f16} (fp8 -> bf16/f16 is exact; the key scale
 // multiplies the rows of S^T), runs the online softmax per query column
 // (log2 domain, lazy rescaling), and accumulates O^T += V^T P^T with
-// v_mfma_f32_16x16x16_f16, V^T coming from ds_read_b64_tr_b8 and P * v_scale
-// entering as f16 (a tile whose v scales exceed 255 is shifted by a power of
-// two, exactly).  Only tiles on the diagonal apply the causal mask.
+// v_mfma_f32_16x16x32_bf16 (v_mfma_f32_16x16x16_bf16 for 16-key steps), V^T
+// coming from ds_read_b64_tr_b8 (fp8 -> bf16 is exact) and P * v_scale
+// entering as bf16, whose fp32 exponent range holds every v scale from the
+// 1e-6 floor up.  Only tiles on the diagonal apply the causal mask.
 //
 // Metadata stays on the device: each workgroup finds its sequence and query
 // block from cu_seqlens_q with a wave scan.  Invalid lengths or block ids
@@ -37,7 +38,6 @@ constexpr int kPfColBlocks = 2;                // column blocks per wave
 constexpr int kPfQTile = kPfCols * kPfColBlocks;  // query tokens per workgroup
 constexpr int kPfMaxWaves = 8;                 // GQA group size limit
 constexpr float kPfRescaleThreshold = 8.0f;    // log2 units
-constexpr float kPfF16MaxVScale = 255.0f;      // P <= 2^8, so P * v_scale < 65504
 
 struct PrefillArgs {
   const void* q;
@@ -146,7 +146,7 @@ paged_prefill_kernel(const PrefillArgs a) {
   constexpr int NB = KT >= 32 ? 2 : 1;            // 16-key blocks per softmax step
   constexpr int kStep = 16 * NB;                  // keys per softmax step
   static_assert(NB == 1 || KT / kStep <= 2, "the V reads below cover two steps per tile");
-  using POp = typename std::conditional<NB == 2, f16x8, f16x4>::type;
+  using POp = typename std::conditional<NB == 2, bf16x8, shortx4>::type;  // P * v_scale, bf16 (bits for NB = 1)
   __shared__ __attribute__((aligned(16))) uint8_t stages[2 * kStage];
 
   int seq, qblock;
@@ -301,7 +301,7 @@ paged_prefill_kernel(const PrefillArgs a) {
         if (key0 > qpos0 + kPfQTile - 1) break;              // above the diagonal for every column
         // per 16-key block b: K rows, scales and the transposed V reads
         u32x4 kw[NB][2];
-        floatx4 ksv[NB], vsv[NB];
+        floatx4 ksv[NB];
         uint64_t vt[NB][4];
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
@@ -311,7 +311,6 @@ paged_prefill_kernel(const PrefillArgs a) {
           kw[b][1] = *reinterpret_cast<const u32x4*>(sbp + k_off1);
           const float* scl = reinterpret_cast<const float*>(st + 2 * kPayload) + sb * 16 + 4 * g;
           ksv[b] = *reinterpret_cast<const floatx4*>(scl);
-          vsv[b] = *reinterpret_cast<const floatx4*>(scl + KT);
         }
         {
           uint32_t ad[4];
@@ -338,18 +337,6 @@ paged_prefill_kernel(const PrefillArgs a) {
 #pragma unroll
             for (int jp = 0; jp < 4; ++jp) vt[b][jp] &= keep2;
           }
-        }
-        float vmax4 = fmaxf(fmaxf(vsv[0][0], vsv[0][1]), fmaxf(vsv[0][2], vsv[0][3]));
-        if constexpr (NB == 2) vmax4 = fmaxf(vmax4, fmaxf(fmaxf(vsv[1][0], vsv[1][1]), fmaxf(vsv[1][2], vsv[1][3])));
-        int vexp = 0;  // wave-uniform power-of-two shift of P * v_scale
-        if (__builtin_amdgcn_ballot_w64(vmax4 > kPfF16MaxVScale) != 0) {
-          float vmax = vmax4;
-#pragma unroll
-          for (int off = 32; off >= 1; off >>= 1) vmax = fmaxf(vmax, __shfl_xor(vmax, off));
-          vexp = __builtin_amdgcn_readfirstlane(ilogbf(vmax / kPfF16MaxVScale) + 1);
-          const float down = ldexpf(1.f, -vexp);
-#pragma unroll
-          for (int b = 0; b < NB; ++b) vsv[b] *= down;  // P * v_scale enters shifted down by 2^vexp
         }
         // S^T = K Q^T for both column blocks, one K block at a time (its
         // operand converted once)
@@ -430,6 +417,13 @@ paged_prefill_kernel(const PrefillArgs a) {
             }
           }
         }
+        // v scales are read here, where P is formed, not with the K scales:
+        // held across the QK MFMAs they push the kernel past 256 VGPRs
+        floatx4 vsv[NB];
+#pragma unroll
+        for (int b = 0; b < NB; ++b)
+          vsv[b] = *reinterpret_cast<const floatx4*>(reinterpret_cast<const float*>(st + 2 * kPayload) + KT +
+                                                     (sp * NB + b) * 16 + 4 * g);
 #pragma unroll
         for (int cb = 0; cb < kPfColBlocks; ++cb) {
           const float m_use = (m_run[cb] == -INFINITY) ? 0.f : m_run[cb];
@@ -441,19 +435,13 @@ paged_prefill_kernel(const PrefillArgs a) {
               // v_exp_f32: arguments are at most 2^3 above the running max;
               // results below 2^-126 (flushed to 0) weigh nothing next to it
               p[b][i] = __builtin_amdgcn_exp2f(fmaf(x[cb][b][i], a.scale_log2, -m_use));  // 0 where masked
-              pa[cb][4 * b + i] = static_cast<_Float16>(p[b][i] * vsv[b][i]);
+              if constexpr (NB == 2) pa[cb][4 * b + i] = static_cast<__bf16>(p[b][i] * vsv[b][i]);
+              else pa[cb][4 * b + i] = __builtin_bit_cast(short, static_cast<__bf16>(p[b][i] * vsv[b][i]));
             }
           }
           float ps = (p[0][0] + p[0][1]) + (p[0][2] + p[0][3]);
           if constexpr (NB == 2) ps += (p[1][0] + p[1][1]) + (p[1][2] + p[1][3]);
           l_run[cb] += ps;
-        }
-        if (vexp != 0) {
-          const float down = ldexpf(1.f, -vexp);
-#pragma unroll
-          for (int cb = 0; cb < kPfColBlocks; ++cb)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) acc[cb][j] *= down;
         }
         // O += P V: V operand (B) for dims 16 j + c, one N-tile at a time,
         // shared by the column blocks; k-slots as P's
@@ -462,26 +450,19 @@ paged_prefill_kernel(const PrefillArgs a) {
 #pragma unroll
           for (int hi = 0; hi < 2; ++hi) {
             const int j = 2 * jp + hi;
-            const f16x4 v0 = fp8x4_to_f16x4(static_cast<uint32_t>(vt[0][jp] >> (32 * hi)));
+            const uint32_t w0 = static_cast<uint32_t>(vt[0][jp] >> (32 * hi));
             if constexpr (NB == 2) {
-              const f16x4 v1 = fp8x4_to_f16x4(static_cast<uint32_t>(vt[NB - 1][jp] >> (32 * hi)));
-              const f16x8 vb = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
+              const bf16x8 vb = fp8x8_to_bf16x8(w0, static_cast<uint32_t>(vt[NB - 1][jp] >> (32 * hi)));
 #pragma unroll
               for (int cb = 0; cb < kPfColBlocks; ++cb)
-                acc[cb][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(pa[cb], vb, acc[cb][j], 0, 0, 0);
+                acc[cb][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[cb], vb, acc[cb][j], 0, 0, 0);
             } else {
+              const shortx4 v0 = fp8x4_to_bf16x4_bits(w0);
 #pragma unroll
               for (int cb = 0; cb < kPfColBlocks; ++cb)
-                acc[cb][j] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa[cb], v0, acc[cb][j], 0, 0, 0);
+                acc[cb][j] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa[cb], v0, acc[cb][j], 0, 0, 0);
             }
           }
-        }
-        if (vexp != 0) {
-          const float up = ldexpf(1.f, vexp);
-#pragma unroll
-          for (int cb = 0; cb < kPfColBlocks; ++cb)
-#pragma unroll
-            for (int j = 0; j < 8; ++j) acc[cb][j] *= up;
         }
       }
     }

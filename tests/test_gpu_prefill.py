@@ -124,8 +124,8 @@ def test_prefill_unit_scale_and_f16_queries():
 
 
 def test_prefill_large_v_scales_and_packed_qkv_view():
-    """v scales above 255 take the power-of-two shift of P * v_scale; q is a
-    strided view of a packed QKV projection."""
+    """v scales in the thousands (P * v_scale far above f16's range, held by
+    the bf16 PV operand); q is a strided view of a packed QKV projection."""
 
     require_gpu()
     c = _case(20260815, [(33, 200), (20, 500)], v_scale_mult=4000.0, qkv_view=True)
@@ -133,6 +133,29 @@ def test_prefill_large_v_scales_and_packed_qkv_view():
     want = _want(c, oracle.prefill_reference_fp32).float()
     rel = (got - want).abs().max().item() / want.abs().max().item()
     assert rel < 2e-2, rel
+
+
+@pytest.mark.parametrize("spread", ["mixed", "tiny"])
+def test_prefill_v_scales_across_the_range(spread):
+    """v scales from the 1e-6 floor to 1e4 mixed inside the same pages
+    ("mixed"), or all between 1e-6 and 1e-3 ("tiny"): P * v_scale enters the
+    PV MFMA as bf16, whose exponent range is fp32's, so no v scale loses
+    precision to subnormals or overflows.  Checked per (token, head) relative
+    to that row's largest |output| (1e-2), as the decode scale tests do."""
+
+    require_gpu()
+    c = _case(20260820 if spread == "mixed" else 20260821, [(48, 300), (17, 700), (64, 64)])
+    g = torch.Generator().manual_seed(7)
+    lo, hi = (-6.0, 4.0) if spread == "mixed" else (-6.0, -3.0)
+    c["vs"] = torch.pow(10.0, torch.empty(c["vs"].shape).uniform_(lo, hi, generator=g))
+    got = _run(c).float()
+    want = _want(c, oracle.prefill_reference_fp32).float()
+    assert torch.isfinite(got).all()
+    row_max = want.abs().amax(dim=-1, keepdim=True)
+    rel = (got - want).abs() / row_max.clamp(min=1e-30)
+    print(f"[v scales {spread}] row-relative max {rel.max().item():.3e} mean {rel.mean().item():.3e}; "
+          f"|out| {row_max.min().item():.3e}..{row_max.max().item():.3e}", flush=True)
+    assert rel.max().item() < 1e-2 and rel.mean().item() < 1e-3
 
 
 def test_prefill_long_chunk():
