@@ -361,8 +361,8 @@ def main() -> int:
     torch.cuda.synchronize()
     _log(f"timing {args.steps} steps")
     sec_per_step = _time_loop(step, args.steps, torch)
-    # dominant kernel alone (stage 1: the partial kernel, without the streaming
-    # kernel's plan -- still valid in the workspace -- and without the merge),
+    # dominant kernel alone (stage 1: the streaming kernel, which checks the
+    # plan in the workspace and merges its own partials -- the whole step),
     # same stream, same rotation
     for i in range(args.warmup):
         step(i, 1)

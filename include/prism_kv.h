@@ -103,11 +103,12 @@ int prism_kv_store(const void* key, const void* value, int in_dtype, const int64
  *              bytes for the same geometry; may be NULL when that function
  *              returns 0.  It holds split-K partials with their arrival
  *              counters (tagged per call, so leftovers of any other call or
- *              use count as zero) and, for the streaming kernel, a work plan
- *              (prefix-sharing groups, tile ranges) together with the inputs
- *              it was computed from; a call whose block tables and context
- *              lengths equal those of the previous call on the same
- *              workspace reuses the plan.  Any initial contents are valid.
+ *              use count as zero) and, for the streaming kernel, two work
+ *              plans (prefix-sharing groups, tile ranges), each with the
+ *              inputs it was computed from, behind a plan word; a call whose
+ *              block tables and context lengths equal those of the current
+ *              plan reuses it, otherwise one workgroup of the call builds the
+ *              other plan and publishes it.  Any initial contents are valid.
  *              Calls that share a workspace must be ordered on one stream.
  */
 int64_t prism_paged_decode_workspace_bytes(int batch, int num_heads, int num_kv_heads, int head_dim,
@@ -151,12 +152,12 @@ int prism_paged_decode_noalloc(const void* q, int q_dtype, const int64_t q_strid
 /*
  * Stage selector for measurement: the same as prism_paged_decode but runs only
  * one part of it.  stage 0 runs everything and is identical to
- * prism_paged_decode; stage 1 runs the decode kernel without the streaming
- * kernel's plan (both the split-K and the streaming kernel merge their own
- * partials in the same launch, so stage 1 of those is the whole decode and
- * stage 2 launches nothing); stage 3 only the streaming kernel's plan
- * (nothing for the other kernels).  Stage 1 of the streaming kernel uses the
- * plan already in the workspace: run stage 0 or 3 with the same inputs first.
+ * prism_paged_decode; stage 1 runs the decode kernel (every family is one
+ * launch that merges its own partials and, for the streaming kernel, checks
+ * and if needed builds its plan, so stage 1 is the whole decode and stage 2
+ * launches nothing); stage 3 only builds the streaming kernel's plan in the
+ * workspace, as a separate one-workgroup launch (nothing for the other
+ * kernels).
  */
 int prism_paged_decode_stage(int stage, const void* q, int q_dtype, const int64_t q_strides[3],
                              const void* k_cache, const void* v_cache, int cache_dtype,

@@ -41,11 +41,11 @@ namespace {
 // loads, 4: plan phase stamps, 8: per-workgroup start/end times, 16: default
 // cache policy for private pages, 32: per-workgroup stamps of the kernel's
 // phases and merge counts, 64: per-wave cycles spent waiting, issuing,
-// computing and flushing) exist only in a build that defines
-// PRISM_DECODE_MEASURE (read from PRISM_STREAM_DEBUG there).  Bits 32 and 64
-// write into the plan's key area, so the call after a stamped one rebuilds
-// its plan.  The product library compiles them out: it always loads and
-// computes every tile.
+// computing and flushing, 128: trust the plan slot without comparing its
+// key) exist only in a build that defines PRISM_DECODE_MEASURE (read from
+// PRISM_STREAM_DEBUG there).  Bits 32 and 64 write into a stamp area after
+// the plan slots.  The product library compiles them out: it always checks
+// the plan and loads and computes every tile.
 #ifdef PRISM_DECODE_MEASURE
 #define PRISM_DBG(a) ((a).debug)
 #else
@@ -75,7 +75,7 @@ struct DecodeArgs {
   int64_t o_sb, o_sh, o_sd;
   float* part_acc;  // [B][S][Hq][D]
   float* part_ml;   // [B][S][Hq][2]
-  int* plan;        // streaming path: shared-page plan at the workspace start
+  int* plan_region;  // streaming path: plan word, two plan slots, measurement stamps (workspace start)
   int64_t vrow0;    // streaming path: first partial row of the virtual sequences
   int share;        // streaming path: analyse prefix sharing
   int stream_nwg;   // streaming path: grid size
@@ -85,13 +85,13 @@ struct DecodeArgs {
   int split;     // split-K path: tokens per chunk (multiple of 8 tiles)
   int max_splits;  // split-K path: chunks per (sequence, kv head)
   unsigned long long* split_cnt;  // split-K path: arrival counters, [batch][kv heads]
-  unsigned int epoch;             // split-K path: this call's counter tag (nonzero)
+  unsigned int epoch;             // this call's tag (nonzero): split-K counters, streaming plan word
   float scale_log2;  // sm_scale * log2(e)
   int cache_dtype;
   int debug;         // measurement aid for the stream kernel (0 in normal use)
   // streaming path: tokens per 1 KB LDS row (8 / num_kv_heads) and per tile
   // (16 rows); the streaming and merge kernels take the former as a template
-  // parameter, the plan kernel reads both
+  // parameter, the plan code reads both
   int s_tpr, s_ttok;
 };
 
@@ -793,9 +793,12 @@ paged_decode_split_kernel(const DecodeArgs a) {
 // Persistent, tile-balanced kernel for the canonical page layout
 // ([num_blocks][P % 16 == 0][8 kv heads][128] FP8, scales [num_blocks][P][8]):
 //
-// * Three kernels: a one-workgroup plan kernel (prefix-sharing groups and the
-//   tile prefix sums, see "shared pages" below), the streaming kernel, and
-//   the merge of its partials.
+// * One launch.  Every workgroup first checks the plan (prefix-sharing
+//   groups and the tile prefix sums, see "shared pages" below) left in the
+//   workspace by an earlier call against this call's metadata; when it
+//   differs, one workgroup rebuilds it into the other of two plan slots while
+//   the rest wait (plan_select_slow).  The workgroups merge the partials of
+//   the sequences they complete (stream_finish).
 // * One workgroup (8 waves, wave = kv head) per CU.  The 16-token tiles
 //   of the stream (virtual sequences over shared pages first, then every
 //   sequence's own tiles) are split into gridDim.x equal contiguous ranges, so
@@ -803,7 +806,7 @@ paged_decode_split_kernel(const DecodeArgs a) {
 //   mix.  A range spanning several stream entries emits one (m, l, acc)
 //   partial per (workgroup, entry) pair; as ranges are contiguous and
 //   monotone the pairs form a staircase and `wg + entry` indexes them
-//   uniquely.  The merge kernel combines them.
+//   uniquely.  The last workgroup to finish a sequence combines them.
 // * A tile is one contiguous slab per tensor (K [16 tok][8 h][128 B], V
 //   likewise, and the fp32 scales).  The workgroup copies tiles straight into
 //   LDS with global_load_lds (16 B per lane), four stages, so while the
@@ -813,13 +816,15 @@ paged_decode_split_kernel(const DecodeArgs a) {
 //   head row are XOR-swizzled by token so row-parallel K reads and transposed
 //   V reads spread over the banks.
 //   Scales are stored [head][token] so a lane's four tokens are one 16-byte read.
-// * QK: 4 MFMA f32_16x16x32_bf16 per tile (A = K rows fp8 -> bf16, exact;
-//   B = Q^T, 16 query columns: the G heads of one sequence, or of up to 16/G
-//   sequences for a virtual sequence).  Lane (g, c) gets the scores of query
-//   column c for tokens 4g..4g+3.
-// * PV: MFMA f32_16x16x16_f16, whose four k slots per lane are exactly those
-//   four tokens, so P needs no data movement; P * v_scale goes in as f16
-//   (2^-11 relative; V bytes convert to f16 exactly), one MFMA per N-tile.  The V operand comes
+// * QK: MFMA f32_16x16x128_f8f6f4 on the fp8 K rows as they are (B = Q^T
+//   split into three fp8 terms whose sum carries q's bf16 value; 16 query
+//   columns: the G heads of one sequence, or of up to 16/G sequences for a
+//   virtual sequence).  Lane (g, c) gets the scores of query column c for
+//   tokens 4g..4g+3.
+// * PV: MFMA f32_16x16x16_bf16, whose four k slots per lane are exactly those
+//   four tokens, so P needs no data movement; P * v_scale goes in as bf16
+//   (2^-9 relative, fp32's exponent range; V bytes convert to bf16 exactly),
+//   one MFMA per N-tile.  The V operand comes
 //   from ds_read_b64_tr_b8, which hands lane i of each 16-lane group byte i of
 //   eight 16-byte rows: rows 0-3 = tokens 4g..4g+3 at dims 16j.., rows 4-7 =
 //   the same tokens at dims 16(j+1).., i.e. two N-tiles per read.
@@ -1118,7 +1123,7 @@ __device__ __forceinline__ void stream_load_q8(const DecodeArgs& a, int qrow, in
 //
 // Prefix sharing: sequences whose block tables start with the same physical
 // pages (a shared read-only prefix) would each stream those pages.  The plan
-// kernel finds, on the device, groups of sequences with the same first page
+// build finds, on the device, groups of sequences with the same first page
 // and, per member, how many leading whole pages it shares with the group's
 // leader (the lowest-numbered member).  Members are packed M = 16 / G at a
 // time into "virtual sequences": a virtual sequence walks the leader's shared
@@ -1128,7 +1133,8 @@ __device__ __forceinline__ void stream_load_q8(const DecodeArgs& a, int qrow, in
 // streams only its private tail (the tokens after the shared pages), and the
 // merge combines the partials of its tail with those of its virtual sequence.
 //
-// Plan layout (int32 at the start of the workspace):
+// Plan slot layout (int32; two slots follow the plan word at the start of
+// the workspace):
 //   [0] V (virtual sequences), [1] total tiles
 //   tstart[NS + 1]      tile prefix sums over the stream order, NS = V + batch:
 //                       virtual sequences first, then the real ones
@@ -1182,18 +1188,26 @@ constexpr int kPlanKeyEff = kPlanKey + kPlanKeyParams;       // attended lengths
 constexpr int kPlanKeyBt = kPlanKeyEff + kSMaxBatch;         // compared block-table prefix
 // Per real sequence b, one int at kPlanCnt + b: how many workgroups have
 // flushed a partial that sequence's output depends on in the running call.
-// The plan kernel zeroes them whenever it computes a plan; the workgroup whose
+// A plan build zeroes them in the slot it writes; the workgroup whose
 // flush completes a sequence merges it and sets the counter back to 0, so a
 // call that reuses the plan finds them at zero.
 constexpr int kPlanCnt = kPlanKeyBt + kSShareMaxBatch * kPlanMaxPages;
 constexpr int kPlanInts = kPlanCnt + kSMaxBatch + kSMaxWg;  // + measurement aid: finish times
+// The plan region of the workspace: the plan word (below), then two plan
+// slots of kPlanInts each (4 KB multiples, so no cache line holds parts of
+// both), then the measurement build's stamps.
+constexpr int kPlanHdrInts = 1024;
+constexpr int kPlanSlotInts = (kPlanInts + 1023) / 1024 * 1024;
+constexpr int kPlanMeasure = kPlanHdrInts + 2 * kPlanSlotInts;
+constexpr int kPlanRegionInts = kPlanMeasure + 8 * kSMaxWg + 4 * kSMaxWg * kSKv;
 constexpr int kPlanMagic = 0x504C414E;
+static_assert(kPlanKeyBt % 4 == 0 && kPlanHdrInts % 4 == 0 && kPlanSlotInts % 4 == 0, "16-byte key reads");
 constexpr int kPlanThreads = 1024;
 constexpr int kPlanHashBits = 10;
 constexpr int kPlanHash = 1 << kPlanHashBits;  // >= 2 * kSShareMaxBatch slots
 static_assert(2 * kSShareMaxBatch <= kPlanHash, "hash table load factor");
 static_assert(kSShareMaxBatch / 2 <= kSMaxVirt, "virtual sequences of a full batch fit");
-static_assert(kSMaxBatch <= kPlanThreads, "one thread per sequence in the plan kernel");
+static_assert(kSShareMaxBatch <= kSThreads, "one thread per sequence in the sharing analysis");
 
 // Work split: workgroup w streams tiles [floor(w * total / nwg),
 // floor((w + 1) * total / nwg)).  (Measured on MI355X: per-workgroup times
@@ -1274,8 +1288,10 @@ struct PlanLds {
   int vmem_s[kSMaxVirt * kSCols];
   int hkey[kPlanHash];
   int hmin[kPlanHash];
-  int bt_s[kSShareMaxBatch * kPlanMaxPages];  // compared part of the block tables
+  __attribute__((aligned(16))) int bt_s[kSShareMaxBatch * kPlanMaxPages];  // compared part of the block tables
   int wsum_s[kPlanThreads / 64];
+  unsigned long long w_s;  // plan word as read by thread 0
+  int won_s;               // this workgroup builds the plan
   __attribute__((aligned(16))) int cnt_rank_s[kSShareMaxBatch];  // group of each member or -1
 };
 
@@ -1298,40 +1314,50 @@ __device__ __forceinline__ void plan_key_params(const DecodeArgs& a, bool share,
 // (geometry, attended lengths, compared block-table prefix, plan header)
 // and stages the lengths and the compared block-table prefix into L for a
 // rebuild.  Returns this thread's verdict; the workgroup ANDs them.  All
-// loads of the check go out before anything is compared (one round).  Key
-// words are read with device-scope loads: within one launch of the
-// streaming kernel the key may be rewritten by workgroup 0, and a reader
-// then sees either the old key (and waits for the new plan) or the new one.
+// loads of the check go out before anything is compared (one round).  The
+// slot compared is one the plan word names, which no workgroup writes while
+// the word names it, so ordinary loads read it whole (they are served by each
+// XCD's L2: device-scope loads, which bypass it, send every workgroup of the
+// launch to the same few memory channels and cost about 5 us).
 template <int NT>
-__device__ __forceinline__ bool plan_key_check(const DecodeArgs& a, PlanLds& L) {
+__device__ __forceinline__ bool plan_key_check(const DecodeArgs& a, const int* plan, PlanLds& L) {
   const int tid = threadIdx.x;
   const int B = a.batch;
   const int P = a.page_size;
   const int Wc = min(a.width, kPlanMaxPages);
   const bool share = plan_share(a);
-  const int* key = a.plan + kPlanKey;
-  auto kld = [](const int* p) { return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT); };
+  const int* key = plan + kPlanKey;
+  auto kld = [](const int* p) { return *p; };
   int kp[kPlanKeyParams];
   plan_key_params(a, share, kp);
-  bool same = true;
-  if (tid < kPlanKeyParams - 2) {
-#pragma unroll
-    for (int i = 0; i < kPlanKeyParams - 2; ++i)
-      if (i == tid) same = kld(key + i) == kp[i];
-  }
-  if (tid == 0)
-    same = same && kld(key + kPlanKeyParams - 2) == kld(a.plan) && kld(key + kPlanKeyParams - 1) == kld(a.plan + 1);
-  for (int b = tid; b < B; b += NT) {
-    const int n = effective_len(a, b);
-    same = same && kld(key + kPlanKeyEff - kPlanKey + b) == n;
-    L.eff_s[b] = n;
-    const int cap = min(n / P, Wc);
-    L.cap_s[b] = cap;
-  }
-  const int items = share ? B * Wc : 0;
+  // Every load of the check goes out before the first comparison: lanes
+  // 0..11 read one key word each (a branch per word with a uniform address
+  // would be a chain of dependent scalar loads; words 10 and 11 are copies
+  // of the plan header), each thread the lengths of up to kE sequences and kU
+  // entries of the compared block-table prefix, each with its key word.
+  constexpr int kE = (kSMaxBatch + NT - 1) / NT;
   constexpr int kU = 8;
-  for (int base = 0; base < items; base += kU * NT) {
-    int val[kU], old[kU];
+  const int items = share ? B * Wc : 0;
+  int kword = 0, kwant = 0;  // lanes without a key word compare 0 with 0
+  if (tid < kPlanKeyParams) {
+    kwant = kp[0];
+#pragma unroll
+    for (int i = 1; i < kPlanKeyParams - 2; ++i) kwant = tid == i ? kp[i] : kwant;
+    kword = kld(key + tid);
+    if (tid >= kPlanKeyParams - 2) kwant = kld(plan + (tid - (kPlanKeyParams - 2)));
+  }
+  const int mx = ld_meta(a.max_ctx);
+  int ctxv[kE], keff[kE];
+#pragma unroll
+  for (int e = 0; e < kE; ++e) {
+    const int b = tid + e * NT;
+    ctxv[e] = b < B ? a.ctx[b] : 0;
+    keff[e] = b < B ? kld(key + kPlanKeyEff - kPlanKey + b) : 0;
+  }
+  // block-table prefix entries base + u * NT + tid with their key words
+  bool same = true;
+  int val[kU], old[kU];
+  auto load_bt = [&](int base) {
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
       const int idx = base + u * NT + tid;
@@ -1340,11 +1366,68 @@ __device__ __forceinline__ bool plan_key_check(const DecodeArgs& a, PlanLds& L) 
       val[u] = idx < items ? a.bt[static_cast<int64_t>(b) * a.bt_sb + static_cast<int64_t>(j) * a.bt_sn] : -1;
       old[u] = idx < items ? kld(key + kPlanKeyBt - kPlanKey + idx) : -1;
     }
+  };
+  auto check_bt = [&](int base) {
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
       const int idx = base + u * NT + tid;
       if (idx < items) L.bt_s[idx] = val[u];
-      same = same && old[u] == val[u];
+      same &= old[u] == val[u];
+    }
+  };
+  // block tables with contiguous, 16-byte aligned rows of a multiple of 4
+  // compared pages: 16-byte loads, 4 entries per lane (a quarter of the
+  // requests: every workgroup of the launch reads the same 2 x 16 KB)
+  const bool vec = a.bt_sn == 1 && (a.bt_sb & 3) == 0 && (reinterpret_cast<uintptr_t>(a.bt) & 15) == 0 &&
+                   (Wc & 3) == 0;
+  constexpr int kU4 = 2;
+  int4 val4[kU4], old4[kU4];
+  auto load_bt4 = [&](int base) {  // entries base + 4 (u * NT + tid) .. + 3
+#pragma unroll
+    for (int u = 0; u < kU4; ++u) {
+      const int idx = base + 4 * (u * NT + tid);
+      const int b = idx / Wc;
+      const int j = idx - b * Wc;
+      const bool in = idx < items;
+      val4[u] = in ? *reinterpret_cast<const int4*>(a.bt + static_cast<int64_t>(b) * a.bt_sb + j) : int4{-1, -1, -1, -1};
+      old4[u] = in ? *reinterpret_cast<const int4*>(key + kPlanKeyBt - kPlanKey + idx) : int4{-1, -1, -1, -1};
+    }
+  };
+  auto check_bt4 = [&](int base) {
+#pragma unroll
+    for (int u = 0; u < kU4; ++u) {
+      const int idx = base + 4 * (u * NT + tid);
+      if (idx < items) *reinterpret_cast<int4*>(&L.bt_s[idx]) = val4[u];
+      same &= old4[u].x == val4[u].x && old4[u].y == val4[u].y && old4[u].z == val4[u].z &&
+              old4[u].w == val4[u].w;
+    }
+  };
+  if (vec) load_bt4(0);
+  else load_bt(0);  // the first (usually only) batch leaves with the loads above
+  same = kword == kwant;
+  const int64_t cap_tok = static_cast<int64_t>(a.width) * P;
+#pragma unroll
+  for (int e = 0; e < kE; ++e) {
+    const int b = tid + e * NT;
+    if (b >= B) continue;
+    int64_t n = ctxv[e] < mx ? ctxv[e] : mx;  // effective_len() from the loaded values
+    if (n > cap_tok) n = cap_tok;
+    const int ni = n > 0 ? static_cast<int>(n) : 0;
+    same &= keff[e] == ni;
+    L.eff_s[b] = ni;
+    L.cap_s[b] = min(ni / P, Wc);
+  }
+  if (vec) {
+    check_bt4(0);
+    for (int base = 4 * kU4 * NT; base < items; base += 4 * kU4 * NT) {
+      load_bt4(base);
+      check_bt4(base);
+    }
+  } else {
+    check_bt(0);
+    for (int base = kU * NT; base < items; base += kU * NT) {
+      load_bt(base);
+      check_bt(base);
     }
   }
   return same;
@@ -1354,8 +1437,7 @@ __device__ __forceinline__ bool plan_key_check(const DecodeArgs& a, PlanLds& L) 
 // writes it, its key and zeroed merge counters to the workspace.  tst_s
 // receives the tile prefix sums (NS + 1 entries).
 template <int NT>
-__device__ void plan_build(const DecodeArgs& a, PlanLds& L, int* tst_s) {
-  int* plan = a.plan;
+__device__ void plan_build(const DecodeArgs& a, int* plan, PlanLds& L, int* tst_s) {
   const int tid = threadIdx.x;
   const int B = a.batch;
   const int P = a.page_size;
@@ -1574,32 +1656,119 @@ __device__ void plan_build(const DecodeArgs& a, PlanLds& L, int* tst_s) {
   }
 }
 
-// The plan on its own (stage 3): check the key, rebuild when it differs.
+// The plan word, 64 bits at the start of the plan region:
+//   (epoch << 32) | (building << 1) | slot.
+// `slot` names the plan slot holding the current plan.  A launch whose inputs
+// differ from that slot's key builds the other slot and publishes it by
+// rewriting the word with its own epoch; while it builds, the word carries
+// the building bit and that epoch.  The slot a word names is never written
+// while the word names it, so a reader that compares the key of the slot the
+// word names with its inputs reads a plan that is whole: within a launch only
+// the other slot is written, and a launch starts with the previous launches'
+// writes visible on every XCD.
+constexpr unsigned long long kPlanBuilding = 2;
+constexpr int kPlanSpinLimit = 1 << 22;  // polls of a waiting workgroup (far beyond any build)
+
+__device__ __forceinline__ unsigned long long* plan_word(const DecodeArgs& a) {
+  return reinterpret_cast<unsigned long long*>(a.plan_region);
+}
+
+__device__ __forceinline__ int* plan_slot(const DecodeArgs& a, int slot) {
+  return a.plan_region + kPlanHdrInts + slot * kPlanSlotInts;
+}
+
+__device__ __forceinline__ bool plan_building_here(unsigned long long w, unsigned int epoch) {
+  return (w & kPlanBuilding) != 0 && static_cast<unsigned int>(w >> 32) == epoch;
+}
+
+// Plan selection after the fast check failed (the inputs differ from the key
+// of the slot that word w names, or a workgroup of this launch is building):
+// the first workgroup to swap the plan word from the value it read builds the
+// other slot, writes it back to the device-coherent level (release fence) and
+// publishes it; every other workgroup waits for the publication.  The builder
+// waits for nobody, so the wait ends; it is bounded all the same (after
+// kPlanSpinLimit polls the workgroup gives up with -1).  Returns the slot to
+// use.  Every thread of the workgroup calls it.
+template <int NT>
+__device__ int plan_select_slow(const DecodeArgs& a, PlanLds& L, int* tst_s, unsigned long long w) {
+  unsigned long long* word = plan_word(a);
+  const unsigned int epoch = a.epoch;
+  for (int attempt = 0; attempt < 4; ++attempt) {
+    if (plan_building_here(w, epoch)) {
+      if (threadIdx.x == 0) {
+        unsigned long long x = w;
+        for (int n = 0; n < kPlanSpinLimit && plan_building_here(x, epoch); ++n) {
+          __builtin_amdgcn_s_sleep(4);
+          x = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        L.w_s = x;
+      }
+      __syncthreads();
+      w = L.w_s;
+      __syncthreads();
+      if (plan_building_here(w, epoch)) return -1;
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+    }
+    const int slot = static_cast<int>(w & 1);
+    const bool same = plan_key_check<NT>(a, plan_slot(a, slot), L);
+    if (__syncthreads_and(same ? 1 : 0)) return slot;
+    if (threadIdx.x == 0) {
+      unsigned long long expect = w;
+      const unsigned long long mine =
+          (static_cast<unsigned long long>(epoch) << 32) | kPlanBuilding | static_cast<unsigned long long>(slot);
+      const bool won = __hip_atomic_compare_exchange_strong(word, &expect, mine, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
+                                                            __HIP_MEMORY_SCOPE_AGENT);
+      L.won_s = won ? 1 : 0;
+      L.w_s = won ? mine : expect;
+    }
+    __syncthreads();
+    const bool won = L.won_s != 0;
+    const unsigned long long seen = L.w_s;
+    __syncthreads();
+    if (won) {
+      plan_build<NT>(a, plan_slot(a, 1 - slot), L, tst_s);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");  // the slot reaches the device-coherent level
+      __syncthreads();
+      if (threadIdx.x == 0)
+        __hip_atomic_store(word, (static_cast<unsigned long long>(epoch) << 32) | static_cast<unsigned long long>(1 - slot),
+                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return 1 - slot;
+    }
+    w = seen;  // another workgroup builds (or the word changed): wait for it, then check again
+  }
+  return -1;
+}
+
+// The plan on its own (stage 3): check the key of the current slot, build
+// and publish the other one when it differs.
 __global__ void __launch_bounds__(kPlanThreads) paged_decode_stream_plan_kernel(const DecodeArgs a) {
   __shared__ PlanLds L;
   __shared__ int tst_s[kSMaxBatch + kSMaxVirt + 1];
-  const bool same = plan_key_check<kPlanThreads>(a, L);
-  if (__syncthreads_and(same ? 1 : 0)) return;  // the previous plan still holds
-  plan_build<kPlanThreads>(a, L, tst_s);
+  if (threadIdx.x == 0) L.w_s = __hip_atomic_load(plan_word(a), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  const unsigned long long w = L.w_s;
+  __syncthreads();
+  plan_select_slow<kPlanThreads>(a, L, tst_s, w);
 }
 
 // Walk parameters of stream entry i (i < V: virtual sequence i, else real
 // sequence i - V): block-table row, first token, end token, and the tile at
 // which a virtual sequence starts its walk (it wraps around).
 template <int TPR>
-__device__ __forceinline__ void stream_seq(const DecodeArgs& a, const int* tstart, int V, int i, int& bt_row,
+__device__ __forceinline__ void stream_seq(const DecodeArgs& a, const int* plan, const int* tstart, int V, int i,
+                                           int& bt_row,
                                            int& tok0, int& n_end, int& rot) {
   if (i >= V) {
     const int b = i - V;
     bt_row = b;
-    tok0 = ld_meta(a.plan + kPlanSkip + b);
+    tok0 = ld_meta(plan + kPlanSkip + b);
     n_end = effective_len(a, b);
     rot = 0;
   } else {
-    bt_row = ld_meta(a.plan + kPlanVsrc + i);
+    bt_row = ld_meta(plan + kPlanVsrc + i);
     tok0 = 0;
     n_end = (tstart[i + 1] - tstart[i]) * (kSTile * TPR);
-    rot = ld_meta(a.plan + kPlanVrot + i);
+    rot = ld_meta(plan + kPlanVrot + i);
   }
 }
 
@@ -1607,7 +1776,8 @@ __device__ __forceinline__ void stream_seq(const DecodeArgs& a, const int* tstar
 // sequence b -> q head hk*G + c (c < G); virtual sequence -> q head hk*G + qh
 // of member m, c = m*G + qh.
 template <int TPR>
-__device__ __forceinline__ void stream_column(const DecodeArgs& a, int V, int i, int h_slot, int c, int& qrow,
+__device__ __forceinline__ void stream_column(const DecodeArgs& a, const int* plan, int V, int i, int h_slot, int c,
+                                              int& qrow,
                                               int& qhead, bool& valid) {
   const int G = a.groups;
   const int h = h_slot % (kSKv / TPR);  // kv head of the slot
@@ -1619,7 +1789,7 @@ __device__ __forceinline__ void stream_column(const DecodeArgs& a, int V, int i,
   }
   const int m = c / G;
   const int qh = c - m * G;
-  const int member = (m < kSCols / G) ? a.plan[kPlanVmem + i * kSCols + m] : -1;
+  const int member = (m < kSCols / G) ? plan[kPlanVmem + i * kSCols + m] : -1;
   valid = member >= 0;
   qrow = valid ? member : 0;
   qhead = h * G + (valid ? qh : 0);
@@ -1787,7 +1957,8 @@ __device__ __forceinline__ void stream_merge_batch(const DecodeArgs& a, int V, c
 // that attend no token at all (no tiles, no flushes) get zeros from
 // workgroup b % nwg.  `scratch` is LDS no longer in use (the drained stages).
 template <int QDT, int TPR>
-__device__ __forceinline__ void stream_finish(const DecodeArgs& a, int V, const int* tstart, int e_first, int nent,
+__device__ __forceinline__ void stream_finish(const DecodeArgs& a, int* plan, int V, const int* tstart, int e_first,
+                                              int nent,
                                               int* scratch) {
   constexpr int kRec = 5;
   int* n_merge = scratch;
@@ -1797,7 +1968,7 @@ __device__ __forceinline__ void stream_finish(const DecodeArgs& a, int V, const 
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   if (threadIdx.x == 0) *n_merge = 0;
   __syncthreads();
-  int* cnt = a.plan + kPlanCnt;
+  int* cnt = plan + kPlanCnt;
   const int members = kSCols / a.groups;
   for (int t = threadIdx.x; t < nent * kSCols; t += kSThreads) {
     const int i = e_first + t / kSCols;
@@ -1805,10 +1976,10 @@ __device__ __forceinline__ void stream_finish(const DecodeArgs& a, int V, const 
     if (tstart[i + 1] == tstart[i]) continue;  // no tiles: never flushed
     int seq = -1;
     if (i >= V) seq = slot == 0 ? i - V : -1;
-    else if (slot < members) seq = a.plan[kPlanVmem + i * kSCols + slot];
+    else if (slot < members) seq = plan[kPlanVmem + i * kSCols + slot];
     if (seq < 0) continue;
-    const int4 r0 = *reinterpret_cast<const int4*>(a.plan + kPlanRec + 8 * seq);
-    const int2 r1 = *reinterpret_cast<const int2*>(a.plan + kPlanRec + 8 * seq + 4);  // virtual end, expected
+    const int4 r0 = *reinterpret_cast<const int4*>(plan + kPlanRec + 8 * seq);
+    const int2 r1 = *reinterpret_cast<const int2*>(plan + kPlanRec + 8 * seq + 4);  // virtual end, expected
     const int prev = __hip_atomic_fetch_add(cnt + seq, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     if (prev + 1 == r1.y) {
       __hip_atomic_store(cnt + seq, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1823,7 +1994,7 @@ __device__ __forceinline__ void stream_finish(const DecodeArgs& a, int V, const 
   }
   // zeros for sequences without a single partial
   for (int b = blockIdx.x; b < a.batch; b += a.stream_nwg) {
-    if (a.plan[kPlanRec + 8 * b + 5] != 0) continue;  // uniform
+    if (plan[kPlanRec + 8 * b + 5] != 0) continue;  // uniform
     for (int e = threadIdx.x; e < a.num_heads * kHeadDim; e += kSThreads) {
       const int hq = e / kHeadDim;
       const int d = e - hq * kHeadDim;
@@ -1833,12 +2004,12 @@ __device__ __forceinline__ void stream_finish(const DecodeArgs& a, int V, const 
   __syncthreads();
   const int nm = *n_merge;
   if ((PRISM_DBG(a) & 32) && threadIdx.x == 0) {  // measurement aid: merges, counted
-    int* d = a.plan + kPlanKeyBt + 8 * blockIdx.x;
+    int* d = a.plan_region + kPlanMeasure + 8 * blockIdx.x;
     d[3] = nm;
     d[4] = static_cast<int>(__builtin_amdgcn_s_memrealtime() & 0x7FFFFFFF);
   }
   if (nm == 0) return;
-  const StreamSplit sp = stream_split(a, a.plan[1]);
+  const StreamSplit sp = stream_split(a, plan[1]);
   // merges in batches: as many at once as the workgroup has slots (one at a
   // time when the q heads fill the workgroup)
   const int units = a.num_heads * 16;
@@ -1847,7 +2018,7 @@ __device__ __forceinline__ void stream_finish(const DecodeArgs& a, int V, const 
     stream_merge_batch<QDT, TPR>(a, V, merge_rec + 8 * k, min(slots, nm - k), sp,
                                  reinterpret_cast<float*>(scratch) + kMergeRedOffset);
     if ((PRISM_DBG(a) & 32) && k == 0 && threadIdx.x == 0) {  // measurement aid: first batch done
-      int* d = a.plan + kPlanKeyBt + 8 * blockIdx.x;
+      int* d = a.plan_region + kPlanMeasure + 8 * blockIdx.x;
       d[6] = static_cast<int>(__builtin_amdgcn_s_memrealtime() & 0x7FFFFFFF);
     }
   }
@@ -1861,6 +2032,7 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   constexpr int kTTok = kSTile * TPR;  // tokens per tile
   __shared__ __attribute__((aligned(16))) uint8_t stages[kSStages * kSStage];
   __shared__ int tstart[kSMaxBatch + kSMaxVirt + 1];
+  static_assert(sizeof(PlanLds) <= sizeof(stages), "the plan's LDS lies over the idle stages");
   const int lane = threadIdx.x & 63;
   const int h = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // head slot of this wave (uniform)
   const int g = lane >> 4;
@@ -1868,22 +2040,62 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   const int B = a.batch;
   const uint64_t r_entry = (PRISM_DBG(a) & 32) ? __builtin_amdgcn_s_memrealtime() : 0;
 
-  // ---- the plan's tile prefix sums (virtual sequences, then real ones)
-  // one round of loads: this workgroup's start record, the plan header and
-  // the prefix sums (copied up to the largest possible entry count, so that
-  // these loads need not wait for V)
-  const int4 wr0 = *reinterpret_cast<const int4*>(a.plan + kPlanWgRec + 8 * blockIdx.x);
-  const int4 wr1 = *reinterpret_cast<const int4*>(a.plan + kPlanWgRec + 8 * blockIdx.x + 4);
-  for (int i = threadIdx.x; i <= B + kSMaxVirt; i += kSThreads) tstart[i] = a.plan[kPlanTstart + i];
-  const int V = ld_meta(a.plan);
+  // ---- the plan.  Round 1: the plan word.  Round 2: from the slot it names,
+  // this workgroup's start record, the plan header, the tile prefix sums
+  // (virtual sequences, then real ones; copied up to the largest possible
+  // entry count, so that these loads need not wait for V) and the key, which
+  // is compared with this call's inputs.  When they differ, the plan is
+  // (re)built by one workgroup of the launch while the others wait, and the
+  // same loads are repeated on the new slot.
+  PlanLds& L = *reinterpret_cast<PlanLds*>(stages);
+  const unsigned long long w0 = *reinterpret_cast<const __attribute__((address_space(4))) unsigned long long*>(
+      reinterpret_cast<uintptr_t>(a.plan_region));
+  int* plan = plan_slot(a, __builtin_amdgcn_readfirstlane(static_cast<int>(w0 & 1)));
+  // prefix sums go to registers first and to LDS after the key check, so the
+  // check's loads leave in the same round
+  constexpr int kTs = (kSMaxBatch + kSMaxVirt + 1 + kSThreads - 1) / kSThreads;
+  int4 wr0, wr1;
+  int tsv[kTs];
+  int V;
+  int64_t total;
+  auto load_plan = [&]() {
+    wr0 = *reinterpret_cast<const int4*>(plan + kPlanWgRec + 8 * blockIdx.x);
+    wr1 = *reinterpret_cast<const int4*>(plan + kPlanWgRec + 8 * blockIdx.x + 4);
+#pragma unroll
+    for (int t = 0; t < kTs; ++t) {
+      const int i = threadIdx.x + t * kSThreads;
+      tsv[t] = i <= B + kSMaxVirt ? plan[kPlanTstart + i] : 0;
+    }
+    V = ld_meta(plan);
+    total = ld_meta(plan + 1);
+  };
+  auto store_tstart = [&]() {
+#pragma unroll
+    for (int t = 0; t < kTs; ++t) {
+      const int i = threadIdx.x + t * kSThreads;
+      if (i <= B + kSMaxVirt) tstart[i] = tsv[t];
+    }
+  };
+  load_plan();
+  const bool same =
+      (PRISM_DBG(a) & 128) ? true : (!plan_building_here(w0, a.epoch) && plan_key_check<kSThreads>(a, plan, L));
+  store_tstart();
+  if (__builtin_expect(!__syncthreads_and(same ? 1 : 0), 0)) {
+    const int slot = __builtin_amdgcn_readfirstlane(plan_select_slow<kSThreads>(a, L, tstart, w0));
+    if (slot < 0) return;  // the builder never published (cannot happen: it waits for nobody)
+    plan = plan_slot(a, slot);
+    __syncthreads();  // every thread is done with the build's tstart before it is reloaded
+    load_plan();
+    store_tstart();
+    __syncthreads();
+  }
   const int NS = B + V;
-  const int64_t total = ld_meta(a.plan + 1);
   const StreamSplit sp = stream_split(a, total);
   const int64_t s = split_begin(sp, blockIdx.x);
   const int64_t e = split_begin(sp, blockIdx.x + 1);
   __syncthreads();
   if (s >= e) {  // uniform: an empty range flushes nothing
-    stream_finish<QDT, TPR>(a, V, tstart, 0, 0, reinterpret_cast<int*>(stages));
+    stream_finish<QDT, TPR>(a, plan, V, tstart, 0, 0, reinterpret_cast<int*>(stages));
     return;
   }
   const uint64_t t_begin = __builtin_amdgcn_s_memrealtime();
@@ -1925,7 +2137,7 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   auto ientry = [&](int lt, int first_raw) {
     intl = __builtin_amdgcn_readfirstlane(tstart[ie + 1] - tstart[ie]);
     int rot;
-    stream_seq<TPR>(a, tstart, V, ie, irow, itok0, iend, rot);
+    stream_seq<TPR>(a, plan, tstart, V, ie, irow, itok0, iend, rot);
     irow = __builtin_amdgcn_readfirstlane(irow);
     itok0 = __builtin_amdgcn_readfirstlane(itok0);
     iend = __builtin_amdgcn_readfirstlane(iend);
@@ -1988,7 +2200,7 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   bool colv;
   {
     int qrow, qhead;
-    stream_column<TPR>(a, V, b, h, c, qrow, qhead, colv);
+    stream_column<TPR>(a, plan, V, b, h, c, qrow, qhead, colv);
     stream_load_q8<QDT, QVEC>(a, qrow, qhead, colv, g, qop);
   }
 
@@ -2230,24 +2442,24 @@ paged_decode_stream_kernel(const DecodeArgs a) {
         b = __builtin_amdgcn_readfirstlane(b);
         cleft = min(__builtin_amdgcn_readfirstlane(tstart[b + 1] - tstart[b]), count - done - 1);
         int qrow, qhead;
-        stream_column<TPR>(a, V, b, h, c, qrow, qhead, colv);
+        stream_column<TPR>(a, plan, V, b, h, c, qrow, qhead, colv);
         stream_load_q8<QDT, QVEC>(a, qrow, qhead, colv, g, qop);
       }
     }
     xs_mark(3);
   }
   if ((PRISM_DBG(a) & 64) && lane == 0) {
-    int* d = a.plan + kPlanKeyBt + 4096 + 4 * (blockIdx.x * kSKv + h);
+    int* d = a.plan_region + kPlanMeasure + 8 * kSMaxWg + 4 * (blockIdx.x * kSKv + h);
     for (int k = 0; k < 4; ++k) d[k] = static_cast<int>(xs[k] & 0x7FFFFFFF);
   }
 
   // ---- completion: count this range's flushes, merge completed sequences
   __syncthreads();  // every wave is done with the stages (reused as scratch)
   const uint64_t t_loop = (PRISM_DBG(a) & (8 | 32)) ? __builtin_amdgcn_s_memrealtime() : 0;
-  stream_finish<QDT, TPR>(a, V, tstart, __builtin_amdgcn_readfirstlane(wr0.x), b - wr0.x + 1,
+  stream_finish<QDT, TPR>(a, plan, V, tstart, __builtin_amdgcn_readfirstlane(wr0.x), b - wr0.x + 1,
                           reinterpret_cast<int*>(stages));
   if ((PRISM_DBG(a) & 32) && threadIdx.x == 0) {  // measurement aid: phase stamps (100 MHz clock)
-    int* d = a.plan + kPlanKeyBt + 8 * blockIdx.x;
+    int* d = a.plan_region + kPlanMeasure + 8 * blockIdx.x;
     d[0] = static_cast<int>(r_entry & 0x7FFFFFFF);
     d[1] = static_cast<int>(t_begin & 0x7FFFFFFF);
     d[2] = static_cast<int>(t_loop & 0x7FFFFFFF);
@@ -2256,9 +2468,9 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   }
   if ((PRISM_DBG(a) & 8) && threadIdx.x == 0) {  // measurement aid: start, loop end, end (100 MHz clock)
     const uint64_t t_end = __builtin_amdgcn_s_memrealtime();
-    a.plan[kPlanWgTime + 2 * blockIdx.x] = static_cast<int>(t_begin & 0x7FFFFFFF);
-    a.plan[kPlanWgTime + 2 * blockIdx.x + 1] = static_cast<int>(t_end & 0x7FFFFFFF);
-    a.plan[kPlanCnt + kSMaxBatch + blockIdx.x] = static_cast<int>((t_end - t_loop) & 0x7FFFFFFF);
+    plan[kPlanWgTime + 2 * blockIdx.x] = static_cast<int>(t_begin & 0x7FFFFFFF);
+    plan[kPlanWgTime + 2 * blockIdx.x + 1] = static_cast<int>(t_end & 0x7FFFFFFF);
+    plan[kPlanCnt + kSMaxBatch + blockIdx.x] = static_cast<int>((t_end - t_loop) & 0x7FFFFFFF);
   }
 }
 
@@ -2461,9 +2673,9 @@ Geometry geometry(int batch, int num_heads, int num_kv_heads, int head_dim, int 
     geo.split *= 2;
   geo.max_splits = static_cast<int>(cap > 0 ? ceil_div(cap, geo.split) : 1);
   // Every fast-path workspace starts with the streaming kernel's plan region,
-  // which only the plan kernel writes (a workspace shared by calls of
+  // which only the plan code writes (a workspace shared by calls of
   // different geometries never has its plan overwritten by split partials).
-  const int64_t plan_bytes = align_up(static_cast<int64_t>(kPlanInts) * 4, 256);
+  const int64_t plan_bytes = align_up(static_cast<int64_t>(kPlanRegionInts) * 4, 256);
   if (geo.max_splits <= 1) {
     geo.ws_bytes = 0;
   } else {
@@ -2506,10 +2718,9 @@ Geometry geometry(int batch, int num_heads, int num_kv_heads, int head_dim, int 
 
 template <int QDT>
 int launch_stream(int stage, const DecodeArgs& args, const Geometry& geo, hipStream_t stream) {
-  if (stage == 0 || stage == 3) {
+  if (stage == 3) {  // the plan alone (the streaming kernel checks and, when needed, builds it itself)
     hipLaunchKernelGGL(paged_decode_stream_plan_kernel, dim3(1), dim3(kPlanThreads), 0, stream, args);
-    int rc = check_launch("paged_decode_stream_plan_kernel launch");
-    if (rc || stage == 3) return rc;
+    return check_launch("paged_decode_stream_plan_kernel launch");
   }
   // token slots per row: 1 (8 kv heads), 2 (4), 4 (2) or 8 (1)
   if (stage == 0 || stage == 1) {
@@ -2778,7 +2989,8 @@ extern "C" int prism_paged_decode_stage(
                           ks_strides[0] == vs_strides[0] && aligned(k_scale, 16) && aligned(v_scale, 16) &&
                           ks_strides[0] % 4 == 0;
   if (use_stream) {
-    args.plan = static_cast<int*>(workspace);
+    args.plan_region = static_cast<int*>(workspace);
+    args.epoch = next_split_epoch();
     args.part_acc = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + geo.stream_acc_off);
     args.part_ml = reinterpret_cast<float*>(static_cast<uint8_t*>(workspace) + geo.stream_ml_off);
     args.vrow0 = geo.stream_vrow0;
