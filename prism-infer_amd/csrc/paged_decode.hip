@@ -1199,7 +1199,8 @@ constexpr int kPlanInts = kPlanCnt + kSMaxBatch + kSMaxWg;  // + measurement aid
 constexpr int kPlanHdrInts = 1024;
 constexpr int kPlanSlotInts = (kPlanInts + 1023) / 1024 * 1024;
 constexpr int kPlanMeasure = kPlanHdrInts + 2 * kPlanSlotInts;
-constexpr int kPlanRegionInts = kPlanMeasure + 8 * kSMaxWg + 4 * kSMaxWg * kSKv;
+constexpr int kPlanBuildStamps = kPlanMeasure + 8 * kSMaxWg + 4 * kSMaxWg * kSKv;  // measurement aid: 16 ints
+constexpr int kPlanRegionInts = kPlanBuildStamps + 16;
 constexpr int kPlanMagic = 0x504C414E;
 static_assert(kPlanKeyBt % 4 == 0 && kPlanHdrInts % 4 == 0 && kPlanSlotInts % 4 == 0, "16-byte key reads");
 constexpr int kPlanThreads = 1024;
@@ -1688,9 +1689,12 @@ __device__ __forceinline__ bool plan_building_here(unsigned long long w, unsigne
 // publishes it; every other workgroup waits for the publication.  The builder
 // waits for nobody, so the wait ends; it is bounded all the same (after
 // kPlanSpinLimit polls the workgroup gives up with -1).  Returns the slot to
-// use.  Every thread of the workgroup calls it.
+// use.  Every thread of the workgroup calls it.  `staged`: L already holds
+// this call's inputs from a failed check of the slot w names (the first
+// attempt goes straight to the election).
 template <int NT>
-__device__ int plan_select_slow(const DecodeArgs& a, PlanLds& L, int* tst_s, unsigned long long w) {
+__device__ int plan_select_slow(const DecodeArgs& a, PlanLds& L, int* tst_s, unsigned long long w,
+                                bool staged = false) {
   unsigned long long* word = plan_word(a);
   const unsigned int epoch = a.epoch;
   for (int attempt = 0; attempt < 4; ++attempt) {
@@ -1707,31 +1711,66 @@ __device__ int plan_select_slow(const DecodeArgs& a, PlanLds& L, int* tst_s, uns
       w = L.w_s;
       __syncthreads();
       if (plan_building_here(w, epoch)) return -1;
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+      if ((PRISM_DBG(a) & 32) && blockIdx.x == 1 && threadIdx.x == 0)  // measurement aid
+        a.plan_region[kPlanBuildStamps + 4] = static_cast<int>(__builtin_amdgcn_s_memrealtime() & 0x7FFFFFFF);
+      // Published by this launch's builder, from this call's inputs: use it
+      // without another check.  No acquire fence (an L2 invalidate, which
+      // 255 workgroups issuing at once made take 12 us): this workgroup has
+      // not read the new slot in this launch, so no cache level here holds a
+      // line of it from before the publication (a launch starts with its
+      // caches coherent).
+      if (static_cast<unsigned int>(w >> 32) == epoch) return static_cast<int>(w & 1);
     }
     const int slot = static_cast<int>(w & 1);
-    const bool same = plan_key_check<NT>(a, plan_slot(a, slot), L);
-    if (__syncthreads_and(same ? 1 : 0)) return slot;
+    if (!(staged && attempt == 0)) {
+      const bool same = plan_key_check<NT>(a, plan_slot(a, slot), L);
+      if (__syncthreads_and(same ? 1 : 0)) return slot;
+    }
     if (threadIdx.x == 0) {
+      // Test, then swap.  Compare-exchanges on one word serialise at the
+      // memory (about 0.1 us each), so 256 of them would hold the losers for
+      // tens of microseconds: workgroup 0 tries at once, every other one
+      // first watches the word for up to 3 us and tries only if it is still
+      // unclaimed (any running workgroup may win; none is waited for).
       unsigned long long expect = w;
+      if (blockIdx.x != 0) {
+        const uint64_t t0 = __builtin_amdgcn_s_memrealtime();  // 100 MHz
+        while (expect == w && __builtin_amdgcn_s_memrealtime() - t0 < 300) {
+          __builtin_amdgcn_s_sleep(8);
+          expect = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+      }
       const unsigned long long mine =
           (static_cast<unsigned long long>(epoch) << 32) | kPlanBuilding | static_cast<unsigned long long>(slot);
-      const bool won = __hip_atomic_compare_exchange_strong(word, &expect, mine, __ATOMIC_RELAXED, __ATOMIC_RELAXED,
-                                                            __HIP_MEMORY_SCOPE_AGENT);
+      const bool won = expect == w && __hip_atomic_compare_exchange_strong(word, &expect, mine, __ATOMIC_RELAXED,
+                                                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       L.won_s = won ? 1 : 0;
       L.w_s = won ? mine : expect;
+      if ((PRISM_DBG(a) & 32) && blockIdx.x == 1) {  // measurement aid: when workgroup 1 left the election
+        a.plan_region[kPlanBuildStamps + 6] = static_cast<int>(__builtin_amdgcn_s_memrealtime() & 0x7FFFFFFF);
+        a.plan_region[kPlanBuildStamps + 7] = won ? 2 : (expect == w ? 1 : 0);
+      }
     }
     __syncthreads();
     const bool won = L.won_s != 0;
     const unsigned long long seen = L.w_s;
     __syncthreads();
     if (won) {
+      int* bs = a.plan_region + kPlanBuildStamps;  // measurement aid (bit 32): the builder's phases
+      auto stamp = [&](int k) {
+        if ((PRISM_DBG(a) & 32) && threadIdx.x == 0)
+          bs[k] = static_cast<int>(__builtin_amdgcn_s_memrealtime() & 0x7FFFFFFF);
+      };
+      stamp(0);
       plan_build<NT>(a, plan_slot(a, 1 - slot), L, tst_s);
+      stamp(1);
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");  // the slot reaches the device-coherent level
       __syncthreads();
+      stamp(2);
       if (threadIdx.x == 0)
         __hip_atomic_store(word, (static_cast<unsigned long long>(epoch) << 32) | static_cast<unsigned long long>(1 - slot),
                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if ((PRISM_DBG(a) & 32) && threadIdx.x == 0) bs[3] = static_cast<int>(blockIdx.x);
       return 1 - slot;
     }
     w = seen;  // another workgroup builds (or the word changed): wait for it, then check again
@@ -2081,7 +2120,8 @@ paged_decode_stream_kernel(const DecodeArgs a) {
       (PRISM_DBG(a) & 128) ? true : (!plan_building_here(w0, a.epoch) && plan_key_check<kSThreads>(a, plan, L));
   store_tstart();
   if (__builtin_expect(!__syncthreads_and(same ? 1 : 0), 0)) {
-    const int slot = __builtin_amdgcn_readfirstlane(plan_select_slow<kSThreads>(a, L, tstart, w0));
+    const bool staged = !(PRISM_DBG(a) & 128) && !plan_building_here(w0, a.epoch);  // the check above staged L
+    const int slot = __builtin_amdgcn_readfirstlane(plan_select_slow<kSThreads>(a, L, tstart, w0, staged));
     if (slot < 0) return;  // the builder never published (cannot happen: it waits for nobody)
     plan = plan_slot(a, slot);
     __syncthreads();  // every thread is done with the build's tstart before it is reloaded
