@@ -734,12 +734,16 @@ paged_decode_split_kernel(const DecodeArgs a) {
 #pragma unroll
       for (int q = 0; q < kU; ++q) {
         const int k = k0 + q * NG;
-        const int kk = k < n_live ? k : cg;  // past the end: re-read a live row, weighed 0
-        const int64_t row = hrow0 + static_cast<int64_t>(kk) * G + r;
-        const float2 ml = load_coherent2(ml_r, static_cast<uint32_t>(row * 8));
-        xv[q] = load_coherent4(acc_r, static_cast<uint32_t>((row * kHeadDim + d0) * 4));
-        mv[q] = k < n_live ? ml.x : -INFINITY;
-        lv[q] = k < n_live ? ml.y : 0.f;
+        // only live chunks are loaded (device-scope loads bypass the caches)
+        const int64_t row = hrow0 + static_cast<int64_t>(k) * G + r;
+        float2 ml = {-INFINITY, 0.f};
+        xv[q] = floatx4{0.f, 0.f, 0.f, 0.f};
+        if (k < n_live) {
+          ml = load_coherent2(ml_r, static_cast<uint32_t>(row * 8));
+          xv[q] = load_coherent4(acc_r, static_cast<uint32_t>((row * kHeadDim + d0) * 4));
+        }
+        mv[q] = ml.x;
+        lv[q] = ml.y;
       }
       float mx = m_acc;
 #pragma unroll
@@ -1200,7 +1204,8 @@ constexpr int kPlanHdrInts = 1024;
 constexpr int kPlanSlotInts = (kPlanInts + 1023) / 1024 * 1024;
 constexpr int kPlanMeasure = kPlanHdrInts + 2 * kPlanSlotInts;
 constexpr int kPlanBuildStamps = kPlanMeasure + 8 * kSMaxWg + 4 * kSMaxWg * kSKv;  // measurement aid: 16 ints
-constexpr int kPlanRegionInts = kPlanBuildStamps + 16;
+constexpr int kPlanMergeStamps = kPlanBuildStamps + 16;  // measurement aid: 4 ints per workgroup
+constexpr int kPlanRegionInts = kPlanMergeStamps + 4 * kSMaxWg;
 constexpr int kPlanMagic = 0x504C414E;
 static_assert(kPlanKeyBt % 4 == 0 && kPlanHdrInts % 4 == 0 && kPlanSlotInts % 4 == 0, "16-byte key reads");
 constexpr int kPlanThreads = 1024;
@@ -1858,7 +1863,7 @@ constexpr int kMergeRedOffset = 4096;  // floats: the merge's LDS scratch starts
 // record (first, end, virtual slot, virtual first, virtual end), stride 8.
 template <int QDT, int TPR>
 __device__ __forceinline__ void stream_merge_batch(const DecodeArgs& a, int V, const int* recs, int nb,
-                                                   const StreamSplit& sp, float* red) {
+                                                   const StreamSplit& sp, float* red, bool stamp = false) {
   constexpr int tl = 0;  // one partial per kv head and workgroup entry: the token slots met at the flush
   constexpr int hkv = kSKv / TPR;
   constexpr int kU = 8;
@@ -1927,16 +1932,26 @@ __device__ __forceinline__ void stream_merge_batch(const DecodeArgs& a, int V, c
           const int64_t w = (second ? lo1 : lo0) + wk;
           ok = ok && split_begin(sp, w) < split_begin(sp, w + 1);
         }
-        const float2 ml = load_coherent2(ml_r, static_cast<uint32_t>(row) * 8u);
-        const uint32_t off = (static_cast<uint32_t>(row) * kHeadDim + d0) * 4u;
-        x0[k] = load_coherent4(acc_r, off);
-        x1[k] = load_coherent4(acc_r, off + 16);
+        // only live candidates are loaded: these device-scope loads bypass
+        // the caches, and re-reading a live row for every unused candidate
+        // slot made a 2-candidate merge move 4x its bytes through one CU
+        float2 ml = {-INFINITY, 0.f};
+        x0[k] = floatx4{0.f, 0.f, 0.f, 0.f};
+        x1[k] = floatx4{0.f, 0.f, 0.f, 0.f};
+        if (base + k < mine) {
+          ml = load_coherent2(ml_r, static_cast<uint32_t>(row) * 8u);
+          const uint32_t off = (static_cast<uint32_t>(row) * kHeadDim + d0) * 4u;
+          x0[k] = load_coherent4(acc_r, off);
+          x1[k] = load_coherent4(acc_r, off + 16);
+        }
         mv[k] = ok ? ml.x : -INFINITY;
         lv[k] = ok ? ml.y : 0.f;
       }
       float mx = m_run;
 #pragma unroll
       for (int k = 0; k < kU; ++k) mx = fmaxf(mx, mv[k]);
+      if ((PRISM_DBG(a) & 32) && stamp && threadIdx.x == 0 && base == 0 && mx != 12345.f)  // measurement aid: loads back
+        a.plan_region[kPlanMergeStamps + 4 * blockIdx.x + 1] = static_cast<int>(__builtin_amdgcn_s_memrealtime() & 0x7FFFFFFF);
       if (mx == -INFINITY) continue;  // nothing attended so far
       const float alpha = exp2f(m_run - mx);  // 0 while m_run = -inf
       l_sum *= alpha;
@@ -1996,9 +2011,8 @@ __device__ __forceinline__ void stream_merge_batch(const DecodeArgs& a, int V, c
 // that attend no token at all (no tiles, no flushes) get zeros from
 // workgroup b % nwg.  `scratch` is LDS no longer in use (the drained stages).
 template <int QDT, int TPR>
-__device__ __forceinline__ void stream_finish(const DecodeArgs& a, int* plan, int V, const int* tstart, int e_first,
-                                              int nent,
-                                              int* scratch) {
+__device__ __forceinline__ void stream_finish(const DecodeArgs& a, int* plan, int V, int64_t total, const int* tstart,
+                                              int e_first, int nent, int* scratch) {
   constexpr int kRec = 5;
   int* n_merge = scratch;
   int* merge_rec = scratch + 4;  // per merged sequence: b, then its 5-int plan record (stride 8)
@@ -2048,14 +2062,16 @@ __device__ __forceinline__ void stream_finish(const DecodeArgs& a, int* plan, in
     d[4] = static_cast<int>(__builtin_amdgcn_s_memrealtime() & 0x7FFFFFFF);
   }
   if (nm == 0) return;
-  const StreamSplit sp = stream_split(a, plan[1]);
+  const StreamSplit sp = stream_split(a, total);  // (not re-read: a round trip on the kernel's tail)
   // merges in batches: as many at once as the workgroup has slots (one at a
   // time when the q heads fill the workgroup)
   const int units = a.num_heads * 16;
   const int slots = units >= kSThreads ? 1 : kSThreads / units;
   for (int k = 0; k < nm; k += slots) {
+    if ((PRISM_DBG(a) & 32) && k == 0 && threadIdx.x == 0)  // measurement aid: first batch starts
+      a.plan_region[kPlanMergeStamps + 4 * blockIdx.x] = static_cast<int>(__builtin_amdgcn_s_memrealtime() & 0x7FFFFFFF);
     stream_merge_batch<QDT, TPR>(a, V, merge_rec + 8 * k, min(slots, nm - k), sp,
-                                 reinterpret_cast<float*>(scratch) + kMergeRedOffset);
+                                 reinterpret_cast<float*>(scratch) + kMergeRedOffset, k == 0);
     if ((PRISM_DBG(a) & 32) && k == 0 && threadIdx.x == 0) {  // measurement aid: first batch done
       int* d = a.plan_region + kPlanMeasure + 8 * blockIdx.x;
       d[6] = static_cast<int>(__builtin_amdgcn_s_memrealtime() & 0x7FFFFFFF);
@@ -2135,7 +2151,7 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   const int64_t e = split_begin(sp, blockIdx.x + 1);
   __syncthreads();
   if (s >= e) {  // uniform: an empty range flushes nothing
-    stream_finish<QDT, TPR>(a, plan, V, tstart, 0, 0, reinterpret_cast<int*>(stages));
+    stream_finish<QDT, TPR>(a, plan, V, total, tstart, 0, 0, reinterpret_cast<int*>(stages));
     return;
   }
   const uint64_t t_begin = __builtin_amdgcn_s_memrealtime();
@@ -2496,7 +2512,7 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   // ---- completion: count this range's flushes, merge completed sequences
   __syncthreads();  // every wave is done with the stages (reused as scratch)
   const uint64_t t_loop = (PRISM_DBG(a) & (8 | 32)) ? __builtin_amdgcn_s_memrealtime() : 0;
-  stream_finish<QDT, TPR>(a, plan, V, tstart, __builtin_amdgcn_readfirstlane(wr0.x), b - wr0.x + 1,
+  stream_finish<QDT, TPR>(a, plan, V, total, tstart, __builtin_amdgcn_readfirstlane(wr0.x), b - wr0.x + 1,
                           reinterpret_cast<int*>(stages));
   if ((PRISM_DBG(a) & 32) && threadIdx.x == 0) {  // measurement aid: phase stamps (100 MHz clock)
     int* d = a.plan_region + kPlanMeasure + 8 * blockIdx.x;
