@@ -1228,12 +1228,27 @@ __device__ __forceinline__ StreamSplit stream_split(const DecodeArgs& a, int64_t
   return StreamSplit{total, a.stream_nwg};
 }
 
-__device__ __forceinline__ int64_t split_begin(const StreamSplit& sp, int64_t w) { return w * sp.total / sp.nwg; }
+// floor(x / d) for 0 <= x < 2^53, 0 < d < 2^53, through one fp64 division
+// and an exact correction (64-bit integer division is a long emulated
+// sequence; these run on the merge's critical path).  The operands convert to
+// fp64 exactly, so the correctly rounded quotient is at least floor(x / d)
+// and exceeds it by at most one.
+__device__ __forceinline__ int64_t div_floor_small(int64_t x, int64_t d) {
+  int64_t q = static_cast<int64_t>(static_cast<double>(x) / static_cast<double>(d));
+  q -= q * d > x ? 1 : 0;
+  q += (q + 1) * d <= x ? 1 : 0;
+  return q;
+}
+
+// (w * total < 2^41: total < 2^31 tiles, w <= nwg <= 1024)
+__device__ __forceinline__ int64_t split_begin(const StreamSplit& sp, int64_t w) {
+  return div_floor_small(w * sp.total, sp.nwg);
+}
 
 // The workgroup whose range holds tile t (0 <= t < total): the last w with
 // split_begin(w) <= t, i.e. ceil((t + 1) * nwg / total) - 1.
 __device__ __forceinline__ int64_t split_owner(const StreamSplit& sp, int64_t t) {
-  return ((t + 1) * sp.nwg + sp.total - 1) / sp.total - 1;
+  return div_floor_small((t + 1) * sp.nwg + sp.total - 1, sp.total) - 1;
 }
 
 // Number of streaming workgroups whose ranges meet tiles [first, end) of a
@@ -1968,6 +1983,8 @@ __device__ __forceinline__ void stream_merge_batch(const DecodeArgs& a, int V, c
         }
       }
       m_run = mx;
+      if ((PRISM_DBG(a) & 32) && stamp && threadIdx.x == 0 && base == 0 && o[7] != 12345.f)  // measurement aid: accumulated
+        a.plan_region[kPlanMergeStamps + 4 * blockIdx.x + 2] = static_cast<int>(__builtin_amdgcn_s_memrealtime() & 0x7FFFFFFF);
     }
     if (gpm > 1) {  // a sequence's slots meet in LDS; its slot 0 finishes the unit
       __syncthreads();  // `red` is free (the previous batch may still read it)
