@@ -2178,6 +2178,10 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   const int count = static_cast<int>(e - s);
   const int P = a.page_size;
   const int tpp = P / kTTok;  // tiles per page (the streaming shape has P % kTTok == 0)
+  // unit-scale FP8 caches (no scale tensors): every stage still issues its
+  // fifth load per lane -- the loop's waits count five -- from the tile's own
+  // K bytes (valid memory, a cache hit), and the scales read as 1
+  const bool unscaled = a.ks == nullptr;
   const float* sbase = pl.which ? a.vs : a.ks;  // wave-uniform: the scales this wave's lanes load
 
   // ---- issue side: walks this workgroup's tiles kSStages - 1 ahead of the
@@ -2205,7 +2209,7 @@ paged_decode_stream_kernel(const DecodeArgs a) {
     const int64_t tip_rows = static_cast<int64_t>(itip) * kSTile;
     ikb = a.k + blk * a.k_sblk + tip_rows * kSRow;
     ivb = a.v + blk * a.v_sblk + tip_rows * kSRow;
-    isb = sbase + blk * a.ks_sblk + tip_rows * kSKv;
+    isb = unscaled ? reinterpret_cast<const float*>(ikb) : sbase + blk * a.ks_sblk + tip_rows * kSKv;
   };
   auto ientry = [&](int lt, int first_raw) {
     intl = __builtin_amdgcn_readfirstlane(tstart[ie + 1] - tstart[ie]);
@@ -2337,8 +2341,12 @@ paged_decode_stream_kernel(const DecodeArgs a) {
       // ---- all LDS reads of the tile first, so their latencies overlap
       const u32x4 k0 = lds_load_b128(k_off0 + slot);
       const u32x4 k1 = lds_load_b128(k_off1 + slot);
-      const floatx4 ks = lds_load_f4(s_off + slot);
-      const floatx4 vs = lds_load_f4(s_off + slot + kSScaleBytes);
+      floatx4 ks = lds_load_f4(s_off + slot);
+      floatx4 vs = lds_load_f4(s_off + slot + kSScaleBytes);
+      if (unscaled) {  // uniform
+        ks = floatx4{1.f, 1.f, 1.f, 1.f};
+        vs = floatx4{1.f, 1.f, 1.f, 1.f};
+      }
       uint32_t ad[4];
 #pragma unroll
       for (int jp = 0; jp < 4; ++jp) ad[jp] = v_off[jp] + slot;
@@ -3052,15 +3060,17 @@ extern "C" int prism_paged_decode_stage(
   }
 #endif
   const bool page_aligned = (page_size % kTile) == 0;
-  // Streaming path: canonical contiguous page layout with scales.
+  // Streaming path: canonical contiguous page layout, with scales in the
+  // matching [block][token][head] layout or none (unit-scale FP8).
   // (token rows of num_kv_heads * 128 bytes, contiguous within a page)
   const int64_t tok_bytes = static_cast<int64_t>(num_kv_heads) * kHeadDim;
-  const bool use_stream = geo.fast && geo.stream_shape && k_scale != nullptr && k_strides[1] == tok_bytes &&
-                          k_strides[2] == kHeadDim && v_strides[1] == tok_bytes && v_strides[2] == kHeadDim &&
-                          ks_strides[1] == num_kv_heads && ks_strides[2] == 1 && vs_strides[1] == num_kv_heads &&
-                          vs_strides[2] == 1 &&
-                          ks_strides[0] == vs_strides[0] && aligned(k_scale, 16) && aligned(v_scale, 16) &&
-                          ks_strides[0] % 4 == 0;
+  const bool scale_layout = k_scale == nullptr ||
+                            (ks_strides[1] == num_kv_heads && ks_strides[2] == 1 && vs_strides[1] == num_kv_heads &&
+                             vs_strides[2] == 1 && ks_strides[0] == vs_strides[0] && aligned(k_scale, 16) &&
+                             aligned(v_scale, 16) && ks_strides[0] % 4 == 0);
+  const bool use_stream = geo.fast && geo.stream_shape && k_strides[1] == tok_bytes && k_strides[2] == kHeadDim &&
+                          v_strides[1] == tok_bytes && v_strides[2] == kHeadDim &&
+                          scale_layout;
   if (use_stream) {
     args.plan_region = static_cast<int*>(workspace);
     args.epoch = next_split_epoch();

@@ -191,6 +191,27 @@ def test_unit_scale_fp8_fast_path():
     assert_decode_close(got, _oracle(q, k, v, None, None, tables, lens, 128 ** -0.5), label="unit fp8 fast")
 
 
+def test_unit_scale_fp8_streaming_path():
+    """Unit-scale FP8 caches (no scale tensors) on the streaming kernel: ragged
+    lengths, a hole, and a prefix group (virtual entries) against the oracle
+    with unit scales."""
+
+    require_gpu()
+    g = torch.Generator().manual_seed(22)
+    batch, width, pool = 12, 16, 200
+    q = torch.randn(batch, 32, 128, generator=g).to(torch.bfloat16)
+    k = torch.randn(pool, 256, 8, 128, generator=g).to(FP8)
+    v = torch.randn(pool, 256, 8, 128, generator=g).to(FP8)
+    tables = torch.randperm(pool, generator=g)[: batch * width].to(torch.int32).view(batch, width).clone()
+    tables[1:9:2, :3] = tables[0, :3]  # a group of 5 sharing 3 pages
+    tables[10, 2] = -1
+    lens = torch.randint(800, width * 256, (batch,), generator=g, dtype=torch.int32)
+    lens[0] = width * 256
+    set_decode_overrides(path="stream")
+    got = _decode_gpu(q, k, v, None, None, tables, lens, 128 ** -0.5)
+    assert_decode_close(got, _oracle(q, k, v, None, None, tables, lens, 128 ** -0.5), label="unit fp8 stream")
+
+
 @pytest.mark.parametrize("name", ["decode_single", "decode_qwen_vl"])
 def test_single_sequence_configs(name):
     require_gpu()
