@@ -2112,7 +2112,7 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   const int B = a.batch;
   const uint64_t r_entry = (PRISM_DBG(a) & 32) ? __builtin_amdgcn_s_memrealtime() : 0;
 
-  // ---- the plan.  Round 1: the plan word.  Round 2: from the slot it names,
+  // ---- the plan.  First load: the plan word.  Then, together: from the slot it names,
   // this workgroup's start record, the plan header, the tile prefix sums
   // (virtual sequences, then real ones; copied up to the largest possible
   // entry count, so that these loads need not wait for V) and the key, which
