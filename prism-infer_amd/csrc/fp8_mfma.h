@@ -120,4 +120,32 @@ __device__ __forceinline__ shortx4 fp8x4_to_bf16x4_bits(uint32_t w) {
   return __builtin_bit_cast(shortx4, r);
 }
 
+// Four fp32 values -> NT E4M3FN terms per value (largest first; one packed
+// dword per term), each the round-to-nearest of what the previous terms
+// left: four significant bits per term.  The fp8 MFMA's products of these
+// with fp8 operands are exact in fp32, so the sum over the terms carries y.
+// Every term lies on E4M3FN's grid, whose finest step is the subnormal
+// 2^-9: whatever the number of terms, the error per value is at most 2^-10
+// once the remainder falls below the normal range, and zero before.
+template <int NT>
+__device__ __forceinline__ void fp8_split(const float (&y)[4], uint32_t (&out)[NT]) {
+  float r[4] = {y[0], y[1], y[2], y[3]};
+#pragma unroll
+  for (int t = 0; t < NT; ++t) {
+    int w = __builtin_amdgcn_cvt_pk_fp8_f32(r[0], r[1], 0, false);
+    w = __builtin_amdgcn_cvt_pk_fp8_f32(r[2], r[3], w, true);
+    out[t] = static_cast<uint32_t>(w);
+    if (t + 1 < NT) {
+      const floatx2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
+      const floatx2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(w, true);
+      r[0] -= lo[0];
+      r[1] -= lo[1];
+      r[2] -= hi[0];
+      r[3] -= hi[1];
+    }
+  }
+}
+
+__device__ __forceinline__ void fp8_split3(const float (&y)[4], uint32_t (&out)[3]) { fp8_split<3>(y, out); }
+
 }  // namespace prism

@@ -1049,24 +1049,6 @@ struct QOperandF8 {
   float colscale;  // scale_log2 * 2^-e of this lane's column
 };
 
-__device__ __forceinline__ void fp8_split3(const float (&y)[4], uint32_t (&out)[3]) {
-  float r[4] = {y[0], y[1], y[2], y[3]};
-#pragma unroll
-  for (int t = 0; t < 3; ++t) {
-    int w = __builtin_amdgcn_cvt_pk_fp8_f32(r[0], r[1], 0, false);
-    w = __builtin_amdgcn_cvt_pk_fp8_f32(r[2], r[3], w, true);
-    out[t] = static_cast<uint32_t>(w);
-    if (t < 2) {
-      const floatx2 lo = __builtin_amdgcn_cvt_pk_f32_fp8(w, false);
-      const floatx2 hi = __builtin_amdgcn_cvt_pk_f32_fp8(w, true);
-      r[0] -= lo[0];
-      r[1] -= lo[1];
-      r[2] -= hi[0];
-      r[3] -= hi[1];
-    }
-  }
-}
-
 template <int QDT, bool QVEC>
 __device__ __forceinline__ void stream_load_q8(const DecodeArgs& a, int qrow, int qhead, bool qvalid, int g,
                                                QOperandF8& qop) {

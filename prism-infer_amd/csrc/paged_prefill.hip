@@ -13,8 +13,10 @@
 // so each K/V tile is read once into LDS for all of them.  Tiles of KT keys
 // (one page holds whole tiles) are double buffered through LDS: the next
 // tile's loads are in flight while the current one is computed.  Per
-// 16-key sub-block, a wave computes S^T = K Q^T with
-// v_mfma_f32_16x16x32_{bf16,f16} (fp8 -> bf16/f16 is exact; the key scale
+// 16-key sub-block, a wave computes S^T = K Q^T (bf16 queries: the fp8 MFMA
+// 16x16x128 on the K bytes as they are, the query split into two fp8 terms
+// that hold it exactly, products exact in fp32; f16 queries:
+// v_mfma_f32_16x16x32_f16 on K converted to f16, exact; the key scale
 // multiplies the rows of S^T), runs the online softmax per query column
 // (log2 domain, lazy rescaling), and accumulates O^T += V^T P^T with
 // v_mfma_f32_16x16x32_bf16 (v_mfma_f32_16x16x16_bf16 for 16-key steps), V^T
@@ -129,11 +131,74 @@ __device__ bool locate(const PrefillArgs& a, int& seq, int& qblock) {
   return false;
 }
 
+// Query operand (B of S^T = K Q^T); lane (g, c) holds query column c's
+// dims 32g..32g+31, the same dims as the K bytes it meets (row c of the
+// block, LDS chunks 2g and 2g + 1); `mul` turns the column's scores into
+// log2 units.
+//
+// bf16 queries: the fp8 MFMA (16x16x128) on the K bytes as they are.  The
+// column is scaled by 2^e so that its largest |q| lies in [128, 256) and
+// split into two E4M3FN terms (hi, lo).  A bf16 value there is M * 2^k with
+// an 8-bit M; hi rounds it to 4 significant bits, which leaves
+// (M - 16 H) * 2^k with |M - 16 H| <= 8: at most 4 significant bits, held
+// exactly by lo whenever 2^k is on E4M3FN's grid (elements of 2^-2 and up,
+// 2^-10 of the column's largest), and within 2^-10 below (2^-18 of the
+// largest), as a third term would be.  The score is (K . (hi + lo)) * 2^-e;
+// 2^-e joins the softmax scale in `mul`.
+//
+// f16 queries (11 bits, which two terms do not hold): K converted to f16 per
+// block (exact) and v_mfma_f32_16x16x32_f16.
 template <int QDT>
 struct PfQOperand {
-  using T = typename std::conditional<QDT == PRISM_DTYPE_F16, f16x8, bf16x8>::type;
-  T op[4];
+  i32x8 t[2];  // hi, lo
+  float mul;   // scale_log2 * 2^-e of this lane's column
 };
+
+template <>
+struct PfQOperand<PRISM_DTYPE_F16> {
+  f16x8 op[4];
+  float mul;  // scale_log2
+};
+
+template <int QDT>
+__device__ __forceinline__ void pf_load_q(const uint16_t* src, bool valid, float scale_log2, PfQOperand<QDT>& q) {
+  if constexpr (QDT == PRISM_DTYPE_F16) {
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+      const u32x4 w = valid ? *reinterpret_cast<const u32x4*>(src + 8 * cc) : u32x4{0u, 0u, 0u, 0u};
+      q.op[cc] = __builtin_bit_cast(f16x8, w);
+    }
+    q.mul = scale_log2;
+  } else {
+    float x[32];
+#pragma unroll
+    for (int cc = 0; cc < 4; ++cc) {
+      const u32x4 w = valid ? *reinterpret_cast<const u32x4*>(src + 8 * cc) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        x[8 * cc + 2 * e] = bf16_bits_to_f32(w[e] & 0xFFFFu);
+        x[8 * cc + 2 * e + 1] = bf16_bits_to_f32(w[e] >> 16);
+      }
+    }
+    float mx = 0.f;
+#pragma unroll
+    for (int e = 0; e < 32; ++e) mx = fmaxf(mx, fabsf(x[e]));
+    mx = wave_max_across_groups(mx);
+    // ilogb(mx) = frexp exponent - 1; clamped so that 2^-e stays a normal
+    // fp32 number (columns of zeros, or of non-finite values, keep e = 0)
+    const int e = (mx > 0.f && mx <= 3.0e38f) ? min(max(8 - __builtin_amdgcn_frexp_expf(mx), -120), 120) : 0;
+    q.mul = ldexpf(scale_log2, -e);
+#pragma unroll
+    for (int w = 0; w < 8; ++w) {
+      const float y[4] = {ldexpf(x[4 * w], e), ldexpf(x[4 * w + 1], e), ldexpf(x[4 * w + 2], e),
+                          ldexpf(x[4 * w + 3], e)};
+      uint32_t parts[2];
+      fp8_split<2>(y, parts);
+      q.t[0][w] = static_cast<int>(parts[0]);
+      q.t[1][w] = static_cast<int>(parts[1]);
+    }
+  }
+}
 
 // Two waves per SIMD: at most 256 VGPRs + AGPRs per lane.
 template <int QDT, int KT, int NW, bool SCALED>
@@ -181,11 +246,7 @@ paged_prefill_kernel(const PrefillArgs a) {
     colv[cb] = j < qlen;
     const uint16_t* src = static_cast<const uint16_t*>(a.q) + static_cast<int64_t>(qs + (colv[cb] ? j : 0)) * a.q_st +
                           static_cast<int64_t>(qhead) * a.q_sh + 32 * g;
-#pragma unroll
-    for (int cc = 0; cc < 4; ++cc) {
-      u32x4 w = colv[cb] ? *reinterpret_cast<const u32x4*>(src + 8 * cc) : u32x4{0u, 0u, 0u, 0u};
-      qop[cb].op[cc] = __builtin_bit_cast(typename PfQOperand<QDT>::T, w);
-    }
+    pf_load_q<QDT>(src, colv[cb], a.scale_log2, qop[cb]);
   }
 
   // ---- tile loads, straight into LDS (load-to-LDS, 16 B per lane): K then
@@ -338,28 +399,38 @@ paged_prefill_kernel(const PrefillArgs a) {
             for (int jp = 0; jp < 4; ++jp) vt[b][jp] &= keep2;
           }
         }
-        // S^T = K Q^T for both column blocks, one K block at a time (its
-        // operand converted once)
-        floatx4 sc[kPfColBlocks][NB];  // the four per block chained: NB x 2 independent chains
+        // S^T = K Q^T for both column blocks, NB x 2 independent chains
+        floatx4 sc[kPfColBlocks][NB];
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
-          typename PfQOperand<QDT>::T kop[4];
-#pragma unroll
-          for (int cc = 0; cc < 4; ++cc) {
-            const u32x4& w = kw[b][cc >> 1];
-            if constexpr (QDT == PRISM_DTYPE_F16) kop[cc] = fp8x8_to_f16x8(w[(cc & 1) * 2], w[(cc & 1) * 2 + 1]);
-            else kop[cc] = fp8x8_to_bf16x8(w[(cc & 1) * 2], w[(cc & 1) * 2 + 1]);
-          }
-#pragma unroll
-          for (int cb = 0; cb < kPfColBlocks; ++cb) {
-            sc[cb][b] = floatx4{0.f, 0.f, 0.f, 0.f};
+          if constexpr (QDT == PRISM_DTYPE_F16) {
+            // K converted once per block for both column blocks
+            f16x8 kop[4];
 #pragma unroll
             for (int cc = 0; cc < 4; ++cc) {
-              floatx4& d = sc[cb][b];
-              if constexpr (QDT == PRISM_DTYPE_F16)
-                d = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[cc], qop[cb].op[cc], d, 0, 0, 0);
-              else
-                d = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[cc], qop[cb].op[cc], d, 0, 0, 0);
+              const u32x4& w = kw[b][cc >> 1];
+              kop[cc] = fp8x8_to_f16x8(w[(cc & 1) * 2], w[(cc & 1) * 2 + 1]);
+            }
+#pragma unroll
+            for (int cb = 0; cb < kPfColBlocks; ++cb) {
+              floatx4 d = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+              for (int cc = 0; cc < 4; ++cc) d = __builtin_amdgcn_mfma_f32_16x16x32_f16(kop[cc], qop[cb].op[cc], d, 0, 0, 0);
+              sc[cb][b] = d;
+            }
+          } else {
+            // the K bytes are the fp8 MFMA's A operand as they are (row =
+            // key c of the block, k = dims 32g..32g+31); smaller term first
+            const i32x8 ka = {static_cast<int>(kw[b][0][0]), static_cast<int>(kw[b][0][1]),
+                              static_cast<int>(kw[b][0][2]), static_cast<int>(kw[b][0][3]),
+                              static_cast<int>(kw[b][1][0]), static_cast<int>(kw[b][1][1]),
+                              static_cast<int>(kw[b][1][2]), static_cast<int>(kw[b][1][3])};
+#pragma unroll
+            for (int cb = 0; cb < kPfColBlocks; ++cb) {
+              floatx4 d = {0.f, 0.f, 0.f, 0.f};
+              d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, qop[cb].t[1], d, 0, 0, 0, 0, 0, 0);
+              d = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, qop[cb].t[0], d, 0, 0, 0, 0, 0, 0);
+              sc[cb][b] = d;
             }
           }
         }
@@ -399,7 +470,7 @@ paged_prefill_kernel(const PrefillArgs a) {
         for (int cb = 0; cb < kPfColBlocks; ++cb) {
           float t = fmaxf(fmaxf(x[cb][0][0], x[cb][0][1]), fmaxf(x[cb][0][2], x[cb][0][3]));
           if constexpr (NB == 2) t = fmaxf(t, fmaxf(fmaxf(x[cb][1][0], x[cb][1][1]), fmaxf(x[cb][1][2], x[cb][1][3])));
-          tmax[cb] = wave_max_across_groups(t) * a.scale_log2;  // log2 units (the scale is positive)
+          tmax[cb] = wave_max_across_groups(t) * qop[cb].mul;  // log2 units (the multiplier is positive)
           raise[cb] = tmax[cb] > m_run[cb] + kPfRescaleThreshold;
         }
         if (__builtin_amdgcn_ballot_w64(raise[0] || raise[1]) != 0) {
@@ -434,7 +505,7 @@ paged_prefill_kernel(const PrefillArgs a) {
             for (int i = 0; i < 4; ++i) {
               // v_exp_f32: arguments are at most 2^3 above the running max;
               // results below 2^-126 (flushed to 0) weigh nothing next to it
-              p[b][i] = __builtin_amdgcn_exp2f(fmaf(x[cb][b][i], a.scale_log2, -m_use));  // 0 where masked
+              p[b][i] = __builtin_amdgcn_exp2f(fmaf(x[cb][b][i], qop[cb].mul, -m_use));  // 0 where masked
               if constexpr (NB == 2) pa[cb][4 * b + i] = static_cast<__bf16>(p[b][i] * vsv[b][i]);
               else pa[cb][4 * b + i] = __builtin_bit_cast(short, static_cast<__bf16>(p[b][i] * vsv[b][i]));
             }
