@@ -821,7 +821,8 @@ paged_decode_split_kernel(const DecodeArgs a) {
 //   V reads spread over the banks.
 //   Scales are stored [head][token] so a lane's four tokens are one 16-byte read.
 // * QK: MFMA f32_16x16x128_f8f6f4 on the fp8 K rows as they are (B = Q^T
-//   split into three fp8 terms whose sum carries q's bf16 value; 16 query
+//   split into fp8 terms whose sum carries q's value, two for bf16
+//   queries and three for f16/f32; 16 query
 //   columns: the G heads of one sequence, or of up to 16/G sequences for a
 //   virtual sequence).  Lane (g, c) gets the scores of query column c for
 //   tokens 4g..4g+3.
@@ -1038,12 +1039,14 @@ __device__ __forceinline__ void stream_load_q(const DecodeArgs& a, int qrow, int
 // (g, c) holds column c's dims 32g..32g+31 as fp8 bytes, the same bytes of
 // the K rows it multiplies.  Each column is scaled by 2^e so that its
 // largest |q| lies in [128, 256), then split into three E4M3FN terms,
-// hi + mid + lo, each the round-to-nearest of what the previous terms left:
-// four significant bits per term, so a bf16 query (eight bits) is
-// represented exactly except for elements below 2^-9 after scaling (at most
-// 2^-17 of the column's largest), and f16/f32 queries to about 2^-12
-// relative.  The score is then (K . (hi + mid + lo)) * 2^-e, and 2^-e is
-// folded into the per-column score multiplier.
+// hi + mid + lo, each the round-to-nearest of what the previous terms left
+// (four significant bits per term).  A bf16 query (eight bits) is held
+// exactly by hi + mid for elements of 2^-2 and up after scaling (2^-10 of
+// the column's largest) and within 2^-10 below (2^-18 of the largest); its
+// lo term is then zero, so the kernel skips that MFMA for bf16 queries.  An
+// f16 query is held exactly from 2 up and within 2^-10 below, an f32 query
+// to about 2^-12 relative.  The score is then (K . (hi + mid + lo)) * 2^-e,
+// and 2^-e is folded into the per-column score multiplier.
 struct QOperandF8 {
   i32x8 t[3];      // hi, mid, lo
   float colscale;  // scale_log2 * 2^-e of this lane's column
@@ -2340,7 +2343,10 @@ paged_decode_stream_kernel(const DecodeArgs a) {
                         static_cast<int>(k0[3]), static_cast<int>(k1[0]), static_cast<int>(k1[1]),
                         static_cast<int>(k1[2]), static_cast<int>(k1[3])};
       floatx4 sc = {0.f, 0.f, 0.f, 0.f};
-      sc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, qop.t[2], sc, 0, 0, 0, 0, 0, 0);
+      // (a bf16 query's third term is zero: two terms hold every bf16 value
+      // the fp8 grid can, and the third only refines f16/f32 queries)
+      if constexpr (QDT != PRISM_DTYPE_BF16)
+        sc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, qop.t[2], sc, 0, 0, 0, 0, 0, 0);
       sc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, qop.t[1], sc, 0, 0, 0, 0, 0, 0);
       sc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, qop.t[0], sc, 0, 0, 0, 0, 0, 0);
       // ---- scores in the log2 domain.  Query columns without a query hold

@@ -136,8 +136,9 @@ def test_query_magnitudes_per_head(qdtype, lo_exp, hi_exp, decode_path):
     """Query heads spanning many orders of magnitude, plus an all-zero head.
 
     The streaming kernel scales each query column by a power of two and splits
-    it into three fp8 terms for the QK MFMA: tiny heads (near-uniform softmax),
-    huge heads (near one-hot) and a zero head exercise that scaling.
+    it into fp8 terms for the QK MFMA (two for bf16, three for f16/f32): tiny
+    heads (near-uniform softmax), huge heads (near one-hot) and a zero head
+    exercise that scaling.
     """
 
     require_gpu()
