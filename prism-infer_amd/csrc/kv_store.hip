@@ -74,8 +74,10 @@ __device__ __forceinline__ float load_scalar(const void* base, int dtype, int64_
   return dtype == PRISM_DTYPE_BF16 ? bf16_bits_to_f32(bits) : f16_bits_to_f32(bits);
 }
 
-// Four finite values in [-448, 448] -> E4M3FN bytes (the native RNE
-// conversion; fp8_encode4's NaN and overflow handling cannot apply).
+// Four finite values of magnitude at most 448 (1 + 2^-22) -> E4M3FN bytes
+// (the native RNE conversion, which saturates: values above 448 and below
+// 464 give 448 either way; fp8_encode4's NaN and overflow handling cannot
+// apply).
 __device__ __forceinline__ uint32_t fp8_cvt4_in_range(float a, float b, float c, float d) {
   const int lo = __builtin_amdgcn_cvt_pk_fp8_f32(a, b, 0, false);
   return static_cast<uint32_t>(__builtin_amdgcn_cvt_pk_fp8_f32(c, d, lo, true));
@@ -86,15 +88,19 @@ __device__ __forceinline__ uint32_t fp8_cvt4_in_range(float a, float b, float c,
 // quotient, as IEEE division gives it.
 //
 // One division per row gives y = RN(1 / s).  Per element, q0 = RN(x * y) is
-// within one ulp of x / s, so the residual e = x - q0 * s is exact in fp32
-// and one fused step q = RN(q0 + e * y) is the correctly rounded quotient
+// within one ulp of x / s, so the residual e' = q0 * s - x is exact in fp32
+// and one fused step q = RN(q0 - e' * y) is the correctly rounded quotient
 // (Markstein's theorem on division by a correctly rounded reciprocal).  The
-// quotients here are at most 448 in magnitude and s >= 1e-6, so nothing
-// overflows; a quotient below 2^-126 may lose the theorem's guarantee but
-// keeps its sign and is far below 2^-10, so its fp8 byte (a signed zero) is
-// unaffected.  The sign is taken from x, as the division gives it for
-// zeros too.  Rows whose scale is infinite or NaN (an infinite or NaN
-// element) take the division itself.
+// quotients here are at most 448 (1 + 2^-22) in magnitude and s >= 1e-6, so
+// nothing overflows; a quotient below 2^-126 may lose the theorem's
+// guarantee but keeps its sign and is far below 2^-10, so its fp8 byte (a
+// signed zero) is unaffected.  Signs of zeros: x = -0 gives q0 = -0,
+// e' = -0 * s + 0 = +0 and q = -0 - (+0 * y) = -0; x = +0 gives +0 (with the
+// residual of the other sign, x - q0 * s, the sum of opposite zeros would
+// round -0 up to +0).  No clamp: s is amax / 448 rounded (or the 1e-6 floor
+// above it), so |x / s| <= 448 (1 + 2^-22), which the native conversion
+// rounds to 448 like the clamped value.  Rows whose scale is infinite or
+// NaN (an infinite or NaN element) take the division itself.
 __device__ __forceinline__ u32x2 quantize8(const float (&x)[8], float s) {
   float q[8];
   if (s < 0x1p125f) {
@@ -102,10 +108,8 @@ __device__ __forceinline__ u32x2 quantize8(const float (&x)[8], float s) {
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
       const float q0 = x[i] * y;
-      const float e = __builtin_fmaf(-q0, s, x[i]);
-      // s > 0: the quotient has x's sign, which the fused step loses for
-      // x = -0 (-0 + +0 rounds to +0).
-      q[i] = __builtin_amdgcn_fmed3f(__builtin_copysignf(__builtin_fmaf(e, y, q0), x[i]), -kFp8Max, kFp8Max);
+      const float en = __builtin_fmaf(q0, s, -x[i]);
+      q[i] = __builtin_fmaf(-en, y, q0);
     }
     u32x2 out;
     out[0] = fp8_cvt4_in_range(q[0], q[1], q[2], q[3]);
