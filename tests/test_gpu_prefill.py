@@ -123,6 +123,30 @@ def test_prefill_unit_scale_and_f16_queries():
     _check(_case(20260814, [(40, 129), (70, 70)], qdtype=torch.float16), "f16 q")
 
 
+@pytest.mark.parametrize("qdtype", [torch.bfloat16, torch.float16])
+def test_prefill_query_magnitudes_per_head(qdtype):
+    """Query heads over many orders of magnitude, an all-zero head, and a head
+    whose elements spread from 2^-20 to 1 of each row's largest.
+
+    bf16 queries reach the QK MFMA as two fp8 terms of the column scaled so
+    that its largest |q| lies in [128, 256): the per-column power of two and
+    the elements far below the largest (below 2^-10 of it, where the second
+    term's fp8 grid no longer holds them exactly) are what these heads
+    exercise; f16 queries take the 16-bit MFMA on the same data.
+    """
+
+    require_gpu()
+    c = _case(20261203, [(40, 600), (70, 70)], qdtype=qdtype)
+    g = torch.Generator().manual_seed(7)
+    q = c["q"].float()
+    tokens, heads, dim = q.shape
+    q = q * torch.exp2(torch.empty(heads).uniform_(-6.0, 4.0, generator=g)).view(1, heads, 1)
+    q[:, 3] = 0.0
+    q[:, 5] = torch.where(q[:, 5] < 0, -1.0, 1.0) * torch.exp2(-20.0 * torch.rand(tokens, dim, generator=g)) * 4.0
+    c["q"] = q.to(qdtype)
+    _check(c, f"query magnitudes {qdtype}")
+
+
 def test_prefill_large_v_scales_and_packed_qkv_view():
     """v scales in the thousands (P * v_scale far above f16's range, held by
     the bf16 PV operand); q is a strided view of a packed QKV projection."""
