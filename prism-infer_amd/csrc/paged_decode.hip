@@ -126,6 +126,32 @@ __device__ __forceinline__ void store_out(void* out, int64_t idx, float v) {
 }
 
 
+// Eight consecutive dims of one output row, o[j] * inv at idx + j * o_sd.
+// 16-bit outputs with unit dim stride and a 16-byte aligned address take one
+// 16-byte store (the same conversion per element) instead of eight 2-byte
+// stores with their 64-bit address arithmetic; anything else is stored
+// element by element.
+template <int QDT, typename Args>
+__device__ __forceinline__ void store_out8(const Args& a, int64_t idx, const float (&o)[8], float inv) {
+  if constexpr (QDT != PRISM_DTYPE_F32) {
+    uint16_t* p = static_cast<uint16_t*>(a.out) + idx;
+    if (a.o_sd == 1 && (reinterpret_cast<uintptr_t>(p) & 15u) == 0) {
+      u32x4 w;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const float lo = o[2 * j] * inv, hi = o[2 * j + 1] * inv;
+        const uint32_t blo = QDT == PRISM_DTYPE_BF16 ? f32_to_bf16_bits(lo) : f32_to_f16_bits(lo);
+        const uint32_t bhi = QDT == PRISM_DTYPE_BF16 ? f32_to_bf16_bits(hi) : f32_to_f16_bits(hi);
+        w[j] = blo | (bhi << 16);
+      }
+      *reinterpret_cast<u32x4*>(p) = w;
+      return;
+    }
+  }
+#pragma unroll
+  for (int j = 0; j < 8; ++j) store_out<QDT>(a.out, idx + j * a.o_sd, o[j] * inv);
+}
+
 struct TileRegs {
   u32x4 k[2][2];   // [half][part]: 32 bytes of K row (c + 16 * half), dims 32g..32g+31
   u32x2 v[8];      // V rows of tokens {4g+i, 16+4g+i}, dims 8c..8c+7
@@ -2000,8 +2026,7 @@ __device__ __forceinline__ void stream_merge_batch(const DecodeArgs& a, int V, c
     }
     const float inv = l_sum > 0.f ? 1.f / l_sum : 0.f;
     const int64_t obase = static_cast<int64_t>(b) * a.o_sb + static_cast<int64_t>(hq) * a.o_sh;
-#pragma unroll
-    for (int j = 0; j < 8; ++j) store_out<QDT>(a.out, obase + (d0 + j) * a.o_sd, o[j] * inv);
+    store_out8<QDT>(a, obase + d0 * a.o_sd, o, inv);
   }
 }
 
