@@ -269,7 +269,7 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a GPU", file=sys.stderr)
         return 1
-    _native.lib()
+    _native.device_lib(torch.device("cuda", 0))
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     if args.copy_probe:

@@ -199,6 +199,19 @@ int prism_paged_decode_set_overrides(int path, int split_tokens, int share);
 void prism_paged_decode_get_overrides(int out[3]);
 
 /*
+ * Test hook of the streaming decode kernel's plan wait (no counterpart in the
+ * reference).  A workgroup that waits for another workgroup's plan build
+ * gives up after `polls` polls (default prism_paged_decode_default_plan_wait_limit(),
+ * far beyond any build); it then writes NaN to the call's output rows and
+ * counts the give-up in the workspace's plan header, which makes the next
+ * call rebuild the plan.  Setting 0 makes every waiting workgroup give up at
+ * once, so the path can be exercised from the host with kernels that all
+ * exit normally.  Returns the previous limit, or -1 for polls < 0.
+ */
+int prism_paged_decode_set_plan_wait_limit(int polls);
+int prism_paged_decode_default_plan_wait_limit(void);
+
+/*
  * Physical slot compaction.  Replaces the kernels behind
  *   compact_kv_slots(cache, source_slots, destination_slots)
  *   (prism_infer/ops/kv_compaction.py:93-112; gather/scatter kernels :33-86).

@@ -93,6 +93,7 @@ struct DecodeArgs {
   // (16 rows); the streaming and merge kernels take the former as a template
   // parameter, the plan code reads both
   int s_tpr, s_ttok;
+  int plan_spin;  // streaming path: polls a workgroup waits for a plan build before it gives up
 };
 
 // Read-only int32 metadata (block tables, context lengths) through the
@@ -1700,6 +1701,15 @@ __device__ void plan_build(const DecodeArgs& a, int* plan, PlanLds& L, int* tst_
 // writes visible on every XCD.
 constexpr unsigned long long kPlanBuilding = 2;
 constexpr int kPlanSpinLimit = 1 << 22;  // polls of a waiting workgroup (far beyond any build)
+// Give-up count, one int of the plan header (kPlanGiveUps): how many
+// workgroups abandoned a launch because a plan build they waited for did not
+// appear within the poll limit.  Such a launch leaves the completion counters
+// of the slot it used part-way (its flushes are missing), so while the count
+// is nonzero every launch treats the plan as stale: it rebuilds (which zeroes
+// the counters) and the builder resets the count to the value it read at the
+// start of its launch, with a compare-exchange, so that a give-up of the same
+// launch keeps the count nonzero for the next one.
+constexpr int kPlanGiveUps = 2;
 
 __device__ __forceinline__ unsigned long long* plan_word(const DecodeArgs& a) {
   return reinterpret_cast<unsigned long long*>(a.plan_region);
@@ -1725,14 +1735,14 @@ __device__ __forceinline__ bool plan_building_here(unsigned long long w, unsigne
 // attempt goes straight to the election).
 template <int NT>
 __device__ int plan_select_slow(const DecodeArgs& a, PlanLds& L, int* tst_s, unsigned long long w,
-                                bool staged = false) {
+                                bool staged = false, unsigned int give_ups = 0) {
   unsigned long long* word = plan_word(a);
   const unsigned int epoch = a.epoch;
   for (int attempt = 0; attempt < 4; ++attempt) {
     if (plan_building_here(w, epoch)) {
       if (threadIdx.x == 0) {
         unsigned long long x = w;
-        for (int n = 0; n < kPlanSpinLimit && plan_building_here(x, epoch); ++n) {
+        for (int n = 0; n < a.plan_spin && plan_building_here(x, epoch); ++n) {
           __builtin_amdgcn_s_sleep(4);
           x = __hip_atomic_load(word, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
@@ -1753,7 +1763,8 @@ __device__ int plan_select_slow(const DecodeArgs& a, PlanLds& L, int* tst_s, uns
       if (static_cast<unsigned int>(w >> 32) == epoch) return static_cast<int>(w & 1);
     }
     const int slot = static_cast<int>(w & 1);
-    if (!(staged && attempt == 0)) {
+    // a nonzero give-up count makes the slot the word names stale whatever its key
+    if (!(staged && attempt == 0) && !(give_ups != 0 && attempt == 0)) {
       const bool same = plan_key_check<NT>(a, plan_slot(a, slot), L);
       if (__syncthreads_and(same ? 1 : 0)) return slot;
     }
@@ -1795,6 +1806,11 @@ __device__ int plan_select_slow(const DecodeArgs& a, PlanLds& L, int* tst_s, uns
       stamp(0);
       plan_build<NT>(a, plan_slot(a, 1 - slot), L, tst_s);
       stamp(1);
+      if (threadIdx.x == 0 && give_ups != 0) {
+        unsigned int seen_gu = give_ups;
+        __hip_atomic_compare_exchange_strong(reinterpret_cast<unsigned int*>(a.plan_region) + kPlanGiveUps, &seen_gu,
+                                             0u, __ATOMIC_RELAXED, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
       __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");  // the slot reaches the device-coherent level
       __syncthreads();
       stamp(2);
@@ -1814,11 +1830,16 @@ __device__ int plan_select_slow(const DecodeArgs& a, PlanLds& L, int* tst_s, uns
 __global__ void __launch_bounds__(kPlanThreads) paged_decode_stream_plan_kernel(const DecodeArgs a) {
   __shared__ PlanLds L;
   __shared__ int tst_s[kSMaxBatch + kSMaxVirt + 1];
-  if (threadIdx.x == 0) L.w_s = __hip_atomic_load(plan_word(a), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (threadIdx.x == 0) {
+    L.w_s = __hip_atomic_load(plan_word(a), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    L.won_s = static_cast<int>(__hip_atomic_load(reinterpret_cast<unsigned int*>(a.plan_region) + kPlanGiveUps,
+                                                 __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT));
+  }
   __syncthreads();
   const unsigned long long w = L.w_s;
+  const unsigned int give_ups = static_cast<unsigned int>(L.won_s);
   __syncthreads();
-  plan_select_slow<kPlanThreads>(a, L, tst_s, w);
+  plan_select_slow<kPlanThreads>(a, L, tst_s, w, false, give_ups);
 }
 
 // Walk parameters of stream entry i (i < V: virtual sequence i, else real
@@ -2107,6 +2128,31 @@ __device__ __forceinline__ void stream_finish(const DecodeArgs& a, int* plan, in
   static_assert(kRec + 1 <= 8, "merge record stride");
 }
 
+// A workgroup that waited for a plan build past the poll limit (the builder
+// never published: not expected, since the builder waits for nobody) leaves
+// the launch without its tiles.  The sequences it served never complete, so
+// their output rows would keep stale values: it writes NaN to every output
+// row instead (rows that other workgroups complete may overwrite it with
+// their result), and counts the give-up in the plan header, which makes the
+// next launch rebuild the plan and zero the completion counters this launch
+// left part-way.
+template <int QDT>
+__device__ __forceinline__ void stream_give_up(const DecodeArgs& a) {
+  if (threadIdx.x == 0)
+    __hip_atomic_fetch_add(reinterpret_cast<unsigned int*>(a.plan_region) + kPlanGiveUps, 1u, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+  const int64_t per_row = static_cast<int64_t>(a.num_heads) * kHeadDim;
+  const int64_t n = static_cast<int64_t>(a.batch) * per_row;
+  for (int64_t base = 0; base < n; base += kSThreads) {  // uniform trip count
+    const int64_t e = base + threadIdx.x;
+    const int64_t b = e / per_row;
+    const int64_t r = e - b * per_row;
+    const int64_t hq = r / kHeadDim;
+    const int64_t d = r - hq * kHeadDim;
+    if (e < n) store_out<QDT>(a.out, b * a.o_sb + hq * a.o_sh + d * a.o_sd, __builtin_nanf(""));
+  }
+}
+
 // kSWgPerCu 8-wave workgroups per CU need 2 * kSWgPerCu waves per SIMD.
 template <int QDT, bool QVEC, int TPR>
 __global__ void __launch_bounds__(kSThreads) __attribute__((amdgpu_waves_per_eu(2 * kSWgPerCu)))
@@ -2130,8 +2176,11 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   // (re)built by one workgroup of the launch while the others wait, and the
   // same loads are repeated on the new slot.
   PlanLds& L = *reinterpret_cast<PlanLds*>(stages);
-  const unsigned long long w0 = *reinterpret_cast<const __attribute__((address_space(4))) unsigned long long*>(
+  typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+  const u32x4_t hdr = *reinterpret_cast<const __attribute__((address_space(4))) u32x4_t*>(
       reinterpret_cast<uintptr_t>(a.plan_region));
+  const unsigned long long w0 = static_cast<unsigned long long>(hdr.x) | (static_cast<unsigned long long>(hdr.y) << 32);
+  const unsigned int give_ups = hdr.z;  // plan header int kPlanGiveUps
   int* plan = plan_slot(a, __builtin_amdgcn_readfirstlane(static_cast<int>(w0 & 1)));
   // prefix sums go to registers first and to LDS after the key check, so the
   // check's loads leave in the same round
@@ -2160,12 +2209,17 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   };
   load_plan();
   const bool same =
-      (PRISM_DBG(a) & 128) ? true : (!plan_building_here(w0, a.epoch) && plan_key_check<kSThreads>(a, plan, L));
+      (PRISM_DBG(a) & 128) ? true
+                           : (!plan_building_here(w0, a.epoch) && plan_key_check<kSThreads>(a, plan, L) && give_ups == 0);
   store_tstart();
   if (__builtin_expect(!__syncthreads_and(same ? 1 : 0), 0)) {
     const bool staged = !(PRISM_DBG(a) & 128) && !plan_building_here(w0, a.epoch);  // the check above staged L
-    const int slot = __builtin_amdgcn_readfirstlane(plan_select_slow<kSThreads>(a, L, tstart, w0, staged));
-    if (slot < 0) return;  // the builder never published (cannot happen: it waits for nobody)
+    const int slot =
+        __builtin_amdgcn_readfirstlane(plan_select_slow<kSThreads>(a, L, tstart, w0, staged, give_ups));
+    if (slot < 0) {
+      stream_give_up<QDT>(a);
+      return;
+    }
     plan = plan_slot(a, slot);
     __syncthreads();  // every thread is done with the build's tstart before it is reloaded
     load_plan();
@@ -2696,6 +2750,7 @@ struct EnvOverrides {
   std::atomic<int> path{0};   // 0 automatic, 1 split, 2 stream
   std::atomic<int> split{0};  // 0 automatic, else tokens per split
   std::atomic<int> share{1};
+  std::atomic<int> plan_spin{kPlanSpinLimit};
 };
 
 EnvOverrides& env_overrides() {
@@ -2899,6 +2954,17 @@ extern "C" int prism_paged_decode_set_overrides(int path, int split_tokens, int 
   return PRISM_OK;
 }
 
+extern "C" int prism_paged_decode_set_plan_wait_limit(int polls) {
+  prism::clear_error();
+  if (polls < 0) {
+    prism::set_error("prism_paged_decode_set_plan_wait_limit: polls must be >= 0, got %d", polls);
+    return -1;
+  }
+  return prism::env_overrides().plan_spin.exchange(polls > 0 ? polls : 0);
+}
+
+extern "C" int prism_paged_decode_default_plan_wait_limit(void) { return prism::kPlanSpinLimit; }
+
 extern "C" void prism_paged_decode_get_overrides(int out[3]) {
   auto& o = prism::env_overrides();
   out[0] = o.path.load();
@@ -3094,6 +3160,7 @@ extern "C" int prism_paged_decode_stage(
     args.s_ttok = kSTile * args.s_tpr;
     args.share = env_overrides().share.load();
     args.stream_nwg = geo.stream_nwg;
+    args.plan_spin = env_overrides().plan_spin.load();
   }
   hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
   switch (q_dtype) {

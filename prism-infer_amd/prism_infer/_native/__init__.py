@@ -49,6 +49,8 @@ SIGNATURES: dict[str, tuple] = {
     "prism_paged_decode_kernel_family": (_I, [_I, _I, _I, _I, _I, _I, _I]),
     "prism_paged_decode_set_overrides": (_I, [_I, _I, _I]),
     "prism_paged_decode_get_overrides": (None, [ctypes.POINTER(ctypes.c_int)]),
+    "prism_paged_decode_set_plan_wait_limit": (_I, [_I]),
+    "prism_paged_decode_default_plan_wait_limit": (_I, []),
     "prism_paged_decode": (
         _I,
         [_VP, _I, _I64P, _VP, _VP, _I, _I64P, _I64P, _VP, _VP, _I64P, _I64P, _VP, _I64P, _VP, _VP, _VP,
@@ -111,22 +113,31 @@ def lib() -> ctypes.CDLL:
     if version != ABI_VERSION:
         raise RuntimeError(f"{LIB_NAME} ABI version {version} != expected {ABI_VERSION}; rebuild it")
     _LIB = handle
-    _preload(handle)
     return handle
 
 
-def _preload(handle: ctypes.CDLL) -> None:
-    """Load the kernels' code objects on the current GPU now (a code object
-    otherwise loads at its first kernel's launch and stalls that call).
-    Nothing to do without a GPU; a failure on a GPU is an error."""
+_PRELOADED: set[int] = set()
 
-    import torch  # noqa: PLC0415
 
-    if not torch.cuda.is_available():
-        return
-    status = handle.prism_preload()
+def device_lib(device: torch.device | None = None) -> ctypes.CDLL:
+    """The library, with every kernel's code object loaded on ``device``.
+
+    HIP otherwise loads a code object at its kernel's first launch, which
+    stalls that call (28 ms for the decode kernels) and slows the launches
+    right after it.  The GPU ops call this before their first launch on a
+    device; the load runs once per device, and a failure raises here.
+    """
+
+    handle = lib()
+    index = torch.cuda.current_device() if device is None or device.index is None else device.index
+    if index in _PRELOADED:
+        return handle
+    with torch.cuda.device(index):
+        status = handle.prism_preload()
     if status != 0:
         raise RuntimeError(f"prism_preload failed ({status}): {handle.prism_last_error().decode(errors='replace')}")
+    _PRELOADED.add(index)
+    return handle
 
 
 def available() -> bool:
@@ -181,6 +192,7 @@ __all__ = [
     "SIGNATURES",
     "available",
     "check",
+    "device_lib",
     "dtype_code",
     "int64s",
     "is_built",

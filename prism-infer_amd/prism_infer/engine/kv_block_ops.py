@@ -103,7 +103,7 @@ def copy_kv_block_prefixes(kv_cache: torch.Tensor, copies, scale_cache: torch.Te
 def _copy_blocks(dst: torch.Tensor, src: torch.Tensor, dst_ids: list[int], src_ids: list[int], stream) -> None:
     rows = src.shape[0] * src.shape[1]
     block_bytes = math.prod(src.shape[3:]) * src.element_size()
-    status = _native.lib().prism_copy_blocks(
+    status = _native.device_lib(dst.device).prism_copy_blocks(
         dst.data_ptr(), src.data_ptr(), rows, dst.shape[2] * block_bytes, src.shape[2] * block_bytes,
         block_bytes, dst.shape[2], src.shape[2], _native.int64s(*dst_ids), _native.int64s(*src_ids),
         len(dst_ids), stream,

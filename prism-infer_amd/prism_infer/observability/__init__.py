@@ -30,20 +30,24 @@ _region_provider: Optional[ProfileRegionProvider] = None
 _session_provider: Optional[ProfileSessionProvider] = None
 
 
-def install_performance_provider(*, profile_region_provider: Optional[ProfileRegionProvider],
-                                 profile_session_provider: Optional[ProfileSessionProvider]) -> None:
-    """Install both providers, or remove them by passing ``None`` for both."""
+def install_performance_provider(*, profile_region_provider: ProfileRegionProvider,
+                                 profile_session_provider: ProfileSessionProvider) -> None:
+    """Install both providers; anything not callable (``None`` included) is a TypeError."""
 
     global _region_provider, _session_provider
-    if profile_region_provider is None and profile_session_provider is None:
-        _region_provider = _session_provider = None
-        return
     if not callable(profile_region_provider) or not callable(profile_session_provider):
         raise TypeError("install_performance_provider: both providers must be callables "
                         f"(got {type(profile_region_provider).__name__} and "
                         f"{type(profile_session_provider).__name__})")
     _region_provider = profile_region_provider
     _session_provider = profile_session_provider
+
+
+def _reset_performance_providers() -> None:
+    """Remove the installed providers (for tests); regions become no-ops again."""
+
+    global _region_provider, _session_provider
+    _region_provider = _session_provider = None
 
 
 def profile_region(name: str, *, cuda: bool = True, metadata: Optional[dict] = None) -> AbstractContextManager:

@@ -6,8 +6,9 @@ signature (:419-427), same contract validation and error messages
 path :58-78 / :228-230).  The work is done by ``prism_kv_store`` in
 libprism_mi355x.so.  Differences from the reference, all deliberate:
 
-* there is no eager CPU fallback: tensors must be on the GPU, and a missing
-  native library raises (the reference routes CPU tensors to a Python loop);
+* CPU tensors take a vectorized torch path of this module's own (the
+  reference routes them to a per-token Python loop, :439-476); GPU tensors
+  always take the HIP kernels, and a missing native library raises there;
 * the scaled path is bit-exact against the eager oracle, including scales
   (the reference's Triton kernel is only checked to 1e-6 relative);
 * slots >= the cache's slot count are skipped instead of written out of bounds.
@@ -120,12 +121,81 @@ def _validate_device_store_layout(key, value, k_cache, v_cache, slot_mapping, k_
         raise ValueError(f"key/value dtype must be one of float32/bfloat16/float16 and match, got {key.dtype}/{value.dtype}")
 
 
-def _store_profile_region(scaled: bool, k_cache: torch.Tensor) -> str:
+def _store_profile_region(scaled: bool, k_cache: torch.Tensor, on_cpu: bool = False) -> str:
+    if on_cpu:
+        return "attention.kv_store.eager"
     if scaled:
         return "attention.kv_store.hip_scaled_fp8"
     if is_fp8_cache_tensor(k_cache):
         return "attention.kv_store.hip_fp8"
     return "attention.kv_store.hip"
+
+
+def _last_writer_rows(slot_mapping: torch.Tensor, num_slots: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """(token rows, slots) to write: slots < 0 are skipped and, for a slot named
+    by several tokens, only the last token is kept (the reference's loop writes
+    tokens in order, so the last one is what the slot holds afterwards)."""
+
+    slots = slot_mapping.to(torch.long)
+    rows = torch.nonzero(slots >= 0).flatten()
+    slots = slots[rows]
+    if slots.numel() and int(slots.max()) >= num_slots:
+        bad = int(slots.max())
+        raise IndexError(f"slot {bad} is out of range for a KV cache of {num_slots} slots")
+    if slots.numel() > 1:
+        unique, inverse = torch.unique(slots, return_inverse=True)
+        last = torch.full((unique.numel(),), -1, dtype=torch.long)
+        last.scatter_reduce_(0, inverse, rows, reduce="amax")
+        rows, slots = last, unique
+    return rows, slots
+
+
+def _quantize_rows(x: torch.Tensor, cache_dtype: torch.dtype) -> tuple[torch.Tensor, torch.Tensor]:
+    """[n, heads, dim] -> (E4M3FN payload, fp32 scale per (row, head)).
+
+    scale = max(amax|x| / 448, floor), payload = RNE(clamp(x / scale, +-448));
+    the quotient is an IEEE fp32 division, as in the reference's loop."""
+
+    xf = x.float()
+    scale = torch.clamp(xf.abs().amax(dim=-1) / FP8_E4M3FN_MAX, min=PER_TOKEN_HEAD_SCALE_FLOOR)
+    payload = torch.clamp(xf / scale.unsqueeze(-1), min=FP8_E4M3FN_MIN, max=FP8_E4M3FN_MAX).to(cache_dtype)
+    return payload, scale
+
+
+def _store_kvcache_cpu(key, value, k_cache, v_cache, slot_mapping, k_scale_cache, v_scale_cache) -> None:
+    """Host-tensor store: the reference's eager semantics (:183-230), vectorized
+    over tokens. Payload rows and scales are written with index_copy_ on flat
+    [slots, heads, dim] / [slots, heads] views of the caches."""
+
+    caches = tuple(t for t in (k_cache, v_cache, k_scale_cache, v_scale_cache) if t is not None)
+    if not all(t.is_contiguous() for t in caches):
+        raise RuntimeError("KV store requires contiguous KV and scale caches")
+    heads, dim = key.shape[-2], key.shape[-1]
+    flat_k = k_cache.view(-1, heads, dim)
+    flat_v = v_cache.view(-1, heads, dim)
+    rows, slots = _last_writer_rows(slot_mapping, flat_k.shape[0])
+    if rows.numel() == 0:
+        return
+    k_rows = key.index_select(0, rows)
+    v_rows = value.index_select(0, rows)
+    if k_scale_cache is None:
+        _index_copy_bytes(flat_k, slots, k_rows.to(k_cache.dtype))
+        _index_copy_bytes(flat_v, slots, v_rows.to(v_cache.dtype))
+        return
+    k_payload, k_scale = _quantize_rows(k_rows, k_cache.dtype)
+    v_payload, v_scale = _quantize_rows(v_rows, v_cache.dtype)
+    _index_copy_bytes(flat_k, slots, k_payload)
+    _index_copy_bytes(flat_v, slots, v_payload)
+    _index_copy_bytes(k_scale_cache.view(-1, heads), slots, k_scale)
+    _index_copy_bytes(v_scale_cache.view(-1, heads), slots, v_scale)
+
+
+def _index_copy_bytes(dst: torch.Tensor, index: torch.Tensor, rows: torch.Tensor) -> None:
+    """dst[index[i]] = rows[i], moved as raw bytes (exact for every dtype,
+    NaN payloads included)."""
+
+    as_bytes = {1: torch.uint8, 2: torch.int16, 4: torch.int32, 8: torch.int64}[dst.element_size()]
+    dst.view(as_bytes).index_copy_(0, index, rows.contiguous().view(as_bytes))
 
 
 def store_kvcache(
@@ -140,10 +210,18 @@ def store_kvcache(
     """Write current K/V values into canonical paged KV-cache slots (in place)."""
 
     scaled = _validate_store_inputs(key, value, k_cache, v_cache, slot_mapping, k_scale_cache, v_scale_cache)
+    tensors = (key, value, k_cache, v_cache, slot_mapping, k_scale_cache, v_scale_cache)
+    if not any(t is not None and t.is_cuda for t in tensors):
+        with profile_region(
+            _store_profile_region(scaled, k_cache, on_cpu=True),
+            metadata={"cache_dtype": str(k_cache.dtype), "tokens": key.shape[0]},
+        ):
+            _store_kvcache_cpu(key, value, k_cache, v_cache, slot_mapping, k_scale_cache, v_scale_cache)
+        return
     _validate_device_store_layout(key, value, k_cache, v_cache, slot_mapping, k_scale_cache, v_scale_cache)
     num_tokens, num_heads, head_dim = key.shape
     num_slots = k_cache.numel() // (num_heads * head_dim) if k_cache.numel() else 0
-    lib = _native.lib()
+    lib = _native.device_lib(key.device)
     with profile_region(
         _store_profile_region(scaled, k_cache),
         metadata={"cache_dtype": str(k_cache.dtype), "tokens": num_tokens},

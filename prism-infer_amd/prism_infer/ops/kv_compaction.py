@@ -12,8 +12,9 @@ by separate calls, exactly as the reference's caller does.
 The native side first detects on the device whether any destination aliases
 another entry's source; only then does it stage through the workspace (two
 passes), otherwise it moves each slot once.  Every dtype goes through the
-same byte-moving kernels (the reference uses torch index ops for non-FP8 and
-CPU caches; here everything runs on the GPU and a CPU cache raises).
+same byte-moving kernels on the GPU.  A CPU cache is compacted with torch
+index ops over a byte view of the cache (the reference uses index ops for CPU
+and non-FP8 caches, :105-112).
 """
 
 from __future__ import annotations
@@ -56,12 +57,27 @@ def _validate_compaction_inputs(cache, source_slots, destination_slots) -> None:
 def _validate_device_layout(cache, source_slots, destination_slots) -> None:
     if not HAS_HIP_KERNELS:
         _native.lib()  # raises with the reason
-    if not cache.is_cuda:
-        raise RuntimeError("MI355X KV compaction requires GPU tensors (there is no CPU fallback)")
     if not cache.is_contiguous():
         raise RuntimeError("MI355X KV compaction requires contiguous cache")
     if not source_slots.is_contiguous() or not destination_slots.is_contiguous():
         raise RuntimeError("MI355X KV compaction requires contiguous slot tensors")
+
+
+def _compact_cpu(cache: torch.Tensor, source_slots: torch.Tensor, destination_slots: torch.Tensor) -> None:
+    """Host caches: gather every source slot, then scatter to the destinations.
+
+    The cache is seen as [rows, slots, bytes] so every dtype (FP8 payload,
+    fp32 scales, NaN bit patterns) moves exactly.  The gather completes before
+    the scatter starts, so overlapping plans read what the sources held before
+    the call.  Out-of-range slots raise from index_select, as the reference's
+    index ops do."""
+
+    if not cache.is_contiguous():
+        raise RuntimeError("KV compaction requires a contiguous cache")
+    rows = cache.shape[0] * cache.shape[1]
+    as_bytes = cache.view(torch.uint8).view(rows, cache.shape[2], -1)
+    gathered = as_bytes.index_select(1, source_slots)
+    as_bytes.index_copy_(1, destination_slots, gathered)
 
 
 def compaction_workspace_bytes(cache: torch.Tensor, retained: int) -> int:
@@ -83,12 +99,15 @@ def compact_kv_slots(
     """
 
     _validate_compaction_inputs(cache, source_slots, destination_slots)
+    if not cache.is_cuda:
+        _compact_cpu(cache, source_slots, destination_slots)
+        return
     _validate_device_layout(cache, source_slots, destination_slots)
     rows = cache.shape[0] * cache.shape[1]
     num_slots = cache.shape[2]
     vec_bytes = math.prod(cache.shape[3:]) * cache.element_size()
     retained = source_slots.numel()
-    lib = _native.lib()
+    lib = _native.device_lib(cache.device)
     ws_bytes = compaction_workspace_bytes(cache, retained)
     workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=cache.device)
     with torch.cuda.device(cache.device):

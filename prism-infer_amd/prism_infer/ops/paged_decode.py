@@ -201,7 +201,7 @@ def _launch_paged_decode_attention(q, k_cache, v_cache, block_tables, context_le
                                    workspace: torch.Tensor | None = None) -> torch.Tensor:
     batch, num_heads, head_dim = q.shape
     num_blocks, page_size, num_kv_heads, _ = k_cache.shape
-    lib = _native.lib()
+    lib = _native.device_lib(q.device)
     if output is None:
         output = torch.empty_like(q)
     ws_bytes = decode_workspace_bytes(q, k_cache, block_tables)

@@ -125,10 +125,11 @@ def _launch_paged_prefill(q, k_cache, v_cache, context, *, num_heads, num_kv_hea
             "K/V caches must be [num_blocks, block_size, num_kv_heads, head_dim] matching q, "
             f"got {list(k_cache.shape)}"
         )
-    lib = _native.lib()  # raises with the reason the library is unavailable
+    _native.lib()  # raises with the reason the library is unavailable
     tensors = [q, k_cache, v_cache] + ([k_scale_cache, v_scale_cache] if scaled else [])
     if not all(t.is_cuda for t in tensors) or any(t.device != q.device for t in tensors):
         raise RuntimeError("paged_prefill_attention runs on the GPU: q, caches and scales must share one CUDA device")
+    lib = _native.device_lib(q.device)
     if k_cache.dtype != torch.float8_e4m3fn:
         raise RuntimeError(f"the HIP paged prefill kernel reads FP8 E4M3FN caches, got {k_cache.dtype}")
     if q.dtype not in (torch.bfloat16, torch.float16):

@@ -27,11 +27,18 @@ def _oracle_built():
 
 
 @pytest.fixture(autouse=True)
-def _reset_decode_overrides():
-    """Every test starts and ends with the automatic decode kernel choice."""
+def _restore_decode_overrides():
+    """A test that forces a decode kernel family leaves the process's choice as
+    it found it (the automatic choice, or what PRISM_DECODE_* selected)."""
 
-    yield
+    import ctypes
+
     from prism_infer import _native
 
-    if _native.available():
-        _native.lib().prism_paged_decode_set_overrides(0, 0, 1)
+    if not _native.available():
+        yield
+        return
+    saved = (ctypes.c_int * 3)()
+    _native.lib().prism_paged_decode_get_overrides(saved)
+    yield
+    _native.lib().prism_paged_decode_set_overrides(saved[0], saved[1], saved[2])

@@ -3,8 +3,8 @@
 Error types and messages follow the reference runner
 (prism_infer/engine/model_runner.py:917-1031): prefix rows outside
 [1, block_size] raise ValueError, a bad swap direction ValueError, a missing
-CPU cache or unpaired scale caches RuntimeError.  Valid CPU tensors reach the
-device path and raise (there is no CPU fallback).
+CPU cache or unpaired scale caches RuntimeError.  Valid CPU caches go through
+``compact_kv_slots``'s CPU branch, like the reference's torch copies.
 """
 
 from __future__ import annotations
@@ -56,7 +56,12 @@ def test_swap_contract():
         swap_blocks(kv, kv.clone(), [(0, 0)], "out")
 
 
-def test_copies_have_no_cpu_fallback():
+def test_copies_on_cpu_caches():
     kv, sc = _caches()
-    with pytest.raises(RuntimeError, match="no CPU fallback"):
-        copy_kv_blocks(kv, [(0, 1)], sc)
+    kv[:, :, 0].copy_(torch.randn(2, 1, 4, 1, 2))
+    sc[:, :, 0].copy_(torch.randn(2, 1, 4, 1))
+    copy_kv_blocks(kv, [(0, 1)], sc)
+    assert torch.equal(kv[:, :, 1], kv[:, :, 0]) and torch.equal(sc[:, :, 1], sc[:, :, 0])
+    copy_kv_block_prefixes(kv, [(0, 2, 3)], sc)
+    assert torch.equal(kv[:, :, 2, :3], kv[:, :, 0, :3]) and bool((kv[:, :, 2, 3] == 0).all())
+    assert torch.equal(sc[:, :, 2, :3], sc[:, :, 0, :3])

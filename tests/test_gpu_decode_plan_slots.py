@@ -113,3 +113,56 @@ def test_stale_building_word_is_rebuilt(fill):
     assert_decode_close(out.cpu(), want, label=f"stale building word, fill {fill:#x}")
     w = int(word.item())
     assert (w & 2) == 0, "the plan word is published"
+
+
+def test_plan_wait_give_up_is_loud_and_rebuilt():
+    """Workgroups that stop waiting for a plan build leave NaN rows, and the next call rebuilds.
+
+    The wait limit is set to 0 polls from the host, so every workgroup that
+    finds another one building gives up at once (all kernels still exit).  The
+    give-up is counted in the plan header (int 2 of the workspace); the next
+    call with the normal limit rebuilds the plan, zeroing the completion
+    counters the abandoned call left part-way, and its output is the same bits
+    as a call on a fresh workspace.
+    """
+
+    require_gpu()
+    from prism_infer import _native
+    from prism_infer.ops.paged_decode import _launch_paged_decode_attention, decode_workspace_bytes
+
+    set_decode_overrides(path="stream")
+    lib = _native.lib()
+    dev = torch.device("cuda")
+    q, k, v, ks, vs, tables, lens_a, lens_b = _case()
+    to = lambda t: t.view(torch.uint8).to(dev).view(FP8) if t.dtype == FP8 else t.to(dev)  # noqa: E731
+    qd, kd, vd, ksd, vsd, td = map(to, (q, k, v, ks, vs, tables))
+    lens_dev = {"a": to(lens_a), "b": to(lens_b)}
+    mx = torch.tensor([tables.shape[1] * 256], dtype=torch.int32, device=dev)
+    nbytes = decode_workspace_bytes(qd, kd, td)
+    ws = torch.zeros(nbytes, dtype=torch.uint8, device=dev)
+
+    def run(which, workspace):
+        out = _launch_paged_decode_attention(qd, kd, vd, td, lens_dev[which], 128 ** -0.5, mx, k_scale_cache=ksd,
+                                             v_scale_cache=vsd, scaled_kv=True, workspace=workspace)
+        torch.cuda.synchronize()
+        return out.cpu()
+
+    fresh_b = run("b", torch.zeros(nbytes, dtype=torch.uint8, device=dev))
+    run("a", ws)
+    default = lib.prism_paged_decode_default_plan_wait_limit()
+    previous = lib.prism_paged_decode_set_plan_wait_limit(0)
+    try:
+        assert previous == default
+        abandoned = run("b", ws)  # metadata changed: one workgroup builds, the waiters give up
+    finally:
+        assert lib.prism_paged_decode_set_plan_wait_limit(default) == 0
+    give_ups = int(ws[8:12].view(torch.int32).item())
+    print(f"give-ups: {give_ups}, NaN rows: {int(torch.isnan(abandoned.float()).any(-1).any(-1).sum())}", flush=True)
+    if give_ups:
+        assert bool(torch.isnan(abandoned.float()).any()), "a give-up leaves NaN rows"
+    else:
+        assert torch.equal(abandoned, fresh_b)
+    assert torch.equal(run("b", ws), fresh_b), "rebuilt after the give-up"
+    assert int(ws[8:12].view(torch.int32).item()) == 0, "the rebuild clears the give-up count"
+    assert torch.equal(run("b", ws), fresh_b), "the rebuilt plan is reused"
+    assert lib.prism_paged_decode_set_plan_wait_limit(-1) == -1

@@ -19,9 +19,9 @@ from prism_infer.ops.kv_cache_store import _store_profile_region
 
 @pytest.fixture(autouse=True)
 def _no_provider():
-    obs.install_performance_provider(profile_region_provider=None, profile_session_provider=None)
+    obs._reset_performance_providers()
     yield
-    obs.install_performance_provider(profile_region_provider=None, profile_session_provider=None)
+    obs._reset_performance_providers()
 
 
 def test_default_is_a_noop():
@@ -35,6 +35,8 @@ def test_non_callable_providers_raise():
     with pytest.raises(TypeError):
         obs.install_performance_provider(profile_region_provider=lambda *a, **k: nullcontext(),
                                          profile_session_provider=3)
+    with pytest.raises(TypeError):
+        obs.install_performance_provider(profile_region_provider=None, profile_session_provider=None)
 
 
 def test_installed_providers_receive_name_cuda_and_metadata():
