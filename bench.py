@@ -549,6 +549,7 @@ def _extras(torch, dev, workloads) -> dict:
     # the launch): measure it with a one-element kernel, to read short calls.
     tiny = torch.zeros(1, device=dev)
     out["queued_call_floor_us"] = round(_time_queued(lambda i: tiny.add_(1), 1, torch, flush=flush) * 1e6, 2)
+    out["copy_ceiling"] = _copy_ceiling(torch, dev, flush)
     # store: 8192 tokens into a 512-page pool; one call cold, and 8 calls back
     # to back over 8 distinct input chunks (268 MB, more than the MALL), as a
     # prefill's layers issue them
@@ -568,6 +569,9 @@ def _extras(torch, dev, workloads) -> dict:
     store_kvcache(keys[0], values[0], kc, vc, sw.slot_mapping, ks, vs)
     sw8 = _time_queued(lambda i: store_kvcache(keys[0], values[0], kc, vc, sw.slot_mapping, ks, vs), 8, torch)
     out["store_prefill"] = {"us": round(s8 * 1e6, 2), "GBps": round(sw.algorithmic_bytes() / s8 / 1e9, 1),
+                            "pct_of_hbm_peak": round(100.0 * sw.algorithmic_bytes() / s8 / 1e9 / HBM_PEAK_GBPS, 2),
+                            "frac_of_copy_ceiling": round(sw.algorithmic_bytes() / s8 / 1e9 /
+                                                          out["copy_ceiling"]["best_store_size_GBps"], 4),
                             "us_single_call": round(s1 * 1e6, 2), "us_warm_inputs": round(sw8 * 1e6, 2),
                             "bytes": sw.algorithmic_bytes(),
                             "timing": "8 calls back to back over 8 distinct cold input chunks, queued behind a "
@@ -587,18 +591,15 @@ def _extras(torch, dev, workloads) -> dict:
         compact_kv_slots(scales, src, dst)
 
     s = _time_queued(compact, 1, torch, flush=flush)
-    # the practical ceiling of a gather/scatter copy: a 1 GiB device copy, cold
-    big = torch.empty(1 << 30, dtype=torch.uint8, device=dev)
-    big2 = torch.empty_like(big)
-    sc = _time_queued(lambda i: big2.copy_(big), 1, torch, flush=flush)
-    copy_gbps = 2 * big.numel() / sc / 1e9
-    del big, big2
+    copy_gbps = out["copy_ceiling"]["best_GBps"]
     out["compaction_out_of_place"] = {"us": round(s * 1e6, 2), "GBps": round(cw.algorithmic_bytes() / s / 1e9, 1),
                                       "bytes": cw.algorithmic_bytes(), "kept_tokens": cw.kept,
-                                      "copy_probe_GBps": round(copy_gbps, 1),
-                                      "frac_of_copy_probe": round(cw.algorithmic_bytes() / s / 1e9 / copy_gbps, 4),
-                                      "timing": "queued behind a spin, cold (payload and scale calls); copy probe: "
-                                                "1 GiB device-to-device copy, read + write bytes, cold"}
+                                      "pct_of_hbm_peak": round(100.0 * cw.algorithmic_bytes() / s / 1e9 /
+                                                               HBM_PEAK_GBPS, 2),
+                                      "copy_ceiling_GBps": round(copy_gbps, 1),
+                                      "frac_of_copy_ceiling": round(cw.algorithmic_bytes() / s / 1e9 / copy_gbps, 4),
+                                      "timing": "queued behind a spin, cold (payload and scale calls); copy "
+                                                "ceiling: the copy_ceiling extra"}
     del payload, scales, src, dst
     # single-sequence decode (latency bound): Qwen3-VL-shaped, B=1, 1800 tokens, 36 layers with their own pools
     layers = [workloads.decode_qwen_vl(dev, seed=20260803 + li) for li in range(36)]
@@ -665,6 +666,8 @@ def _extras(torch, dev, workloads) -> dict:
     # sequence's pages (shared ones included) once per sequence
     w = workloads.decode_mixed(dev)
     attended = int(w.context_lens.sum().item())
+    unique = w.unique_kv_tokens()
+    fixed = w.algorithmic_bytes() - unique * 2112  # q, output, tables, lengths
     variants = {}
     for name, k, v, row in (("unit_scale_fp8", w.k_cache, w.v_cache, 2 * 8 * 128),
                             ("bf16", (w.k_cache.float() * w.k_scale.unsqueeze(-1)).to(torch.bfloat16),
@@ -672,12 +675,102 @@ def _extras(torch, dev, workloads) -> dict:
         call = lambda i, k=k, v=v: paged_decode_attention(  # noqa: E731
             w.q, k, v, w.block_tables, w.context_lens, w.scale, max_context_len=w.max_context_len)
         s = _time_queued(call, 3, torch, flush=flush)
-        variants[name] = {"us": round(s * 1e6, 1), "GBps_attended": round(attended * row / s / 1e9, 1),
-                          "bytes_attended": attended * row}
+        alg = unique * row + fixed
+        variants[name] = {"us": round(s * 1e6, 1), "GBps": round(alg / s / 1e9, 1),
+                          "pct_of_hbm_peak": round(100.0 * alg / s / 1e9 / HBM_PEAK_GBPS, 2), "bytes": alg,
+                          "GBps_attended": round(attended * row / s / 1e9, 1), "bytes_attended": attended * row}
         del k, v
-    out["decode_mixed_dense_variants"] = {**variants, "timing": "3 calls back to back, queued behind a spin, cold"}
+    out["decode_mixed_dense_variants"] = {
+        **variants, "timing": "3 calls back to back, queued behind a spin, cold",
+        "bytes_note": "bytes: each unique (page, row) once (the shared prefix once) + q, output, tables, lengths; "
+                      "bytes_attended counts the shared prefix once per sequence"}
     del w
+    out["decode_small_batch_matrix"] = _small_batch_matrix(torch, dev, flush)
     return out
+
+
+def _copy_ceiling(torch, dev, flush) -> dict:
+    """Read + write ceiling of a plain device copy, cold: torch's Tensor.copy_
+    of 1 GiB, and the library's streaming copy (prism_device_copy: persistent
+    grid, non-temporal 16-byte loads and stores, eight in flight per lane) at
+    1, 2, 4 and 8 workgroups per CU, over 1 GiB (one call) and over the store's
+    size (25.4 MB read + 25.4 MB written, 8 calls back to back over 8 distinct
+    buffers, as the store extra is timed)."""
+
+    from prism_infer import _native  # noqa: PLC0415
+
+    lib = _native.device_lib(dev)
+    stream = _native.stream_handle(dev)
+    res = {}
+    for nbytes, calls, tag in ((1 << 30, 1, "1GiB"), (25_444_352, 8, "store_size")):
+        srcs = [torch.ones(nbytes, dtype=torch.uint8, device=dev) for _ in range(calls)]
+        dsts = [torch.empty_like(x) for x in srcs]
+        sec = _time_queued(lambda i: dsts[i].copy_(srcs[i]), calls, torch, flush=flush)
+        res[f"torch_copy_{tag}_GBps"] = round(2 * nbytes / sec / 1e9, 1)
+        for wpc in (1, 2, 4, 8):
+            call = lambda i, w=wpc: _native.check(  # noqa: E731
+                lib.prism_device_copy(dsts[i].data_ptr(), srcs[i].data_ptr(), nbytes, w, stream),
+                "prism_device_copy")
+            sec = _time_queued(call, calls, torch, flush=flush)
+            res[f"stream_copy_{tag}_wpc{wpc}_GBps"] = round(2 * nbytes / sec / 1e9, 1)
+            res[f"stream_copy_{tag}_wpc{wpc}_us"] = round(sec * 1e6, 2)
+        assert all(torch.equal(d, x) for d, x in zip(dsts, srcs))
+        del srcs, dsts
+    res["best_GBps"] = max(v for k, v in res.items() if "1GiB" in k and k.endswith("GBps"))
+    res["best_store_size_GBps"] = max(v for k, v in res.items() if "store_size" in k and k.endswith("GBps"))
+    res["timing"] = "queued behind a spin, cold; GBps = 2 x bytes (read + write) / time per call"
+    return res
+
+
+def _small_batch_matrix(torch, dev, flush) -> dict:
+    """The reference's kernel benchmark matrix (benchmarks/bench_paged_decode.py:40-51):
+    B in {1, 2, 4, 8} x context in {256, 1024, 4096} tokens, 32 q / 8 kv heads,
+    head_dim 128, 256-token pages, bf16 queries; caches bf16, unit-scale FP8
+    (the reference harness's "fp8": a cast, no scales) and scaled FP8.  Each
+    shape runs as 8 layers with their own pools, back to back, cold (the
+    reference times one warm call with host timers)."""
+
+    from prism_infer.ops.kv_cache_store import store_kvcache  # noqa: PLC0415
+    from prism_infer.ops.paged_decode import paged_decode_attention  # noqa: PLC0415
+
+    layers, page, hq, hkv, d = 8, 256, 32, 8, 128
+    g = torch.Generator(device=dev)
+    g.manual_seed(20260717)
+    rows = {}
+    for ctx in (256, 1024, 4096):
+        for batch in (1, 2, 4, 8):
+            pages = -(-ctx // page)
+            tables = torch.arange(batch * pages, dtype=torch.int32, device=dev).view(batch, pages)
+            lens = torch.full((batch,), ctx, dtype=torch.int32, device=dev)
+            q = torch.randn(batch, hq, d, generator=g, device=dev, dtype=torch.bfloat16)
+            slots = torch.arange(batch * pages * page, dtype=torch.int32, device=dev).view(batch, -1)[:, :ctx]
+            slots = slots.reshape(-1).contiguous()
+            dense, unit, scaled = [], [], []
+            for _ in range(layers):
+                kd = torch.zeros(batch * pages, page, hkv, d, dtype=torch.bfloat16, device=dev)
+                vd = torch.zeros_like(kd)
+                key = torch.randn(batch * ctx, hkv, d, generator=g, device=dev, dtype=torch.bfloat16)
+                val = torch.randn(batch * ctx, hkv, d, generator=g, device=dev, dtype=torch.bfloat16)
+                store_kvcache(key, val, kd, vd, slots)
+                dense.append((kd, vd, None, None))
+                unit.append((kd.to(torch.float8_e4m3fn), vd.to(torch.float8_e4m3fn), None, None))
+                k8 = torch.zeros(batch * pages, page, hkv, d, dtype=torch.float8_e4m3fn, device=dev)
+                v8 = torch.zeros_like(k8)
+                ks = torch.zeros(batch * pages, page, hkv, dtype=torch.float32, device=dev)
+                vs = torch.zeros_like(ks)
+                store_kvcache(key, val, k8, v8, slots, ks, vs)
+                scaled.append((k8, v8, ks, vs))
+            fixed = 2 * batch * hq * d * 2 + batch * pages * 4 + batch * 4
+            for name, caches, per_tok in (("bf16", dense, 2 * hkv * d * 2), ("fp8", unit, 2 * hkv * d),
+                                          ("scaled_fp8", scaled, 2 * hkv * d + 2 * hkv * 4)):
+                call = lambda i, c=caches: paged_decode_attention(  # noqa: E731
+                    q, c[i][0], c[i][1], tables, lens, d ** -0.5, k_scale_cache=c[i][2], v_scale_cache=c[i][3])
+                sec = _time_queued(call, layers, torch, flush=flush)
+                alg = batch * ctx * per_tok + fixed
+                rows[f"{name}_b{batch}_ctx{ctx}"] = {"us": round(sec * 1e6, 2), "GBps": round(alg / sec / 1e9, 1)}
+            del dense, unit, scaled
+    return {**rows, "timing": "8 layers back to back per shape, queued behind a spin, cold; GBps: unique K/V "
+                              "(+ scales) + q + output + tables + lengths per call"}
 
 
 if __name__ == "__main__":

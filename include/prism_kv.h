@@ -29,6 +29,7 @@ extern "C" {
 #define PRISM_ERR_INVALID (-1) /* contract violation (shape, dtype, size)   */
 #define PRISM_ERR_LAYOUT (-2)  /* unsupported layout / alignment / stride   */
 #define PRISM_ERR_HIP (-3)     /* a HIP runtime call failed                 */
+#define PRISM_ERR_BUSY (-4)    /* a shared resource is in use by a running call */
 
 #define PRISM_DTYPE_F32 0
 #define PRISM_DTYPE_BF16 1
@@ -134,9 +135,14 @@ int prism_paged_decode(const void* q, int q_dtype, const int64_t q_strides[3], c
  * A geometry whose prism_paged_decode_workspace_bytes() exceeds 64 MiB is
  * rejected with PRISM_ERR_INVALID (e.g. B = 256 at 32k tokens needs about
  * 36 MiB and fits).  Calls no hipMalloc, hipFree or allocating library
- * routine.  Every call on one GPU shares that GPU's scratch: calls that
- * overlap on one GPU (different streams, or different host threads) race
- * and must be serialised by the caller.
+ * routine.  Every call on one GPU shares that GPU's scratch, so calls must
+ * not overlap on one GPU.  The entry point refuses, with PRISM_ERR_BUSY, a
+ * call on another stream while the previous call's kernels have not
+ * finished (checked with an event recorded behind each call; the event is
+ * created with the scratch's address on the device's first call).  Calls on
+ * the same stream are ordered by the stream and always accepted.  Launches
+ * recorded under graph capture are not checked: replays of a captured graph
+ * that overlap other calls on the same GPU race.
  */
 int prism_paged_decode_noalloc(const void* q, int q_dtype, const int64_t q_strides[3],
                                const void* k_cache, const void* v_cache, int cache_dtype,
@@ -255,6 +261,16 @@ int prism_compact_slots(void* cache, int64_t rows, int64_t num_slots, int64_t ve
 int prism_copy_blocks(void* dst, const void* src, int64_t rows, int64_t dst_row_pitch, int64_t src_row_pitch,
                       int64_t block_bytes, int64_t dst_blocks, int64_t src_blocks, const int64_t* dst_ids,
                       const int64_t* src_ids, int64_t n, void* stream);
+
+/*
+ * Streaming device-to-device copy of nbytes (a multiple of 16; both pointers
+ * 16-byte aligned) with `workgroups_per_cu` workgroups per CU (1-64),
+ * non-temporal 16-byte loads and stores, eight in flight per lane.  NO
+ * COUNTERPART IN THE REFERENCE: it is the measured read + write ceiling that
+ * the store and compaction kernels, which touch every byte once, are
+ * compared with.  Returns PRISM_OK, PRISM_ERR_INVALID or PRISM_ERR_LAYOUT.
+ */
+int prism_device_copy(void* dst, const void* src, int64_t nbytes, int workgroups_per_cu, void* stream);
 
 /*
  * Paged prefill attention (chunked / prefix-hit prefill) over paged FP8

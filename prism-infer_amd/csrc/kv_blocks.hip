@@ -7,6 +7,8 @@
 // kernels instead (all reads before writes).
 #include "common.h"
 
+#include <algorithm>
+
 extern "C" int prism_copy_blocks(void* dst, const void* src, int64_t rows, int64_t dst_row_pitch,
                                  int64_t src_row_pitch, int64_t block_bytes, int64_t dst_blocks,
                                  int64_t src_blocks, const int64_t* dst_ids, const int64_t* src_ids, int64_t n,
@@ -44,4 +46,55 @@ extern "C" int prism_copy_blocks(void* dst, const void* src, int64_t rows, int64
     if (rc) return rc;
   }
   return PRISM_OK;
+}
+
+// Streaming device-to-device copy: the read + write ceiling that the store
+// and compaction kernels are measured against (each touches every byte once,
+// as this copy does).  A grid of `workgroups_per_cu` workgroups per CU walks
+// the buffer in trips of kCopyUnroll 16-byte chunks per lane, all loads of a
+// trip issued before its stores, with the non-temporal policy on both sides.
+namespace prism {
+namespace {
+
+constexpr int kCopyThreads = 256;
+constexpr int kCopyUnroll = 8;
+
+__global__ void __launch_bounds__(kCopyThreads)
+stream_copy_kernel(u32x4* __restrict__ dst, const u32x4* __restrict__ src, int64_t n16) {
+  const int64_t stride = static_cast<int64_t>(gridDim.x) * kCopyThreads;
+  const int64_t trip = stride * kCopyUnroll;
+  int64_t i = static_cast<int64_t>(blockIdx.x) * kCopyThreads + threadIdx.x;
+  for (; i + (kCopyUnroll - 1) * stride < n16; i += trip) {  // whole trips
+    u32x4 v[kCopyUnroll];
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u) v[u] = __builtin_nontemporal_load(src + i + u * stride);
+#pragma unroll
+    for (int u = 0; u < kCopyUnroll; ++u) __builtin_nontemporal_store(v[u], dst + i + u * stride);
+  }
+  for (; i < n16; i += stride) __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
+}
+
+}  // namespace
+}  // namespace prism
+
+extern "C" int prism_device_copy(void* dst, const void* src, int64_t nbytes, int workgroups_per_cu,
+                                 void* stream_ptr) {
+  prism::clear_error();
+  if (nbytes < 0 || (nbytes % 16) != 0 || workgroups_per_cu < 1 || workgroups_per_cu > 64) {
+    prism::set_error("prism_device_copy: nbytes must be a non-negative multiple of 16 and workgroups_per_cu in "
+                     "[1, 64] (got %lld, %d)", static_cast<long long>(nbytes), workgroups_per_cu);
+    return PRISM_ERR_INVALID;
+  }
+  if (!prism::aligned(dst, 16) || !prism::aligned(src, 16)) {
+    prism::set_error("prism_device_copy: dst and src must be 16-byte aligned");
+    return PRISM_ERR_LAYOUT;
+  }
+  if (nbytes == 0) return PRISM_OK;
+  const int64_t n16 = nbytes / 16;
+  const int64_t want = static_cast<int64_t>(prism::device_cu_count()) * workgroups_per_cu;
+  const int blocks = static_cast<int>(std::max<int64_t>(1, std::min(want, prism::ceil_div(n16, prism::kCopyThreads))));
+  hipLaunchKernelGGL(prism::stream_copy_kernel, dim3(blocks), dim3(prism::kCopyThreads), 0,
+                     static_cast<hipStream_t>(stream_ptr), static_cast<prism::u32x4*>(dst),
+                     static_cast<const prism::u32x4*>(src), n16);
+  return prism::check_launch("stream_copy_kernel launch");
 }

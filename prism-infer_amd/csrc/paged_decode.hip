@@ -3203,8 +3203,20 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_mutex;
 void* g_scratch_ptr[kMaxDevices] = {};
 
-// The current device's copy of `scratch` (looked up on its first use).
-int scratch_for_current_device(void** out) {
+// In-flight guard of each device's scratch: the stream of the last call that
+// used it and an event recorded behind that call's kernels.  A call on
+// another stream while that event has not completed would overwrite the
+// plan, partials and counters the running call is using, so it is refused.
+struct ScratchUse {
+  hipEvent_t done = nullptr;
+  hipStream_t stream = nullptr;
+  bool recorded = false;
+};
+ScratchUse g_scratch_use[kMaxDevices];
+
+// The current device's copy of `scratch` and its guard (set up on the
+// device's first call: the symbol's address and the guard's event).
+int scratch_for_current_device(void** out, int* device) {
   int dev = 0;
   if (int rc = check_hip(hipGetDevice(&dev), "prism_paged_decode_noalloc: hipGetDevice")) return rc;
   if (dev < 0 || dev >= kMaxDevices) {
@@ -3217,10 +3229,21 @@ int scratch_for_current_device(void** out) {
     if (int rc = check_hip(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)),
                            "prism_paged_decode_noalloc: hipGetSymbolAddress"))
       return rc;
+    hipEvent_t ev = nullptr;
+    if (int rc = check_hip(hipEventCreateWithFlags(&ev, hipEventDisableTiming),
+                           "prism_paged_decode_noalloc: hipEventCreateWithFlags"))
+      return rc;
+    g_scratch_use[dev].done = ev;
     g_scratch_ptr[dev] = p;
   }
   *out = g_scratch_ptr[dev];
+  *device = dev;
   return PRISM_OK;
+}
+
+bool stream_capturing(hipStream_t stream) {
+  hipStreamCaptureStatus st = hipStreamCaptureStatusNone;
+  return hipStreamIsCapturing(stream, &st) == hipSuccess && st != hipStreamCaptureStatusNone;
 }
 
 }  // namespace
@@ -3251,17 +3274,41 @@ extern "C" int prism_paged_decode_noalloc(const void* q, int q_dtype, const int6
     return PRISM_ERR_INVALID;
   }
   void* ws = nullptr;
-  if (need > 0) {
-    if (int rc = scratch_for_current_device(&ws)) return rc;
+  if (need == 0)  // no kernel of this geometry uses a workspace
+    return prism_paged_decode_stage(0, q, q_dtype, q_strides, k_cache, v_cache, cache_dtype, k_strides, v_strides,
+                                    k_scale, v_scale, ks_strides, vs_strides, block_tables, bt_strides,
+                                    context_lens, max_context_len, out, out_strides, batch, num_heads, num_kv_heads,
+                                    head_dim, page_size, num_blocks, max_blocks_per_seq, scale, nullptr, 0, stream);
+  int dev = 0;
+  if (int rc = scratch_for_current_device(&ws, &dev)) return rc;
+  hipStream_t hs = static_cast<hipStream_t>(stream);
+  // Launches under graph capture are not guarded (the replay's timing is the
+  // caller's): the guard sees eager calls only.
+  const bool guarded = !stream_capturing(hs);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);  // one host thread at a time per process
+  ScratchUse& use = g_scratch_use[dev];
+  if (guarded && use.recorded && use.stream != hs) {
+    const hipError_t q_st = hipEventQuery(use.done);
+    if (q_st == hipErrorNotReady) {
+      set_error("prism_paged_decode_noalloc: the device's scratch is in use by a call still running on another "
+                "stream; serialise the calls (or use prism_paged_decode with a workspace per stream)");
+      return PRISM_ERR_BUSY;
+    }
+    if (int rc = check_hip(q_st, "prism_paged_decode_noalloc: hipEventQuery")) return rc;
   }
   // Nothing in the scratch needs clearing: the streaming plan carries the key
   // of the inputs it was computed from (a stale or zero plan is rebuilt, and
   // its rebuild zeroes the merge counters), split-K chunk counters carry the
   // epoch of their call (any other value counts as zero arrivals), and
   // partials are written before they are read.
-  return prism_paged_decode_stage(0, q, q_dtype, q_strides, k_cache, v_cache, cache_dtype, k_strides, v_strides,
-                                  k_scale, v_scale, ks_strides, vs_strides, block_tables, bt_strides, context_lens,
-                                  max_context_len, out, out_strides, batch, num_heads, num_kv_heads, head_dim,
-                                  page_size, num_blocks, max_blocks_per_seq, scale, ws, need > 0 ? need : 0,
-                                  stream);
+  const int rc = prism_paged_decode_stage(0, q, q_dtype, q_strides, k_cache, v_cache, cache_dtype, k_strides,
+                                          v_strides, k_scale, v_scale, ks_strides, vs_strides, block_tables,
+                                          bt_strides, context_lens, max_context_len, out, out_strides, batch,
+                                          num_heads, num_kv_heads, head_dim, page_size, num_blocks,
+                                          max_blocks_per_seq, scale, ws, need, stream);
+  if (rc != PRISM_OK || !guarded) return rc;
+  if (int e = check_hip(hipEventRecord(use.done, hs), "prism_paged_decode_noalloc: hipEventRecord")) return e;
+  use.stream = hs;
+  use.recorded = true;
+  return PRISM_OK;
 }

@@ -69,6 +69,7 @@ SIGNATURES: dict[str, tuple] = {
     "prism_compact_slots_workspace_bytes": (_I64, [_I64, _I64, _I64, _I64]),
     "prism_compact_slots": (_I, [_VP, _I64, _I64, _I64, _VP, _VP, _I64, _VP, _I64, _VP]),
     "prism_copy_blocks": (_I, [_VP, _VP, _I64, _I64, _I64, _I64, _I64, _I64, _I64P, _I64P, _I64, _VP]),
+    "prism_device_copy": (_I, [_VP, _VP, _I64, _I, _VP]),
     "prism_paged_prefill": (
         _I,
         [_VP, _I, _I64P, _VP, _VP, _I, _I64P, _I64P, _VP, _VP, _I64P, _I64P, _VP, _I64P, _VP, _VP, _VP,

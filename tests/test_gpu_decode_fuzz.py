@@ -31,12 +31,13 @@ FP8 = torch.float8_e4m3fn
 MAX_POOL_TOKENS = 96 * 1024
 
 
-def _config(seed: int):
+def _config(seed: int, page: int | None = None):
     g = torch.Generator().manual_seed(20261130 + seed)
     pick = lambda xs: xs[int(torch.randint(len(xs), (1,), generator=g))]
     hkv = pick([1, 2, 4, 8, 8, 8])
     groups = pick([1, 2, 4, 4, 8])
-    page = pick([16, 32, 64, 256, 256])
+    drawn = pick([16, 32, 64, 256, 256])
+    page = drawn if page is None else page
     batch = int(torch.randint(1, 97, (1,), generator=g))
     max_len = max(1, min(int(torch.randint(1, 12000, (1,), generator=g)), MAX_POOL_TOKENS // batch - page))
     width = math.ceil(max_len / page) + 1
@@ -67,12 +68,16 @@ def _quantize(src):
     return k, s
 
 
-@pytest.mark.parametrize("seed", range(10))
-def test_random_decode_configs_all_families(seed, monkeypatch):
+@pytest.mark.parametrize("seed,page", [(s, None) for s in range(10)] + [(s, 128) for s in (10, 11, 16, 17, 20, 24, 31)])
+def test_random_decode_configs_all_families(seed, page, monkeypatch):
+    """Ten random geometries with the page size drawn from {16, 32, 64, 256},
+    and seven more at page size 128 (kv heads 1, 2, 4 and 8), a page size the
+    reference supports (config.py:46)."""
+
     require_gpu()
     from prism_infer.ops.paged_decode import paged_decode_attention
 
-    q, src_k, src_v, tables, lens = _config(seed)
+    q, src_k, src_v, tables, lens = _config(seed, page)
     k, ks = _quantize(src_k)
     v, vs = _quantize(src_v)
     scale = 128 ** -0.5

@@ -100,3 +100,38 @@ def test_no_alloc_rejects_oversized_geometry():
     status = lib.prism_paged_decode_noalloc(*args, _native.stream_handle(w.q.device))
     assert status != 0
     assert b"64" in lib.prism_last_error() or b"67108864" in lib.prism_last_error()
+
+
+def test_no_alloc_refuses_an_overlapping_call_on_another_stream():
+    """The scratch is shared per GPU: a call on stream B while stream A's call is still queued is refused
+    (PRISM_ERR_BUSY, nothing launched), a call on the same stream is accepted, and once A's call has
+    finished B's call runs and gives the workspace entry point's output."""
+
+    require_gpu()
+    from prism_infer import _native, workloads
+
+    dev = torch.device("cuda", 0)
+    w = workloads.decode_mixed(dev)
+    want = _with_workspace(w)
+    lib = _native.lib()
+    stream_a = torch.cuda.Stream(dev)
+    stream_b = torch.cuda.Stream(dev)
+    out_a = torch.full_like(w.q, float("nan"))
+    out_b = torch.full_like(w.q, float("nan"))
+    torch.cuda.synchronize()
+    with torch.cuda.stream(stream_a):
+        torch.cuda._sleep(200_000_000)  # keeps A's decode queued for tens of milliseconds
+        status_a = lib.prism_paged_decode_noalloc(*_args(w, out_a), stream_a.cuda_stream)
+        status_a2 = lib.prism_paged_decode_noalloc(*_args(w, out_a), stream_a.cuda_stream)
+    status_b = lib.prism_paged_decode_noalloc(*_args(w, out_b), stream_b.cuda_stream)
+    message = lib.prism_last_error()
+    torch.cuda.synchronize()
+    assert status_a == 0 and status_a2 == 0, "calls on one stream are ordered by it"
+    assert status_b == -4, f"expected PRISM_ERR_BUSY, got {status_b}"
+    assert b"in use" in message
+    assert bool(torch.isnan(out_b).all()), "the refused call launched nothing"
+    assert torch.equal(out_a, want)
+    status_b = lib.prism_paged_decode_noalloc(*_args(w, out_b), stream_b.cuda_stream)
+    torch.cuda.synchronize()
+    assert status_b == 0
+    assert torch.equal(out_b, want)
