@@ -897,7 +897,21 @@ __device__ __forceinline__ floatx4 lds_load_f4(uint32_t addr) {
   return *reinterpret_cast<const __attribute__((address_space(3))) floatx4*>(static_cast<uintptr_t>(addr));
 }
 
-__device__ __forceinline__ int stream_swz(int t) { return ((2 * t) + (t >> 2)) & 7; }
+// LDS layout of a tile row (16-byte chunks of 8 head slots of 128 bytes).
+// gfx950 LDS (measured with SQ_LDS_BANK_CONFLICT): 64 banks of 4 bytes
+// (address bits 2..7); ds_read_b64 (and _tr_b8) serves lanes 0-31 and 32-63
+// in separate passes; ds_read_b128 serves 16 lanes per pass, the lanes whose
+// bit 5 and parity of bits 2..4 agree.  A wave reads one head slot of every
+// row, 128 bytes, i.e. one half of the banks; so that rows of opposite
+// parity use opposite halves, LDS slot s of row t holds head slot
+// s ^ (t & 1) (stream_slot), and inside a slot the chunks are swizzled by
+// chunk ^= 4 t1 ^ 3 t2 (stream_swz, GF(2)-linear in the row index t).
+// Together they make the K rows' b128 reads (lane (g, c): row c, chunks 2g,
+// 2g + 1) and the V tiles' transposed b64 reads (lane (g, c): rows
+// 4g + (c >> 1 & 3), chunk 2 jp + (c >> 3)) conflict-free under that model
+// (the previous layout cost 4 and 2 extra cycles per read).
+__device__ __forceinline__ int stream_swz(int t) { return (((t >> 1) & 1) * 4) ^ (((t >> 2) & 1) * 3); }
+__device__ __forceinline__ int stream_slot(int h, int t) { return h ^ (t & 1); }
 
 
 
@@ -936,7 +950,7 @@ __device__ __forceinline__ StreamLanePlan stream_plan(int wave, int lane) {
     const int t = p >> 10;
     const int hh = (p >> 7) & 7;
     const int chunk = ((p >> 4) & 7) ^ stream_swz(t);
-    pl.goff[r] = t * kSRow + hh * kHeadDim + chunk * 16;
+    pl.goff[r] = t * kSRow + stream_slot(hh, t) * kHeadDim + chunk * 16;  // LDS slot hh holds this head slot
     pl.lk[r] = r * (kSThreads * 16) + wave * 1024;
   }
   // scales: waves 0/1 k, 2/3 v, 4-7 repeat 0-3 (same bytes, L2 hits) so
@@ -2158,7 +2172,7 @@ template <int QDT, bool QVEC, int TPR>
 __global__ void __launch_bounds__(kSThreads) __attribute__((amdgpu_waves_per_eu(2 * kSWgPerCu)))
 paged_decode_stream_kernel(const DecodeArgs a) {
   constexpr int kTTok = kSTile * TPR;  // tokens per tile
-  __shared__ __attribute__((aligned(16))) uint8_t stages[kSStages * kSStage];
+  __shared__ __attribute__((aligned(256))) uint8_t stages[kSStages * kSStage];
   __shared__ int tstart[kSMaxBatch + kSMaxVirt + 1];
   static_assert(sizeof(PlanLds) <= sizeof(stages), "the plan's LDS lies over the idle stages");
   const int lane = threadIdx.x & 63;
@@ -2352,8 +2366,8 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   float l_run = 0.f;        // this lane's share of the running sum
 
   // Per-lane LDS addresses inside stage 0 (loop invariant).
-  const uint32_t k_off0 = stage0 + c * kSRow + h * kHeadDim + (((2 * g) ^ stream_swz(c)) << 4);
-  const uint32_t k_off1 = stage0 + c * kSRow + h * kHeadDim + (((2 * g + 1) ^ stream_swz(c)) << 4);
+  const uint32_t k_off0 = stage0 + c * kSRow + stream_slot(h, c) * kHeadDim + (((2 * g) ^ stream_swz(c)) << 4);
+  const uint32_t k_off1 = stage0 + c * kSRow + stream_slot(h, c) * kHeadDim + (((2 * g + 1) ^ stream_swz(c)) << 4);
   const uint32_t s_off = stage0 + 2 * kSKBytes + (h * kSTile + 4 * g) * 4;
   uint32_t v_off[4];
   {
@@ -2363,7 +2377,8 @@ paged_decode_stream_kernel(const DecodeArgs a) {
 #pragma unroll
     for (int jp = 0; jp < 4; ++jp) {
       const int chunk = 2 * jp + (r >> 2);
-      v_off[jp] = stage0 + kSKBytes + t * kSRow + h * kHeadDim + ((chunk ^ stream_swz(t)) << 4) + half * 8;
+      v_off[jp] = stage0 + kSKBytes + t * kSRow + stream_slot(h, t) * kHeadDim + ((chunk ^ stream_swz(t)) << 4) +
+                  half * 8;
     }
   }
   // first token this lane's score rows refer to, relative to the tile:
