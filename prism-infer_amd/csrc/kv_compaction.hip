@@ -3,88 +3,85 @@
 // prism_infer/ops/kv_compaction.py:93-112: index_select(...).clone() then
 // index_copy_).
 //
-// The reference always stages through a temporary (two Triton passes,
-// :157-191).  Here the device decides per call whether staging is needed:
-//   1. clear a bitmap over all slots and a hazard flag (fill kernel; graph safe),
-//   2. mark every source slot in the bitmap,
-//   3. raise the flag if some entry writes a slot that is another entry's
-//      source (dst[i] marked and dst[i] != src[i]),
-//   4. copy: flag clear -> move bytes directly src -> dst (one pass);
-//            flag set   -> gather sources into the workspace,
-//   5. scatter (flag set only): workspace -> dst.
-// No host synchronisation; the flag lives in device memory.  Copies move 16
+// The reference always stages every slot through a temporary (two Triton
+// passes, :157-191).  Here the device decides per call whether staging is
+// needed, in four launches and no host synchronisation:
+//   1. mark: every source slot's tag (one uint32 per slot in the workspace)
+//      gets this call's epoch;
+//   2. detect: if some entry's destination is tagged (another entry's
+//      source; src == dst entries are no-ops), the hazard word gets the epoch;
+//   3. move: hazard word != epoch -> copy every entry src -> dst directly;
+//      otherwise gather the sources into the workspace's temporary;
+//   4. scatter (hazard word == epoch only): temporary -> destinations.
+// Nothing needs clearing: tags and the hazard word are compared with the
+// call's epoch, a value that differs from call to call and from the small
+// integers recycled memory often holds; a stale value that matches by chance
+// only makes the call stage, which gives the same bytes.  Copies move 16
 // bytes per lane when the row width allows it, 4 or 1 bytes otherwise.
 #include "common.h"
 
 #include <algorithm>
+#include <atomic>
 
 namespace prism {
 namespace {
 
 constexpr int kThreads = 256;
+constexpr int kMoveWgPerCu = 8;  // move workgroups per CU, over all rows
+constexpr int kMoveUnroll = 4;   // chunks in flight per lane
 
-struct CompactWorkspace {
-  uint32_t* bitmap;   // ceil(num_slots / 32) words
-  uint32_t* flag;     // [0] hazard flag
-  uint8_t* temp;      // rows * retained * vec_bytes
-};
-
-int64_t bitmap_words(int64_t num_slots) { return ceil_div(num_slots, 32); }
-
-int64_t workspace_layout(int64_t rows, int64_t num_slots, int64_t vec_bytes, int64_t retained,
-                         int64_t* flag_off, int64_t* temp_off) {
-  const int64_t bm = align_up(bitmap_words(num_slots) * 4, 256);
-  *flag_off = bm;
-  *temp_off = bm + 256;
+// Workspace: tags (one uint32 per slot), the hazard word, the temporary.
+int64_t workspace_layout(int64_t rows, int64_t num_slots, int64_t vec_bytes, int64_t retained, int64_t* flag_off,
+                         int64_t* temp_off) {
+  *flag_off = align_up(num_slots * 4, 256);
+  *temp_off = *flag_off + 256;
   return *temp_off + align_up(rows * retained * vec_bytes, 256);
 }
 
-__global__ void __launch_bounds__(kThreads) clear_words_kernel(uint32_t* __restrict__ words, int64_t n) {
-  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n;
-       i += static_cast<int64_t>(gridDim.x) * blockDim.x)
-    words[i] = 0u;
-}
-
-// Sources of one wave that fall in the same bitmap word (plans list kept
-// slots in runs, so a wave usually touches two or three words) are OR-ed
-// together first: one atomic per distinct word instead of one per entry.
-__global__ void __launch_bounds__(kThreads)
-mark_sources_kernel(const int64_t* __restrict__ src, int64_t retained, int64_t num_slots,
-                    uint32_t* __restrict__ bitmap) {
-  const int lane = lane_id();
-  const int64_t wave0 = (static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x) - lane;
-  for (int64_t base = wave0; base < retained; base += static_cast<int64_t>(gridDim.x) * blockDim.x) {
-    const int64_t i = base + lane;
-    const int64_t sl = i < retained ? src[i] : -1;
-    const bool valid = sl >= 0 && sl < num_slots;
-    const int64_t w = valid ? (sl >> 5) : -1;
-    const uint32_t bit = valid ? (1u << (sl & 31)) : 0u;
-    uint64_t todo = __builtin_amdgcn_ballot_w64(valid);
-    while (todo != 0) {  // wave-uniform loop
-      const int leader = __builtin_ctzll(todo);
-      const int64_t lw = __shfl(w, leader);
-      const bool mine = valid && w == lw;
-      uint32_t v = mine ? bit : 0u;
-#pragma unroll
-      for (int off = 32; off >= 1; off >>= 1) v |= __shfl_xor(v, off);
-      if (lane == leader) atomicOr(&bitmap[lw], v);
-      todo &= ~__builtin_amdgcn_ballot_w64(mine);
-    }
+// This call's tag value: a process-wide counter passed through a bijective
+// 32-bit mixer, so that consecutive calls' tags are far apart and unlike the
+// small integers recycled memory often holds (a tag that matches by chance
+// only costs staging); never 0.
+unsigned int next_compaction_epoch() {
+  static std::atomic<unsigned int> counter{0};
+  for (;;) {
+    uint32_t x = counter.fetch_add(1, std::memory_order_relaxed) + 0x9E3779B9u;
+    x ^= x >> 16;
+    x *= 0x7FEB352Du;
+    x ^= x >> 15;
+    x *= 0x846CA68Bu;
+    x ^= x >> 16;
+    if (x != 0u) return x;
   }
 }
 
 __global__ void __launch_bounds__(kThreads)
+mark_sources_kernel(const int64_t* __restrict__ src, int64_t retained, int64_t num_slots,
+                    uint32_t* __restrict__ tags, uint32_t epoch) {
+  for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < retained;
+       i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
+    const int64_t s = src[i];
+    if (s >= 0 && s < num_slots) tags[s] = epoch;
+  }
+}
+
+// Whether entry (s, d) moves anything.
+__device__ __forceinline__ bool entry_live(int64_t s, int64_t d, int64_t num_slots) {
+  return s >= 0 && s < num_slots && d >= 0 && d < num_slots && s != d;
+}
+
+__global__ void __launch_bounds__(kThreads)
 detect_hazard_kernel(const int64_t* __restrict__ src, const int64_t* __restrict__ dst, int64_t retained,
-                     int64_t num_slots, const uint32_t* __restrict__ bitmap, uint32_t* __restrict__ flag) {
+                     int64_t num_slots, const uint32_t* __restrict__ tags, uint32_t* __restrict__ flag,
+                     uint32_t epoch) {
   bool hazard = false;
   for (int64_t i = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < retained;
        i += static_cast<int64_t>(gridDim.x) * blockDim.x) {
     const int64_t s = src[i];
     const int64_t d = dst[i];
-    if (s < 0 || s >= num_slots || d < 0 || d >= num_slots || s == d) continue;
-    if ((bitmap[d >> 5] >> (d & 31)) & 1u) hazard = true;
+    if (entry_live(s, d, num_slots) && tags[d] == epoch) hazard = true;
   }
-  if (__any(hazard) && lane_id() == 0) atomicOr(flag, 1u);
+  if (__any(hazard) && lane_id() == 0) *flag = epoch;  // every writer stores the same value
 }
 
 // Element type used for the byte moves.
@@ -97,36 +94,35 @@ struct Chunk<4> { using T = uint32_t; };
 template <>
 struct Chunk<1> { using T = uint8_t; };
 
-// MODE 0: flag clear -> direct copy src -> dst; flag set -> gather src -> temp
-// MODE 2: scatter temp -> dst (only when the flag is set)
+// MODE 0: hazard word != epoch -> direct copy src -> dst; else gather src -> temp
+// MODE 2: scatter temp -> dst (only when the hazard word == epoch)
 //
 // Grid (x: chunk ranges, y: rows).  Chunk c of a row is part c & (U - 1) of
 // entry c >> USHIFT when a row vector holds U = 2^USHIFT chunks (every
 // canonical shape: token rows of 1024 or 32 bytes, whole blocks), else
-// c / U and c % U (USHIFT < 0).  Each thread moves four chunks per trip with
-// the four loads issued before the stores, and every byte is read and
+// c / U and c % U (USHIFT < 0).  Each thread moves kMoveUnroll chunks per
+// trip with all loads issued before the stores, and every byte is read and
 // written once, so both go through the non-temporal cache policy.
 template <int BYTES, int MODE>
 __global__ void __launch_bounds__(kThreads)
 compact_move_kernel(uint8_t* __restrict__ cache, int64_t num_slots, int64_t vec_bytes, int ushift,
                     const int64_t* __restrict__ src, const int64_t* __restrict__ dst, int64_t retained,
-                    uint8_t* __restrict__ temp, const uint32_t* __restrict__ flag) {
+                    uint8_t* __restrict__ temp, const uint32_t* __restrict__ flag, uint32_t epoch) {
   using T = typename Chunk<BYTES>::T;
-  const bool staged = *flag != 0u;
+  const bool staged = *flag == epoch;
   if (MODE == 2 && !staged) return;
   const int64_t chunks_per_vec = vec_bytes / BYTES;
   const int64_t per_row = retained * chunks_per_vec;
   const int64_t row = blockIdx.y;
   const int64_t row_base = row * num_slots;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
-  constexpr int kUnroll = 4;
   for (int64_t base = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; base < per_row;
-       base += kUnroll * stride) {
-    T val[kUnroll];
-    T* to[kUnroll];
-    bool ok[kUnroll];
+       base += kMoveUnroll * stride) {
+    T val[kMoveUnroll];
+    T* to[kMoveUnroll];
+    bool ok[kMoveUnroll];
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u) {
+    for (int u = 0; u < kMoveUnroll; ++u) {
       const int64_t c = base + u * stride;
       int64_t i, part;
       if (ushift >= 0) {
@@ -136,24 +132,18 @@ compact_move_kernel(uint8_t* __restrict__ cache, int64_t num_slots, int64_t vec_
         i = c / chunks_per_vec;
         part = c - i * chunks_per_vec;
       }
-      ok[u] = c < per_row;
-      const int64_t s = ok[u] ? src[i] : -1;
-      const int64_t d = ok[u] ? dst[i] : -1;
-      ok[u] = ok[u] && s >= 0 && s < num_slots && d >= 0 && d < num_slots;
-      const int64_t item = row * retained + i;
-      const T* from;
-      if (MODE == 0) {
-        from = reinterpret_cast<const T*>(cache + (row_base + s) * vec_bytes) + part;
-        to[u] = staged ? reinterpret_cast<T*>(temp + item * vec_bytes) + part
-                       : reinterpret_cast<T*>(cache + (row_base + d) * vec_bytes) + part;
-      } else {
-        from = reinterpret_cast<const T*>(temp + item * vec_bytes) + part;
-        to[u] = reinterpret_cast<T*>(cache + (row_base + d) * vec_bytes) + part;
-      }
+      const bool in = c < per_row;
+      const int64_t s = in ? src[i] : -1;
+      const int64_t d = in ? dst[i] : -1;
+      ok[u] = entry_live(s, d, num_slots);
+      T* tmp = reinterpret_cast<T*>(temp + (row * retained + i) * vec_bytes) + part;
+      T* direct = reinterpret_cast<T*>(cache + (row_base + d) * vec_bytes) + part;
+      const T* from = MODE == 0 ? reinterpret_cast<const T*>(cache + (row_base + s) * vec_bytes) + part : tmp;
+      to[u] = (MODE == 0 && staged) ? tmp : direct;
       if (ok[u]) val[u] = __builtin_nontemporal_load(from);
     }
 #pragma unroll
-    for (int u = 0; u < kUnroll; ++u)
+    for (int u = 0; u < kMoveUnroll; ++u)
       if (ok[u]) __builtin_nontemporal_store(val[u], to[u]);
   }
 }
@@ -165,9 +155,22 @@ int grid_for(int64_t work, int64_t cap) {
   return static_cast<int>(g);
 }
 
+// Launches both passes of one kernel family over the rows, in chunks of the
+// grid.y limit.
+template <typename Launch>
+int launch_passes(int64_t rows, Launch&& launch) {
+  for (int pass = 0; pass < 2; ++pass) {
+    for (int64_t r0 = 0; r0 < rows; r0 += 65535) {
+      launch(pass, r0, std::min<int64_t>(rows - r0, 65535));
+      if (int rc = check_launch(pass == 0 ? "compact move launch" : "compact scatter launch")) return rc;
+    }
+  }
+  return PRISM_OK;
+}
+
 template <int BYTES>
 int launch_moves(uint8_t* cache, int64_t rows, int64_t num_slots, int64_t vec_bytes, const int64_t* src,
-                 const int64_t* dst, int64_t retained, uint8_t* temp, const uint32_t* flag,
+                 const int64_t* dst, int64_t retained, uint8_t* temp, const uint32_t* flag, uint32_t epoch,
                  hipStream_t stream) {
   const int64_t chunks_per_vec = vec_bytes / BYTES;
   int ushift = -1;
@@ -176,30 +179,19 @@ int launch_moves(uint8_t* cache, int64_t rows, int64_t num_slots, int64_t vec_by
     while ((int64_t{1} << ushift) < chunks_per_vec) ++ushift;
   }
   const int64_t per_row = retained * chunks_per_vec;
-  // about 8 workgroups per CU in total, spread over the rows
-  const int64_t cap = std::max<int64_t>(1, device_cu_count() * 8 / std::max<int64_t>(rows, 1));
-  const int gx = grid_for(ceil_div(per_row, 4), cap);
-  for (int64_t r0 = 0; r0 < rows; r0 += 65535) {  // grid.y limit
-    const int64_t nr = std::min<int64_t>(rows - r0, 65535);
+  const int64_t cap = std::max<int64_t>(1, device_cu_count() * kMoveWgPerCu / std::max<int64_t>(rows, 1));
+  const int gx = grid_for(ceil_div(per_row, kMoveUnroll), cap);
+  return launch_passes(rows, [&](int pass, int64_t r0, int64_t nr) {
     uint8_t* c = cache + r0 * num_slots * vec_bytes;
     uint8_t* t = temp + r0 * retained * vec_bytes;
     const dim3 grid(gx, static_cast<unsigned>(nr));
-    hipLaunchKernelGGL((compact_move_kernel<BYTES, 0>), grid, dim3(kThreads), 0, stream, c, num_slots, vec_bytes,
-                       ushift, src, dst, retained, t, flag);
-    int rc = check_launch("compact copy/gather launch");
-    if (rc) return rc;
-  }
-  for (int64_t r0 = 0; r0 < rows; r0 += 65535) {
-    const int64_t nr = std::min<int64_t>(rows - r0, 65535);
-    uint8_t* c = cache + r0 * num_slots * vec_bytes;
-    uint8_t* t = temp + r0 * retained * vec_bytes;
-    const dim3 grid(gx, static_cast<unsigned>(nr));
-    hipLaunchKernelGGL((compact_move_kernel<BYTES, 2>), grid, dim3(kThreads), 0, stream, c, num_slots, vec_bytes,
-                       ushift, src, dst, retained, t, flag);
-    int rc = check_launch("compact scatter launch");
-    if (rc) return rc;
-  }
-  return PRISM_OK;
+    if (pass == 0)
+      hipLaunchKernelGGL((compact_move_kernel<BYTES, 0>), grid, dim3(kThreads), 0, stream, c, num_slots, vec_bytes,
+                         ushift, src, dst, retained, t, flag, epoch);
+    else
+      hipLaunchKernelGGL((compact_move_kernel<BYTES, 2>), grid, dim3(kThreads), 0, stream, c, num_slots, vec_bytes,
+                         ushift, src, dst, retained, t, flag, epoch);
+  });
 }
 
 }  // namespace
@@ -207,7 +199,8 @@ int launch_moves(uint8_t* cache, int64_t rows, int64_t num_slots, int64_t vec_by
 // Loads this file's code object now rather than at its first kernel launch.
 int preload_kv_compaction() {
   hipFuncAttributes attr;
-  return check_hip(hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&clear_words_kernel)), "preload_kv_compaction");
+  return check_hip(hipFuncGetAttributes(&attr, reinterpret_cast<const void*>(&mark_sources_kernel)),
+                   "preload_kv_compaction");
 }
 
 }  // namespace prism
@@ -248,30 +241,22 @@ extern "C" int prism_compact_slots(void* cache, int64_t rows, int64_t num_slots,
   }
   hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
   uint8_t* ws = static_cast<uint8_t*>(workspace);
-  uint32_t* bitmap = reinterpret_cast<uint32_t*>(ws);
+  uint32_t* tags = reinterpret_cast<uint32_t*>(ws);
   uint32_t* flag = reinterpret_cast<uint32_t*>(ws + flag_off);
   uint8_t* temp = ws + temp_off;
-  const int cap = device_cu_count() * 8;
-
-  // 1. clear bitmap and flag (the flag word sits right after the bitmap's
-  //    256-byte aligned extent, so one fill covers both).
-  const int64_t clear_words = flag_off / 4 + 1;
-  hipLaunchKernelGGL(clear_words_kernel, dim3(grid_for(clear_words, cap)), dim3(kThreads), 0, stream, bitmap,
-                     clear_words);
-  int rc = check_launch("compact clear launch");
-  if (rc) return rc;
-  // 2. mark sources, 3. detect hazards
-  hipLaunchKernelGGL(mark_sources_kernel, dim3(grid_for(retained, cap)), dim3(kThreads), 0, stream, src,
-                     retained, num_slots, bitmap);
-  if ((rc = check_launch("compact mark launch"))) return rc;
-  hipLaunchKernelGGL(detect_hazard_kernel, dim3(grid_for(retained, cap)), dim3(kThreads), 0, stream, src, dst,
-                     retained, num_slots, bitmap, flag);
-  if ((rc = check_launch("compact detect launch"))) return rc;
-  // 4./5. moves
+  const uint32_t epoch = next_compaction_epoch();
+  const int grid = grid_for(retained, device_cu_count() * 8);
+  // 1. mark the sources, 2. detect hazards
+  hipLaunchKernelGGL(mark_sources_kernel, dim3(grid), dim3(kThreads), 0, stream, src, retained, num_slots, tags, epoch);
+  if (int rc = check_launch("compact mark launch")) return rc;
+  hipLaunchKernelGGL(detect_hazard_kernel, dim3(grid), dim3(kThreads), 0, stream, src, dst, retained, num_slots, tags,
+                     flag, epoch);
+  if (int rc = check_launch("compact detect launch")) return rc;
+  // 3./4. move, then scatter when staged
   uint8_t* c = static_cast<uint8_t*>(cache);
   if (vec_bytes % 16 == 0 && aligned(cache, 16))
-    return launch_moves<16>(c, rows, num_slots, vec_bytes, src, dst, retained, temp, flag, stream);
+    return launch_moves<16>(c, rows, num_slots, vec_bytes, src, dst, retained, temp, flag, epoch, stream);
   if (vec_bytes % 4 == 0 && aligned(cache, 4))
-    return launch_moves<4>(c, rows, num_slots, vec_bytes, src, dst, retained, temp, flag, stream);
-  return launch_moves<1>(c, rows, num_slots, vec_bytes, src, dst, retained, temp, flag, stream);
+    return launch_moves<4>(c, rows, num_slots, vec_bytes, src, dst, retained, temp, flag, epoch, stream);
+  return launch_moves<1>(c, rows, num_slots, vec_bytes, src, dst, retained, temp, flag, epoch, stream);
 }

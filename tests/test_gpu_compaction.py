@@ -97,3 +97,44 @@ def test_identity_and_odd_widths():
     assert torch.equal(got, cache)
     got, want = _compact_both(cache, src, torch.tensor([0, 1, 2], dtype=torch.long))
     assert _bytes_equal(got, want)
+
+
+@pytest.mark.parametrize("vec", ["payload", "scales"])
+def test_arbitrary_workspace_contents(vec):
+    """The workspace is never cleared: the source tags and the hazard word are compared with the call's
+    epoch.  Tags holding every small integer (what recycled memory often holds) and a random hazard word
+    give the same bytes as the oracle, on a plan with and without real overlaps."""
+
+    require_gpu()
+    from prism_infer import _native
+
+    dev = torch.device("cuda")
+    g = torch.Generator().manual_seed(20261212)
+    slots = 4096
+    shape = (2, 3, slots, 8) if vec == "scales" else (2, 3, slots, 8, 128)
+    cache = torch.randint(0, 256, shape, generator=g, dtype=torch.uint8)
+    if vec == "payload":
+        cache = cache.view(FP8)
+    else:
+        cache = cache.view(torch.float32)
+    lib = _native.lib()
+    for overlap in (False, True):
+        src = torch.randperm(slots, generator=g)[:1500]
+        dst = torch.randperm(slots, generator=g)[:1500] if overlap else torch.arange(2500, 4000)
+        if not overlap:
+            src = torch.randperm(2500, generator=g)[:1500]
+        want = cache.clone()
+        oracle.compact_slots(want, src, dst)
+        gpu = cache.view(torch.uint8).to(dev).view(cache.dtype)
+        rows, vec_bytes = 6, (cache[0, 0, 0].numel() * cache.element_size())
+        need = lib.prism_compact_slots_workspace_bytes(rows, slots, vec_bytes, src.numel())
+        ws = torch.zeros(need, dtype=torch.uint8, device=dev)
+        tags = ws[: slots * 4].view(torch.int32)
+        tags.copy_(torch.arange(1, slots + 1, dtype=torch.int32, device=dev) % 4096)  # every small integer
+        ws[slots * 4: slots * 4 + 256].copy_(torch.randint(0, 256, (256,), generator=g, dtype=torch.uint8).to(dev))
+        s_dev, d_dev = src.to(dev), dst.to(dev)
+        status = lib.prism_compact_slots(gpu.data_ptr(), rows, slots, vec_bytes, s_dev.data_ptr(), d_dev.data_ptr(),
+                                         src.numel(), ws.data_ptr(), need, _native.stream_handle(dev))
+        _native.check(status, "prism_compact_slots")
+        torch.cuda.synchronize()
+        assert _bytes_equal(gpu.cpu(), want), f"{vec} overlap={overlap}"
