@@ -1289,6 +1289,64 @@ __device__ __forceinline__ int stream_owner_count(int first, int end, int total,
   return static_cast<int>(split_owner(sp, end - 1) - split_owner(sp, first)) + 1;
 }
 
+// Cost-weighted split.  Workgroup ranges are equal in cost units rather than
+// tiles: a tile of a sequence's own pages costs kCostTile, a tile of a
+// virtual walk (shared pages, which the other walks of its group have pulled
+// into the caches) kCostVirt, and every stream entry kCostEntry more (a range
+// that starts an entry reloads the query and its first pages' metadata, and
+// one that ends an entry flushes a partial).  Entry i occupies cost positions
+// [cs(i), cs(i + 1)), its first kCostEntry positions charged to whichever
+// range holds them, then its tiles; a tile belongs to the range holding its
+// first position.  The weights apply when the stream has at least
+// kCostMinTilesPerWg tiles per workgroup, so that every range still holds
+// tiles; otherwise every weight is the unit one and the split is the plain
+// tile split.  Measured on the batch-64 mixed step (8 kv heads, 256
+// workgroups, about 124 tiles each): entry costs of 0 / 1 / 2 / 3 / 4 / 6 / 8
+// / 12 tiles gave 176.0 / 174.9 / 174.5 / 173.6 / 173.6 / 172.2 / 171.9 /
+// 172.6 us, and virtual tiles at 22/16 of a tile 171.1 us (at 13/16: 188 us;
+// a walk of shared pages is followed by merges over its 4 members' outputs).
+// Before the weights, a workgroup meeting two entries ended its loop 2.6 us
+// after one meeting one, and the last loops ended 7 us after the mean.
+#ifndef PRISM_COST_ENTRY
+#define PRISM_COST_ENTRY 128
+#endif
+#ifndef PRISM_COST_VIRT
+#define PRISM_COST_VIRT 22
+#endif
+constexpr int kCostTile = 16;
+constexpr int kCostEntry = PRISM_COST_ENTRY;
+constexpr int kCostVirt = PRISM_COST_VIRT;
+constexpr int kCostMinTilesPerWg = 4;
+// (An entry's first kCostEntry positions may fill a whole range, which then
+// holds no tile and flushes nothing; the merges only visit the ranges that
+// meet an entry's tile positions, and each of those holds a tile start, as a
+// weighted range spans at least kCostTile * kCostMinTilesPerWg positions.)
+static_assert(kCostVirt >= 1 && kCostVirt <= kCostTile * kCostMinTilesPerWg, "a tile fits a range");
+
+struct CostModel {
+  int ce, cv, cr;  // per entry, per virtual tile, per real tile
+  int V;           // virtual entries come first
+  int tv;          // tiles of all virtual entries (tile prefix at entry V)
+};
+
+__device__ __forceinline__ CostModel cost_model(int tiles, int nwg, int V, int tv) {
+  const bool weighted = static_cast<int64_t>(tiles) >= static_cast<int64_t>(kCostMinTilesPerWg) * nwg;
+  return weighted ? CostModel{kCostEntry, kCostVirt, kCostTile, V, tv} : CostModel{0, 1, 1, V, tv};
+}
+
+// Cost position where entry i starts, from its tile prefix ti (entries before
+// V are virtual).
+__device__ __forceinline__ int64_t cost_start(const CostModel& m, int i, int ti) {
+  const int64_t c = static_cast<int64_t>(m.ce) * i;
+  return i <= m.V ? c + static_cast<int64_t>(m.cv) * ti
+                  : c + static_cast<int64_t>(m.cv) * m.tv + static_cast<int64_t>(m.cr) * (ti - m.tv);
+}
+
+// Cost position of tile k of entry i.
+__device__ __forceinline__ int64_t cost_of_tile(const CostModel& m, int i, int ti, int k) {
+  return cost_start(m, i, ti) + m.ce + static_cast<int64_t>(i < m.V ? m.cv : m.cr) * k;
+}
+
 // Inclusive prefix sum over the workgroup of NT threads (every thread calls
 // it): shuffles within each wave, one pass over the wave totals.
 template <int NT>
@@ -1626,6 +1684,8 @@ __device__ void plan_build(const DecodeArgs& a, int* plan, PlanLds& L, int* tst_
     carry += chunk_total;
   }
   __syncthreads();
+  const CostModel cm = cost_model(carry, a.stream_nwg, V, tst_s[V]);
+  const int64_t ctotal = cost_start(cm, NS, carry);  // cost positions of the whole stream
   // ---- write-out
   for (int i = tid; i <= NS; i += NT) plan[kPlanTstart + i] = tst_s[i];
   for (int b = tid; b < B; b += NT) {
@@ -1633,10 +1693,18 @@ __device__ void plan_build(const DecodeArgs& a, int* plan, PlanLds& L, int* tst_
     plan[kPlanVslot + b] = L.vslot_s[b];
     const int vs = L.vslot_s[b];
     const int v = vs >= 0 ? vs / kSCols : 0;
-    const int first = tst_s[V + b], end = tst_s[V + b + 1];
-    const int vfirst = vs >= 0 ? tst_s[v] : 0, vend = vs >= 0 ? tst_s[v + 1] : 0;
-    const int expect = stream_owner_count(first, end, carry, a.stream_nwg) +
-                       stream_owner_count(vfirst, vend, carry, a.stream_nwg);
+    // each tile range as [cost position of its first tile, that of its last + 1)
+    int first = 0, end = 0, vfirst = 0, vend = 0;
+    if (tst_s[V + b + 1] > tst_s[V + b]) {
+      first = static_cast<int>(cost_of_tile(cm, V + b, tst_s[V + b], 0));
+      end = static_cast<int>(cost_of_tile(cm, V + b, tst_s[V + b], tst_s[V + b + 1] - tst_s[V + b] - 1)) + 1;
+    }
+    if (vs >= 0 && tst_s[v + 1] > tst_s[v]) {
+      vfirst = static_cast<int>(cost_of_tile(cm, v, tst_s[v], 0));
+      vend = static_cast<int>(cost_of_tile(cm, v, tst_s[v], tst_s[v + 1] - tst_s[v] - 1)) + 1;
+    }
+    const int expect = stream_owner_count(first, end, static_cast<int>(ctotal), a.stream_nwg) +
+                       stream_owner_count(vfirst, vend, static_cast<int>(ctotal), a.stream_nwg);
     int4* rec = reinterpret_cast<int4*>(plan + kPlanRec + 8 * b);
     rec[0] = int4{first, end, vs, vfirst};
     rec[1] = int4{vend, expect, 0, 0};
@@ -1656,13 +1724,26 @@ __device__ void plan_build(const DecodeArgs& a, int* plan, PlanLds& L, int* tst_
   }
   if (tid == 0) {  // copies of the plan header, checked before the plan is reused
     plan[kPlanKey + kPlanKeyParams - 2] = V;
-    plan[kPlanKey + kPlanKeyParams - 1] = carry;
+    plan[kPlanKey + kPlanKeyParams - 1] = static_cast<int>(ctotal);
   }
   for (int b = tid; b < B; b += NT) plan[kPlanKeyEff + b] = L.eff_s[b];
   for (int i = tid; i < items; i += NT) plan[kPlanKeyBt + i] = L.bt_s[i];
+  // the first tile at or after cost position c (carry past the end)
+  auto tile_at = [&](int64_t c) -> int {
+    int lo = 0, hi = NS - 1;  // the last entry starting at or before c
+    while (lo < hi) {
+      const int mid = (lo + hi + 1) >> 1;
+      if (cost_start(cm, mid, tst_s[mid]) <= c) lo = mid;
+      else hi = mid - 1;
+    }
+    const int64_t rel = c - cost_start(cm, lo, tst_s[lo]) - cm.ce;
+    const int step = lo < V ? cm.cv : cm.cr;
+    const int64_t k = rel <= 0 ? 0 : (rel + step - 1) / step;
+    return tst_s[lo] + static_cast<int>(min(k, static_cast<int64_t>(tst_s[lo + 1] - tst_s[lo])));
+  };
   for (int w = tid; w < a.stream_nwg; w += NT) {
-    const int64_t s0 = static_cast<int64_t>(w) * carry / a.stream_nwg;
-    const int64_t s1 = static_cast<int64_t>(w + 1) * carry / a.stream_nwg;
+    const int s0 = NS > 0 ? tile_at(static_cast<int64_t>(w) * ctotal / a.stream_nwg) : 0;
+    const int s1 = NS > 0 ? tile_at(static_cast<int64_t>(w + 1) * ctotal / a.stream_nwg) : 0;
     int4 r0 = {-1, 0, 0, 0}, r1 = {0, 0, 0, kNoBlock};
     if (s0 < s1) {
       // the entry holding tile s0: the last i with tst_s[i] <= s0
@@ -1690,7 +1771,7 @@ __device__ void plan_build(const DecodeArgs& a, int* plan, PlanLds& L, int* tst_
       const int lr = ilt + rot;
       const int t0 = tok0 + (lr >= intl ? lr - intl : lr) * a.s_ttok;
       const int page = t0 / P;
-      r0 = int4{i, ilt, intl, bt_row};
+      r0 = int4{i, ilt, s1 - s0, bt_row};  // entry, tile within it, tiles of the range, block-table row
       r1 = int4{tok0, n_end, rot, (share && page < Wc) ? L.bt_s[bt_row * Wc + page] : kNoBlock};
     }
     int4* rec = reinterpret_cast<int4*>(plan + kPlanWgRec + 8 * w);
@@ -1699,7 +1780,7 @@ __device__ void plan_build(const DecodeArgs& a, int* plan, PlanLds& L, int* tst_
   }
   if (tid == 0) {
     plan[0] = V;
-    plan[1] = carry;
+    plan[1] = static_cast<int>(ctotal);
   }
 }
 
@@ -2241,11 +2322,9 @@ paged_decode_stream_kernel(const DecodeArgs a) {
     __syncthreads();
   }
   const int NS = B + V;
-  const StreamSplit sp = stream_split(a, total);
-  const int64_t s = split_begin(sp, blockIdx.x);
-  const int64_t e = split_begin(sp, blockIdx.x + 1);
+  const int count = __builtin_amdgcn_readfirstlane(wr0.x) < 0 ? 0 : __builtin_amdgcn_readfirstlane(wr0.z);
   __syncthreads();
-  if (s >= e) {  // uniform: an empty range flushes nothing
+  if (count == 0) {  // uniform: an empty range flushes nothing
     stream_finish<QDT, TPR>(a, plan, V, total, tstart, 0, 0, reinterpret_cast<int*>(stages));
     return;
   }
@@ -2253,7 +2332,6 @@ paged_decode_stream_kernel(const DecodeArgs a) {
 
   const StreamLanePlan pl = stream_plan(h, lane);
   const uint32_t stage0 = lds_addr(stages);
-  const int count = static_cast<int>(e - s);
   const int P = a.page_size;
   const int tpp = P / kTTok;  // tiles per page (the streaming shape has P % kTTok == 0)
   // unit-scale FP8 caches (no scale tensors): every stage still issues its
@@ -2350,7 +2428,8 @@ paged_decode_stream_kernel(const DecodeArgs a) {
 
   // ---- compute side: entry b, tiles left in it for this workgroup
   int b = __builtin_amdgcn_readfirstlane(wr0.x);
-  int cleft = min(__builtin_amdgcn_readfirstlane(wr0.z) - __builtin_amdgcn_readfirstlane(wr0.y), count);
+  int cleft = min(__builtin_amdgcn_readfirstlane(tstart[b + 1] - tstart[b]) - __builtin_amdgcn_readfirstlane(wr0.y),
+                  count);
   QOperandF8 qop;
   bool colv;
   {
