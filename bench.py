@@ -421,7 +421,7 @@ def main() -> int:
 
     if not args.no_extras:
         result["decode_step_graph"] = _graph_steps(step, 36, outs, alg_bytes, torch)
-        result["decode_tp_shards"] = {f"tp{tp}": _tp_shard(base, torch, tp) for tp in (2, 4, 8)}
+        result["decode_tp_shards"] = {f"tp{tp}": _tp_shard(layers, torch, tp) for tp in (2, 4, 8)}
         result["extras"] = _extras(torch, dev, workloads)
     del layers, outs, ws
     torch.cuda.empty_cache()
@@ -460,11 +460,14 @@ def _check_long_sample(lw, out, torch) -> dict:
             "within_tolerance": bool(torch.all(err <= bound))}
 
 
-def _tp_shard(base, torch, tp: int, steps: int = 50) -> dict:
+def _tp_shard(layers, torch, tp: int, steps: int = 50) -> dict:
     """One tensor-parallel rank's share of the headline step at TP = tp: the
     same sequences and pages with the first 8 / tp of the 8 kv heads (a
-    contiguous cache of that many heads, Hq = 32 / tp), plan check + streaming
-    kernel + merge per step, warm, eager, no layer rotation."""
+    contiguous cache of that many heads, Hq = 32 / tp), one streaming launch
+    per step.  Timed as the headline is: the steps rotate over the rotated
+    layer pools' shards (each step reads a shard the previous steps did not),
+    HIP events around `steps` eager steps; `warm_us_per_layer` repeats one
+    pool's shard (at TP 8 a shard is 125 MB, which the 256 MB MALL holds)."""
 
     from prism_infer import _native  # noqa: PLC0415
     from prism_infer.ops.paged_decode import (  # noqa: PLC0415
@@ -472,28 +475,35 @@ def _tp_shard(base, torch, tp: int, steps: int = 50) -> dict:
         decode_workspace_bytes,
     )
 
+    base = layers[0]
     hkv, hq = 8 // tp, 32 // tp
     q = base.q[:, :hq].contiguous()
-    k, v = base.k_cache[:, :, :hkv].contiguous(), base.v_cache[:, :, :hkv].contiguous()
-    ks, vs = base.k_scale[:, :, :hkv].contiguous(), base.v_scale[:, :, :hkv].contiguous()
-    ws = torch.empty(decode_workspace_bytes(q, k, base.block_tables), dtype=torch.uint8, device=q.device)
+    shards = [tuple(t[:, :, :hkv].contiguous() for t in (w.k_cache, w.v_cache, w.k_scale, w.v_scale)) for w in layers]
+    ws = torch.empty(decode_workspace_bytes(q, shards[0][0], base.block_tables), dtype=torch.uint8, device=q.device)
     out = torch.empty_like(q)
-    call = lambda i, stage=0: _launch_paged_decode_attention(  # noqa: E731
-        q, k, v, base.block_tables, base.context_lens, base.scale, base.max_context_len, k_scale_cache=ks,
-        v_scale_cache=vs, scaled_kv=True, stage=stage, output=out, workspace=ws)
+
+    def call(i, stage=0, rotate=True):
+        k, v, ks, vs = shards[i % len(shards)] if rotate else shards[0]
+        _launch_paged_decode_attention(q, k, v, base.block_tables, base.context_lens, base.scale,
+                                       base.max_context_len, k_scale_cache=ks, v_scale_cache=vs, scaled_kv=True,
+                                       stage=stage, output=out, workspace=ws)
+
     for i in range(steps):
         call(i)
     s = _time_loop(call, steps, torch)
     kernel = _time_loop(lambda i: call(i, 1), steps, torch)
+    warm = _time_loop(lambda i: call(i, 0, False), steps, torch)
     family = _native.lib().prism_paged_decode_kernel_family(base.batch, hq, hkv, 128, 256, base.block_tables.shape[1],
                                                             3)
+    k, v, ks, vs = shards[0]
     shard = type(base)(**{**base.__dict__, "q": q, "k_cache": k, "v_cache": v, "k_scale": ks, "v_scale": vs})
     shard_bytes = shard.algorithmic_bytes()
-    del k, v, ks, vs, ws, shard
+    del shards, ws, shard
     return {"us_per_layer": round(s * 1e6, 2), "GBps": round(shard_bytes / s / 1e9, 1),
             "pct_of_hbm_peak": round(100.0 * shard_bytes / s / 1e9 / HBM_PEAK_GBPS, 2),
-            "kernel_us": round(kernel * 1e6, 2), "kernel_family": int(family), "kv_heads": hkv, "q_heads": hq,
-            "timing": "warm, eager, HIP events"}
+            "kernel_us": round(kernel * 1e6, 2), "warm_us_per_layer": round(warm * 1e6, 2),
+            "kernel_family": int(family), "kv_heads": hkv, "q_heads": hq, "layers_rotated": len(layers),
+            "timing": "eager, HIP events, steps rotating over the layer pools' shards as the headline does"}
 
 
 def _graph_steps(step, n_layers: int, outs, alg_bytes: int, torch, reps: int = 8, warm: int = 6) -> dict:
