@@ -910,6 +910,24 @@ __device__ __forceinline__ floatx4 lds_load_f4(uint32_t addr) {
 // 2g + 1) and the V tiles' transposed b64 reads (lane (g, c): rows
 // 4g + (c >> 1 & 3), chunk 2 jp + (c >> 3)) conflict-free under that model
 // (the previous layout cost 4 and 2 extra cycles per read).
+// Eight 16-bit transposed reads at the addresses ad[i] + off, one wait.
+__device__ __forceinline__ void lds_read_tr16_x8(const uint32_t (&ad)[8], uint32_t off, uint64_t (&o)[8]) {
+  asm volatile(
+      "ds_read_b64_tr_b16 %0, %8\n\t"
+      "ds_read_b64_tr_b16 %1, %9\n\t"
+      "ds_read_b64_tr_b16 %2, %10\n\t"
+      "ds_read_b64_tr_b16 %3, %11\n\t"
+      "ds_read_b64_tr_b16 %4, %12\n\t"
+      "ds_read_b64_tr_b16 %5, %13\n\t"
+      "ds_read_b64_tr_b16 %6, %14\n\t"
+      "ds_read_b64_tr_b16 %7, %15\n\t"
+      "s_waitcnt lgkmcnt(0)"
+      : "=&v"(o[0]), "=&v"(o[1]), "=&v"(o[2]), "=&v"(o[3]), "=&v"(o[4]), "=&v"(o[5]), "=&v"(o[6]), "=&v"(o[7])
+      : "v"(ad[0] + off), "v"(ad[1] + off), "v"(ad[2] + off), "v"(ad[3] + off), "v"(ad[4] + off), "v"(ad[5] + off),
+        "v"(ad[6] + off), "v"(ad[7] + off)
+      : "memory");
+}
+
 __device__ __forceinline__ int stream_swz(int t) { return (((t >> 1) & 1) * 4) ^ (((t >> 2) & 1) * 3); }
 __device__ __forceinline__ int stream_slot(int h, int t) { return h ^ (t & 1); }
 
@@ -1028,6 +1046,85 @@ __device__ __forceinline__ void stream_issue(const StreamLanePlan& pl, const uin
 }
 #undef PRISM_STREAM_ISSUE_ASM
 
+// ---- 16-bit caches (bf16 or f16 of the query's dtype, no scales; 8 kv
+// heads).  A token row is 8 head slots of 256 bytes (2 KB) and a tile is
+// still 16 tokens: 32 KB of K and 32 KB of V, so a stage is 64 KB and the
+// workgroup keeps two stages (one tile in flight while one is computed).
+// Inside a head slot the 16-byte chunks are swizzled by chunk ^= 8 t0 ^ 5 t1
+// ^ 2 t2 (t the token in the tile): under the LDS model above this makes the
+// K reads (lane (g, c): token c, chunks 4g .. 4g + 3, b128) and the
+// transposed V reads (lane j of group g: token 4g + (j >> 2), 8 bytes at
+// 32 nt + 8 (j & 3), b64_tr_b16) conflict-free; a 256-byte slot spans every
+// bank, so no slot permutation is needed.
+constexpr int kS16Row = kSKv * kHeadDim * 2;  // 2048 bytes per token row
+constexpr int kS16KBytes = kSTile * kS16Row;  // 32 KB of K per tile
+constexpr int kS16Stage = 2 * kS16KBytes;     // K then V
+constexpr int kS16Stages = 2;
+constexpr int kS16LoadsPerStage = 8;          // per lane: 4 K, 4 V
+static_assert(kS16Stages * kS16Stage <= kSStages * kSStage, "the 16-bit stages fit the stage buffer");
+
+__device__ __forceinline__ int stream_swz16(int t) {
+  return ((t & 1) * 8) ^ (((t >> 1) & 1) * 5) ^ (((t >> 2) & 1) * 2);
+}
+
+// Per-lane offsets of a 16-bit tile's loads (the same for K and V): load r of
+// wave w fills LDS bytes [8 KB r + 1 KB w, +1 KB) of the K (or V) slab.
+struct StreamLanePlan16 {
+  int32_t goff[4];  // byte offset of this lane's chunk inside the tile slab
+  uint32_t lk[4];   // LDS offset (from the stage base) of the wave's kilobyte
+};
+
+__device__ __forceinline__ StreamLanePlan16 stream_plan16(int wave, int lane) {
+  StreamLanePlan16 pl;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int p = r * (kSThreads * 16) + wave * 1024 + lane * 16;  // byte in the LDS slab
+    const int t = p >> 11;
+    const int hh = (p >> 8) & 7;
+    const int chunk = ((p >> 4) & 15) ^ stream_swz16(t);
+    pl.goff[r] = t * kS16Row + hh * (2 * kHeadDim) + chunk * 16;
+    pl.lk[r] = r * (kSThreads * 16) + wave * 1024;
+  }
+  return pl;
+}
+
+#define PRISM_STREAM16_ISSUE_ASM(POL)                                                     \
+  "s_mov_b32 m0, %[lk0]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[g0], %[kb]" POL "\n\t"   \
+  "s_mov_b32 m0, %[lk1]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[g1], %[kb]" POL "\n\t"   \
+  "s_mov_b32 m0, %[lk2]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[g2], %[kb]" POL "\n\t"   \
+  "s_mov_b32 m0, %[lk3]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[g3], %[kb]" POL "\n\t"   \
+  "s_mov_b32 m0, %[lv0]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[g0], %[vb]" POL "\n\t"   \
+  "s_mov_b32 m0, %[lv1]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[g1], %[vb]" POL "\n\t"   \
+  "s_mov_b32 m0, %[lv2]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[g2], %[vb]" POL "\n\t"   \
+  "s_mov_b32 m0, %[lv3]\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %[g3], %[vb]" POL
+
+__device__ __forceinline__ void stream_issue16(const StreamLanePlan16& pl, const uint8_t* kb, const uint8_t* vb,
+                                               uint32_t stage_lds, bool nt) {
+  kb = scalar_ptr(kb);
+  vb = scalar_ptr(vb);
+  const uint32_t lk0 = stage_lds + pl.lk[0], lk1 = stage_lds + pl.lk[1];
+  const uint32_t lk2 = stage_lds + pl.lk[2], lk3 = stage_lds + pl.lk[3];
+  const uint32_t lv0 = lk0 + kS16KBytes, lv1 = lk1 + kS16KBytes, lv2 = lk2 + kS16KBytes, lv3 = lk3 + kS16KBytes;
+  const uint32_t g0 = static_cast<uint32_t>(pl.goff[0]), g1 = static_cast<uint32_t>(pl.goff[1]);
+  const uint32_t g2 = static_cast<uint32_t>(pl.goff[2]), g3 = static_cast<uint32_t>(pl.goff[3]);
+  if (nt) {  // wave-uniform
+    asm volatile(PRISM_STREAM16_ISSUE_ASM(" nt")
+                 :
+                 : [g0] "v"(g0), [g1] "v"(g1), [g2] "v"(g2), [g3] "v"(g3), [kb] "s"(kb), [vb] "s"(vb),
+                   [lk0] "s"(lk0), [lk1] "s"(lk1), [lk2] "s"(lk2), [lk3] "s"(lk3), [lv0] "s"(lv0), [lv1] "s"(lv1),
+                   [lv2] "s"(lv2), [lv3] "s"(lv3)
+                 : "memory", "m0");
+  } else {
+    asm volatile(PRISM_STREAM16_ISSUE_ASM("")
+                 :
+                 : [g0] "v"(g0), [g1] "v"(g1), [g2] "v"(g2), [g3] "v"(g3), [kb] "s"(kb), [vb] "s"(vb),
+                   [lk0] "s"(lk0), [lk1] "s"(lk1), [lk2] "s"(lk2), [lk3] "s"(lk3), [lv0] "s"(lv0), [lv1] "s"(lv1),
+                   [lv2] "s"(lv2), [lv3] "s"(lv3)
+                 : "memory", "m0");
+  }
+}
+#undef PRISM_STREAM16_ISSUE_ASM
+
 // Query operand of one wave: column c (0..15) holds one query vector.
 template <int QDT, bool QVEC>
 __device__ __forceinline__ void stream_load_q(const DecodeArgs& a, int qrow, int qhead, bool qvalid, int g,
@@ -1092,6 +1189,38 @@ struct QOperandF8 {
   i32x8 t[3];      // hi, mid, lo
   float colscale;  // scale_log2 * 2^-e of this lane's column
 };
+
+// B operand of S^T = K Q^T for 16-bit caches (bf16 / f16 MFMA 16x16x32):
+// lane (g, c) holds query column c's dims 32g + 8kb .. 32g + 8kb + 7 for MFMA
+// kb, the dims of the K chunk 4g + kb it meets.
+struct QOperand16 {
+  u32x4 t[4];
+  float colscale;  // scale_log2
+};
+
+template <int QDT, bool QVEC>
+__device__ __forceinline__ void stream_load_q16(const DecodeArgs& a, int qrow, int qhead, bool qvalid, int g,
+                                                QOperand16& qop) {
+  const int64_t qbase = static_cast<int64_t>(qrow) * a.q_sb + static_cast<int64_t>(qhead) * a.q_sh;
+  const uint16_t* q = static_cast<const uint16_t*>(a.q);
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) {
+    const int64_t d0 = 32 * g + 8 * kb;
+    u32x4 w = {0u, 0u, 0u, 0u};
+    if (qvalid) {
+      if constexpr (QVEC) {
+        w = *reinterpret_cast<const u32x4*>(q + qbase + d0);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+          w[e] = static_cast<uint32_t>(q[qbase + (d0 + 2 * e) * a.q_sd]) |
+                 (static_cast<uint32_t>(q[qbase + (d0 + 2 * e + 1) * a.q_sd]) << 16);
+      }
+    }
+    qop.t[kb] = w;
+  }
+  qop.colscale = a.scale_log2;
+}
 
 template <int QDT, bool QVEC>
 __device__ __forceinline__ void stream_load_q8(const DecodeArgs& a, int qrow, int qhead, bool qvalid, int g,
@@ -2249,10 +2378,16 @@ __device__ __forceinline__ void stream_give_up(const DecodeArgs& a) {
 }
 
 // kSWgPerCu 8-wave workgroups per CU need 2 * kSWgPerCu waves per SIMD.
-template <int QDT, bool QVEC, int TPR>
+template <int QDT, bool QVEC, int TPR, bool C16>
 __global__ void __launch_bounds__(kSThreads) __attribute__((amdgpu_waves_per_eu(2 * kSWgPerCu)))
 paged_decode_stream_kernel(const DecodeArgs a) {
+  static_assert(!C16 || (TPR == 1 && QDT != PRISM_DTYPE_F32), "16-bit tiles: 8 kv heads, 16-bit queries");
   constexpr int kTTok = kSTile * TPR;  // tokens per tile
+  // stage geometry: FP8 tiles (K, V, scales; four stages) or 16-bit tiles (K, V; two stages)
+  constexpr int kStg = C16 ? kS16Stages : kSStages;
+  constexpr int kStgBytes = C16 ? kS16Stage : kSStage;
+  constexpr int kRowB = C16 ? kS16Row : kSRow;
+  constexpr int kTileKB = C16 ? kS16KBytes : kSKBytes;
   __shared__ __attribute__((aligned(256))) uint8_t stages[kSStages * kSStage];
   __shared__ int tstart[kSMaxBatch + kSMaxVirt + 1];
   static_assert(sizeof(PlanLds) <= sizeof(stages), "the plan's LDS lies over the idle stages");
@@ -2331,6 +2466,7 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   const uint64_t t_begin = __builtin_amdgcn_s_memrealtime();
 
   const StreamLanePlan pl = stream_plan(h, lane);
+  const StreamLanePlan16 pl16 = stream_plan16(h, lane);
   const uint32_t stage0 = lds_addr(stages);
   const int P = a.page_size;
   const int tpp = P / kTTok;  // tiles per page (the streaming shape has P % kTTok == 0)
@@ -2363,8 +2499,8 @@ paged_decode_stream_kernel(const DecodeArgs a) {
     ivalid = raw >= 0 && raw < a.num_blocks;
     const int64_t blk = ivalid ? raw : 0;  // loads of an invalid block read page 0 and are skipped
     const int64_t tip_rows = static_cast<int64_t>(itip) * kSTile;
-    ikb = a.k + blk * a.k_sblk + tip_rows * kSRow;
-    ivb = a.v + blk * a.v_sblk + tip_rows * kSRow;
+    ikb = a.k + blk * a.k_sblk + tip_rows * kRowB;
+    ivb = a.v + blk * a.v_sblk + tip_rows * kRowB;
     isb = unscaled ? reinterpret_cast<const float*>(ikb) : sbase + blk * a.ks_sblk + tip_rows * kSKv;
   };
   auto ientry = [&](int lt, int first_raw) {
@@ -2391,10 +2527,12 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   auto issue_next = [&]() {
     const int nv = ivalid ? min(iend - it0, kTTok) : 0;
     stage_nv = (stage_nv & ~(0xFFu << (8 * istage))) | (static_cast<uint32_t>(nv) << (8 * istage));
-    if (!(PRISM_DBG(a) & 2))
-      stream_issue(pl, ikb, ivb, isb, stage0 + static_cast<uint32_t>(istage) * kSStage, iprivate);
+    if (!(PRISM_DBG(a) & 2)) {
+      if constexpr (C16) stream_issue16(pl16, ikb, ivb, stage0 + static_cast<uint32_t>(istage) * kStgBytes, iprivate);
+      else stream_issue(pl, ikb, ivb, isb, stage0 + static_cast<uint32_t>(istage) * kStgBytes, iprivate);
+    }
     ++issued;
-    istage = istage == kSStages - 1 ? 0 : istage + 1;
+    istage = istage == kStg - 1 ? 0 : istage + 1;
     if (issued == count) return;  // the range is done (no page past it is read)
     if (--ileft == 0) {  // the entry is done: the next one with tiles
       do {
@@ -2407,8 +2545,8 @@ paged_decode_stream_kernel(const DecodeArgs a) {
     ++ipt;
     it0 += kTTok;
     ++itip;
-    ikb += kSKBytes;
-    ivb += kSKBytes;
+    ikb += kTileKB;
+    ivb += kTileKB;
     isb += kSTile * kSKv;
     if (ipt == intl) {  // a rotated walk wraps to the entry's first tile
       ipt = 0;
@@ -2423,20 +2561,23 @@ paged_decode_stream_kernel(const DecodeArgs a) {
     }
   };
 #pragma unroll
-  for (int i = 0; i < kSStages - 1; ++i)
+  for (int i = 0; i < kStg - 1; ++i)
     if (issued < count) issue_next();
 
   // ---- compute side: entry b, tiles left in it for this workgroup
   int b = __builtin_amdgcn_readfirstlane(wr0.x);
   int cleft = min(__builtin_amdgcn_readfirstlane(tstart[b + 1] - tstart[b]) - __builtin_amdgcn_readfirstlane(wr0.y),
                   count);
-  QOperandF8 qop;
+  using QOp = typename std::conditional<C16, QOperand16, QOperandF8>::type;
+  QOp qop;
   bool colv;
-  {
+  auto load_query = [&]() {
     int qrow, qhead;
     stream_column<TPR>(a, plan, V, b, h, c, qrow, qhead, colv);
-    stream_load_q8<QDT, QVEC>(a, qrow, qhead, colv, g, qop);
-  }
+    if constexpr (C16) stream_load_q16<QDT, QVEC>(a, qrow, qhead, colv, g, qop);
+    else stream_load_q8<QDT, QVEC>(a, qrow, qhead, colv, g, qop);
+  };
+  load_query();
 
   floatx4 acc[8];
 #pragma unroll
@@ -2463,6 +2604,22 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   // first token this lane's score rows refer to, relative to the tile:
   // row 4g + i of this wave's slot is token TPR * (4g + i) + h / Hkv
   const int tok_lane = TPR * 4 * g + h / (kSKv / TPR);
+  // 16-bit tiles: K chunks 4g + kb of token c; V for N-tile nt: token
+  // 4g + (c >> 2), 8 bytes at 32 nt + 8 (c & 3) of the head slot (the b64_tr_b16
+  // read then hands lane (g, n) dims 16 nt + n of tokens 4g .. 4g + 3)
+  uint32_t k16_off[4], v16_off[8];
+  if constexpr (C16) {
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+      k16_off[kb] = stage0 + c * kS16Row + h * (2 * kHeadDim) + (((4 * g + kb) ^ stream_swz16(c)) << 4);
+    const int t = 4 * g + (c >> 2);
+#pragma unroll
+    for (int nt = 0; nt < 8; ++nt) {
+      const int byte = 32 * nt + 8 * (c & 3);
+      v16_off[nt] = stage0 + kS16KBytes + t * kS16Row + h * (2 * kHeadDim) + (((byte >> 4) ^ stream_swz16(t)) << 4) +
+                    (byte & 15);
+    }
+  }
 
   int cstage = 0;
   // measurement aid (bit 64): cycles per section of the loop, per wave
@@ -2479,8 +2636,11 @@ paged_decode_stream_kernel(const DecodeArgs a) {
     // Wait for this tile's loads (the younger tiles' loads may stay in flight),
     // then one barrier: every wave's loads have landed and every wave has
     // finished the previous tile, whose stage the refill below reuses.
-    static_assert(kSStages == 4, "wait counts below assume three tiles in flight");
-    if (done + 3 < count) {  // steady state: three younger tiles in flight
+    static_assert(kSStages == 4 && kS16Stages == 2, "wait counts below assume three (16-bit: one) tiles in flight");
+    if constexpr (C16) {
+      if (done + 1 < count) __builtin_amdgcn_s_waitcnt(0xF70 | kS16LoadsPerStage);  // one younger tile in flight
+      else __builtin_amdgcn_s_waitcnt(0xF70);
+    } else if (done + 3 < count) {  // steady state: three younger tiles in flight
       __builtin_amdgcn_s_waitcnt(0xF70 | (3 * kSLoadsPerStage));
     } else {
       const int younger = count - done - 1;
@@ -2494,7 +2654,85 @@ paged_decode_stream_kernel(const DecodeArgs a) {
     if (issued < count) issue_next();
     xs_mark(1);
 
-    if (nv != 0 && !(PRISM_DBG(a) & 1)) {
+    if constexpr (C16) {
+      if (nv != 0 && !(PRISM_DBG(a) & 1)) {
+        const uint32_t slot = static_cast<uint32_t>(cstage) * kS16Stage;
+        // ---- all LDS reads of the tile first
+        u32x4 kw[4];
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) kw[kb] = lds_load_b128(k16_off[kb] + slot);
+        uint64_t vt[8];
+        lds_read_tr16_x8(v16_off, slot, vt);
+        // ---- QK over 16 tokens: the K rows are the MFMA's A operand as they
+        // are (row = token c, k = dims 32g + 8kb ..), the query the B operand
+        floatx4 sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb) {
+          if constexpr (QDT == PRISM_DTYPE_BF16)
+            sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kw[kb]),
+                                                         __builtin_bit_cast(bf16x8, qop.t[kb]), sc, 0, 0, 0);
+          else
+            sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, kw[kb]),
+                                                        __builtin_bit_cast(f16x8, qop.t[kb]), sc, 0, 0, 0);
+        }
+        float x[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) x[i] = sc[i] * qop.colscale;
+        // only a sequence's last tile can reach past its end: masked tokens
+        // get score -inf and zero V elements (rows past the end may hold NaN)
+        if (nv < kTTok) {
+          uint64_t keep = 0;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const bool tv = tok_lane + i < nv;
+            x[i] = tv ? x[i] : -INFINITY;
+            keep |= tv ? (uint64_t{0xFFFF} << (16 * i)) : 0;
+          }
+#pragma unroll
+          for (int nt = 0; nt < 8; ++nt) vt[nt] &= keep;
+        }
+        float tmax = nan_max(nan_max(x[0], x[1]), nan_max(x[2], x[3]));
+        tmax = wave_maximum_across_groups(tmax);
+        const bool raise = tmax > m_run + kSRescaleThreshold;
+        if (__builtin_amdgcn_ballot_w64(raise) != 0) {  // wave-uniform branch
+          const float m_new = raise ? tmax : m_run;
+          const float alpha = raise ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.f;
+          m_run = m_new;
+          l_run *= alpha;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float ai = __shfl(alpha, 4 * g + i);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) acc[j][i] *= ai;
+          }
+        }
+        const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
+        float pv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          pv[i] = __builtin_amdgcn_exp2f(x[i] - m_use);  // 0 for masked tokens
+          l_run += pv[i];
+        }
+        // ---- PV: P (A operand, k = tokens 4g .. 4g + 3) in the cache's
+        // 16-bit type, V N-tile nt from the transposed read (B operand)
+        if constexpr (QDT == PRISM_DTYPE_BF16) {
+          const shortx4 pa = {__builtin_bit_cast(short, static_cast<__bf16>(pv[0])),
+                              __builtin_bit_cast(short, static_cast<__bf16>(pv[1])),
+                              __builtin_bit_cast(short, static_cast<__bf16>(pv[2])),
+                              __builtin_bit_cast(short, static_cast<__bf16>(pv[3]))};
+#pragma unroll
+          for (int nt = 0; nt < 8; ++nt)
+            acc[nt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, __builtin_bit_cast(shortx4, vt[nt]), acc[nt], 0,
+                                                                0, 0);
+        } else {
+          const f16x4 pa = {static_cast<_Float16>(pv[0]), static_cast<_Float16>(pv[1]), static_cast<_Float16>(pv[2]),
+                            static_cast<_Float16>(pv[3])};
+#pragma unroll
+          for (int nt = 0; nt < 8; ++nt)
+            acc[nt] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(f16x4, vt[nt]), acc[nt], 0, 0, 0);
+        }
+      }
+    } else if (nv != 0 && !(PRISM_DBG(a) & 1)) {
       const uint32_t slot = static_cast<uint32_t>(cstage) * kSStage;
       // ---- all LDS reads of the tile first, so their latencies overlap
       const u32x4 k0 = lds_load_b128(k_off0 + slot);
@@ -2589,7 +2827,7 @@ paged_decode_stream_kernel(const DecodeArgs a) {
       }
     }
     const int cdone = cstage;  // the stage just consumed (refilled only after the next barrier)
-    cstage = cstage == kSStages - 1 ? 0 : cstage + 1;
+    cstage = cstage == kStg - 1 ? 0 : cstage + 1;
     xs_mark(2);
 
     // ---- flush at the end of a stream entry (or of this workgroup's range)
@@ -2683,9 +2921,7 @@ paged_decode_stream_kernel(const DecodeArgs a) {
         } while (tstart[b + 1] == tstart[b] && b + 1 < NS);
         b = __builtin_amdgcn_readfirstlane(b);
         cleft = min(__builtin_amdgcn_readfirstlane(tstart[b + 1] - tstart[b]), count - done - 1);
-        int qrow, qhead;
-        stream_column<TPR>(a, plan, V, b, h, c, qrow, qhead, colv);
-        stream_load_q8<QDT, QVEC>(a, qrow, qhead, colv, g, qop);
+        load_query();
       }
     }
     xs_mark(3);
@@ -2932,7 +3168,12 @@ Geometry geometry(int batch, int num_heads, int num_kv_heads, int head_dim, int 
                     (num_kv_heads & (num_kv_heads - 1)) == 0)
                        ? kSTile * (kSKv / num_kv_heads)
                        : 0;  // 8, 4, 2 or 1 kv heads
-  geo.stream_shape = cache_dtype == PRISM_DTYPE_FP8_E4M3FN && ttok > 0 && page_size % ttok == 0 &&
+  // FP8 caches with 8, 4, 2 or 1 kv heads; 16-bit caches with 8 (a 2 KB token
+  // row of 16-bit elements makes 16-token tiles of 8 heads)
+  const bool stream_dtype = cache_dtype == PRISM_DTYPE_FP8_E4M3FN ||
+                            ((cache_dtype == PRISM_DTYPE_BF16 || cache_dtype == PRISM_DTYPE_F16) &&
+                             num_kv_heads == kSKv);
+  geo.stream_shape = stream_dtype && ttok > 0 && page_size % ttok == 0 &&
                      batch <= kSMaxBatch && !stream_disabled() &&
                      device_cu_count() * kSWgPerCu <= kSMaxWg;
   if (geo.stream_shape && forced_path() != 2) {
@@ -2969,8 +3210,13 @@ int launch_stream(int stage, const DecodeArgs& args, const Geometry& geo, hipStr
   if (stage == 0 || stage == 1) {
     const dim3 grid(geo.stream_nwg), block(kSThreads);
 #define PRISM_LAUNCH_STREAM(V, T) \
-  hipLaunchKernelGGL((paged_decode_stream_kernel<QDT, V, T>), grid, block, 0, stream, args)
-    if (args.q_vec) {
+  hipLaunchKernelGGL((paged_decode_stream_kernel<QDT, V, T, false>), grid, block, 0, stream, args)
+    if (args.cache_dtype != PRISM_DTYPE_FP8_E4M3FN) {  // 16-bit cache of the query's dtype, 8 kv heads
+      if constexpr (QDT != PRISM_DTYPE_F32) {
+        if (args.q_vec) hipLaunchKernelGGL((paged_decode_stream_kernel<QDT, true, 1, true>), grid, block, 0, stream, args);
+        else hipLaunchKernelGGL((paged_decode_stream_kernel<QDT, false, 1, true>), grid, block, 0, stream, args);
+      }
+    } else if (args.q_vec) {
       if (args.s_tpr == 8) PRISM_LAUNCH_STREAM(true, 8);
       else if (args.s_tpr == 4) PRISM_LAUNCH_STREAM(true, 4);
       else if (args.s_tpr == 2) PRISM_LAUNCH_STREAM(true, 2);
@@ -3243,7 +3489,7 @@ extern "C" int prism_paged_decode_stage(
                              aligned(v_scale, 16) && ks_strides[0] % 4 == 0);
   const bool use_stream = geo.fast && geo.stream_shape && k_strides[1] == tok_bytes && k_strides[2] == kHeadDim &&
                           v_strides[1] == tok_bytes && v_strides[2] == kHeadDim &&
-                          scale_layout;
+                          scale_layout && (cache_dtype == PRISM_DTYPE_FP8_E4M3FN || cache_dtype == q_dtype);
   if (use_stream) {
     args.plan_region = static_cast<int*>(workspace);
     args.epoch = next_split_epoch();

@@ -1,8 +1,10 @@
 """GPU parity of paged decode over bf16 and f16 KV caches (the dense variants).
 
-A 16-bit cache whose dtype is the query's runs the split-K kernel (the K rows
-feed the QK MFMA as they are; V pairs are assembled with byte permutes); other
-16-bit combinations run the generic kernel.  Each case is compared with
+A 16-bit cache whose dtype is the query's runs the streaming kernel's 16-bit
+tiles (8 kv heads and batches with enough tiles; K rows feed the QK MFMA as
+they are, V comes from 16-bit transposed LDS reads) or the split-K kernel (the
+K rows feed the QK MFMA as they are; V pairs are assembled with byte
+permutes); other 16-bit combinations run the generic kernel.  Each case is compared with
 ``decode_kernel_semantics`` (the float64 oracle of
 prism_infer/ops/paged_decode.py:83-180) within the decode tolerance of
 tests/test_scaled_fp8_kv_cache.py:470-472.  The reference's decode reads a
@@ -90,3 +92,57 @@ def test_mixed_16bit_dtypes_use_the_generic_kernel():
         want = oracle.decode_kernel_semantics(qq, kk, vv, tables, lens, scale)
         got = _run(qq, kk, vv, tables, lens, scale)
         assert_decode_close(got, want, label=f"q {qd} cache {kd}")
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("page", [256, 64, 16])
+def test_16bit_cache_streaming_kernel(dtype, page):
+    """The streaming kernel's 16-bit tiles, forced and automatic: ragged lengths (one token, tile tails,
+    the table's full capacity, zero), holes, NaN bytes in the pages past every sequence's end (masked
+    out, never multiplied), and a group of sequences sharing leading pages (virtual walks)."""
+
+    require_gpu()
+    g = torch.Generator().manual_seed(20261213 + page)
+    batch, hkv, groups = 40, 8, 4
+    width = max(2, 6144 // page)
+    pool = batch * width + 5
+    q = torch.randn(batch, hkv * groups, 128, generator=g).to(dtype)
+    k = (torch.randn(pool, page, hkv, 128, generator=g) * 2).to(dtype)
+    v = torch.randn(pool, page, hkv, 128, generator=g).to(dtype)
+    tables = torch.randperm(pool, generator=g)[: batch * width].to(torch.int32).view(batch, width).clone()
+    lens = torch.randint(1, width * page + 1, (batch,), generator=g, dtype=torch.int32)
+    lens[:4] = torch.tensor([1, 15, 17, width * page], dtype=torch.int32)
+    lens[5] = 0
+    tables[7, 1] = -1
+    members = torch.arange(10, 22)
+    lens[members] = torch.clamp(lens[members], min=2 * page + 3)
+    tables[members, :2] = tables[members[0], :2]
+    for b in range(batch):  # garbage past each end: NaN rows in the last page's tail
+        n = int(lens[b])
+        if 0 < n < width * page and n % page:
+            blk = int(tables[b, n // page])
+            if blk >= 0:
+                k[blk, n % page:] = float("nan")
+                v[blk, n % page:] = float("nan")
+    scale = 128 ** -0.5
+    shared = {int(tables[b, j]) for b in range(batch) for j in range(width) if int(tables[b, j]) >= 0}
+    assert len(shared) < batch * width  # the group's pages appear more than once
+    want = oracle.decode_kernel_semantics(q, k, v, tables, lens, scale)
+    for path in ("stream", "auto"):
+        set_decode_overrides(path=path)
+        fam = _family(q, k, tables)
+        if path == "stream":
+            assert fam == 2
+        got = _run(q, k, v, tables, lens, scale)
+        assert torch.all(got[5] == 0), "ctx = 0 row"
+        assert_decode_close(got, want, label=f"{dtype} P={page} path={path} family={fam}")
+
+
+def test_16bit_cache_streaming_is_automatic_for_large_batches():
+    require_gpu()
+    q, k, v, tables, lens = _case(20261214, torch.bfloat16, batch=64, width=40)
+    assert _family(q, k, tables) == 2
+    scale = 128 ** -0.5
+    want = oracle.decode_kernel_semantics(q, k, v, tables, lens, scale)
+    got = _run(q, k, v, tables, lens, scale)
+    assert_decode_close(got, want, label="bf16 B=64 automatic")
