@@ -94,6 +94,7 @@ struct DecodeArgs {
   // parameter, the plan code reads both
   int s_tpr, s_ttok;
   int plan_spin;  // streaming path: polls a workgroup waits for a plan build before it gives up
+  int vcols;      // streaming path: query columns of a virtual sequence (16, or 32 = two MFMA column blocks)
 };
 
 // Read-only int32 metadata (block tables, context lengths) through the
@@ -1311,6 +1312,7 @@ __device__ __forceinline__ void stream_load_q8(const DecodeArgs& a, int qrow, in
 // (workgroup, stream entry) indexes a partial uniquely as w + entry.
 
 constexpr int kSCols = 16;                 // query columns of the MFMA operand
+constexpr int kVMax = 32;                  // query columns of a virtual sequence at most (two column blocks)
 constexpr int kSMinKv = 1;                 // fewest kv heads on the streaming path (8 token slots)
 constexpr int kSMaxWg = 1024;              // grid size bound of the streaming kernel
 constexpr int kSMaxVirt = 128;             // virtual sequences (>= 2 members each)
@@ -1321,7 +1323,7 @@ constexpr int kPlanSkip = kPlanTstart + kSMaxBatch + kSMaxVirt + 16;
 constexpr int kPlanVslot = kPlanSkip + kSMaxBatch;
 constexpr int kPlanVsrc = kPlanVslot + kSMaxBatch;
 constexpr int kPlanVmem = kPlanVsrc + kSMaxVirt;
-constexpr int kPlanVrot = kPlanVmem + kSMaxVirt * kSCols;  // first tile of each virtual walk
+constexpr int kPlanVrot = kPlanVmem + kSMaxVirt * kVMax;  // first tile of each virtual walk
 constexpr int kPlanWgTime = kPlanVrot + kSMaxVirt;         // measurement aid: per-workgroup times
 // Key of the plan: everything the plan is computed from.  A call whose
 // inputs equal the key left by the previous call on the same workspace keeps
@@ -1436,11 +1438,18 @@ __device__ __forceinline__ int stream_owner_count(int first, int end, int total,
 // a walk of shared pages is followed by merges over its 4 members' outputs).
 // Before the weights, a workgroup meeting two entries ended its loop 2.6 us
 // after one meeting one, and the last loops ended 7 us after the mean.
+// With two column blocks per virtual walk (a wide walk computes both blocks
+// from one LDS tile, about 1.6 us per tile against 1.25 us for a private
+// tile) the measured step was, over three runs each: virtual 22 / 26 / 30 /
+// 34 with entry 128: 171.0 / 169.8 / 171.6 / 170.6 us; virtual 26 with
+// entry 96 / 160: 169.0 / 170.3 us.  A walk's workgroup must end its loop
+// well before the others, or it completes its members' sequences and
+// merges them one after another (virtual 16: 215 us, eight merges).
 #ifndef PRISM_COST_ENTRY
-#define PRISM_COST_ENTRY 128
+#define PRISM_COST_ENTRY 96
 #endif
 #ifndef PRISM_COST_VIRT
-#define PRISM_COST_VIRT 22
+#define PRISM_COST_VIRT 26
 #endif
 constexpr int kCostTile = 16;
 constexpr int kCostEntry = PRISM_COST_ENTRY;
@@ -1519,7 +1528,7 @@ struct PlanLds {
   int vk_s[kSMaxVirt];      // chunk index of v in its group
   int vn_s[kSMaxVirt];      // virtual sequences of v's group
   int vsrc_s[kSMaxVirt];
-  int vmem_s[kSMaxVirt * kSCols];
+  int vmem_s[kSMaxVirt * kVMax];
   int hkey[kPlanHash];
   int hmin[kPlanHash];
   __attribute__((aligned(16))) int bt_s[kSShareMaxBatch * kPlanMaxPages];  // compared part of the block tables
@@ -1532,13 +1541,13 @@ struct PlanLds {
 // Whether prefix sharing is analysed for this call.
 __device__ __forceinline__ bool plan_share(const DecodeArgs& a) {
   const int Wc = min(a.width, kPlanMaxPages);
-  return a.share && a.batch <= kSShareMaxBatch && (kSCols / a.groups) >= 2 && Wc >= 1;
+  return a.share && a.batch <= kSShareMaxBatch && (a.vcols / a.groups) >= 2 && Wc >= 1;
 }
 
 __device__ __forceinline__ void plan_key_params(const DecodeArgs& a, bool share, int (&kp)[kPlanKeyParams]) {
   const int vals[kPlanKeyParams] = {kPlanMagic, a.batch, a.width, a.page_size, a.groups,
                                     static_cast<int>(a.num_blocks & 0x7FFFFFFF),
-                                    static_cast<int>(a.num_blocks >> 31), share ? 1 : 0, a.stream_nwg,
+                                    static_cast<int>(a.num_blocks >> 31), share ? a.vcols : 0, a.stream_nwg,
                                     a.num_kv_heads, 0, 0};
 #pragma unroll
   for (int i = 0; i < kPlanKeyParams; ++i) kp[i] = vals[i];
@@ -1676,7 +1685,7 @@ __device__ void plan_build(const DecodeArgs& a, int* plan, PlanLds& L, int* tst_
   const int B = a.batch;
   const int P = a.page_size;
   const int Wc = min(a.width, kPlanMaxPages);
-  const int M = kSCols / a.groups;  // members per virtual sequence
+  const int M = a.vcols / a.groups;  // members per virtual sequence
   const bool share = plan_share(a);
   const int items = share ? B * Wc : 0;
   for (int b = tid; b < B; b += NT) {
@@ -1696,7 +1705,7 @@ __device__ void plan_build(const DecodeArgs& a, int* plan, PlanLds& L, int* tst_
       L.hkey[i] = -1;
       L.hmin[i] = INT_MAX;
     }
-    for (int i = tid; i < kSMaxVirt * kSCols; i += NT) L.vmem_s[i] = -1;
+    for (int i = tid; i < kSMaxVirt * kVMax; i += NT) L.vmem_s[i] = -1;
     __syncthreads();
     // group by first page: open addressing, the lowest index wins the slot
     int slot = -1;
@@ -1783,8 +1792,8 @@ __device__ void plan_build(const DecodeArgs& a, int* plan, PlanLds& L, int* tst_
         if (chunk >= 2) {
           const int v = L.vb_s[ld] + k;
           const int m = rank - k * M;
-          L.vmem_s[v * kSCols + m] = tid;
-          L.vslot_s[tid] = v * kSCols + m;
+          L.vmem_s[v * kVMax + m] = tid;
+          L.vslot_s[tid] = v * kVMax + m;
           atomicMin(&L.vlen_s[v], ld == tid ? L.smax_s[tid] : L.sh_s[tid]);
           if (m == 0) {
             L.vsrc_s[v] = ld;
@@ -1795,7 +1804,7 @@ __device__ void plan_build(const DecodeArgs& a, int* plan, PlanLds& L, int* tst_
       }
     }
     __syncthreads();
-    if (tid < B && L.vslot_s[tid] >= 0) L.skip_s[tid] = L.vlen_s[L.vslot_s[tid] / kSCols] * P;
+    if (tid < B && L.vslot_s[tid] >= 0) L.skip_s[tid] = L.vlen_s[L.vslot_s[tid] / kVMax] * P;
     __syncthreads();
   }
   // tile prefix sums in stream order: virtual sequences, then real ones
@@ -1821,7 +1830,7 @@ __device__ void plan_build(const DecodeArgs& a, int* plan, PlanLds& L, int* tst_
     plan[kPlanSkip + b] = L.skip_s[b];
     plan[kPlanVslot + b] = L.vslot_s[b];
     const int vs = L.vslot_s[b];
-    const int v = vs >= 0 ? vs / kSCols : 0;
+    const int v = vs >= 0 ? vs / kVMax : 0;
     // each tile range as [cost position of its first tile, that of its last + 1)
     int first = 0, end = 0, vfirst = 0, vend = 0;
     if (tst_s[V + b + 1] > tst_s[V + b]) {
@@ -1839,7 +1848,7 @@ __device__ void plan_build(const DecodeArgs& a, int* plan, PlanLds& L, int* tst_
     rec[1] = int4{vend, expect, 0, 0};
     plan[kPlanCnt + b] = 0;
   }
-  for (int i = tid; i < V * kSCols; i += NT) plan[kPlanVmem + i] = L.vmem_s[i];
+  for (int i = tid; i < V * kVMax; i += NT) plan[kPlanVmem + i] = L.vmem_s[i];
   for (int v = tid; v < V; v += NT) {
     plan[kPlanVsrc + v] = L.vsrc_s[v];
     plan[kPlanVrot + v] = (L.vk_s[v] * L.vlen_s[v] / L.vn_s[v]) * (P / a.s_ttok);
@@ -2104,7 +2113,7 @@ __device__ __forceinline__ void stream_column(const DecodeArgs& a, const int* pl
   }
   const int m = c / G;
   const int qh = c - m * G;
-  const int member = (m < kSCols / G) ? plan[kPlanVmem + i * kSCols + m] : -1;
+  const int member = (m < a.vcols / G) ? plan[kPlanVmem + i * kVMax + m] : -1;
   valid = member >= 0;
   qrow = valid ? member : 0;
   qhead = h * G + (valid ? qh : 0);
@@ -2165,7 +2174,7 @@ __device__ __forceinline__ void stream_merge_batch(const DecodeArgs& a, int V, c
   const bool all_ranges = sp.total >= sp.nwg;
   // per candidate: row = base + w * stride + slot * slot_stride, where the
   // real candidates' (w from lo0) and the virtual ones' (w from lo1) differ
-  const int stride0 = kSKv * a.groups, stride1 = kSKv * kSCols;
+  const int stride0 = kSKv * a.groups, stride1 = kSKv * a.vcols;
   const int sstride0 = a.num_heads, sstride1 = hkv * kSCols;
   // whole-region resources (the partial region is far below 4 GiB)
   const __amdgpu_buffer_rsrc_t acc_r = __builtin_amdgcn_make_buffer_rsrc(a.part_acc, 0, 0x7FFFFFFF, 0x00020000);
@@ -2175,10 +2184,10 @@ __device__ __forceinline__ void stream_merge_batch(const DecodeArgs& a, int V, c
     const int rbase0 = (V + b) * stride0 + hq + lo0 * stride0;
     int rbase1 = 0;
     if (vslot >= 0) {
-      const int v = vslot / kSCols;
-      const int m = vslot - v * kSCols;
+      const int v = vslot / kVMax;
+      const int m = vslot - v * kVMax;
       const int hk = hq / a.groups;
-      rbase1 = static_cast<int>(a.vrow0) + (v * kSKv + hk) * kSCols + m * a.groups + (hq - hk * a.groups) +
+      rbase1 = static_cast<int>(a.vrow0) + (v * kSKv + hk) * a.vcols + m * a.groups + (hq - hk * a.groups) +
                lo1 * stride1;
     }
     float m_run = -INFINITY, l_sum = 0.f;
@@ -2294,14 +2303,14 @@ __device__ __forceinline__ void stream_finish(const DecodeArgs& a, int* plan, in
   if (threadIdx.x == 0) *n_merge = 0;
   __syncthreads();
   int* cnt = plan + kPlanCnt;
-  const int members = kSCols / a.groups;
-  for (int t = threadIdx.x; t < nent * kSCols; t += kSThreads) {
-    const int i = e_first + t / kSCols;
-    const int slot = t - (t / kSCols) * kSCols;
+  const int members = a.vcols / a.groups;
+  for (int t = threadIdx.x; t < nent * kVMax; t += kSThreads) {
+    const int i = e_first + t / kVMax;
+    const int slot = t - (t / kVMax) * kVMax;
     if (tstart[i + 1] == tstart[i]) continue;  // no tiles: never flushed
     int seq = -1;
     if (i >= V) seq = slot == 0 ? i - V : -1;
-    else if (slot < members) seq = plan[kPlanVmem + i * kSCols + slot];
+    else if (slot < members) seq = plan[kPlanVmem + i * kVMax + slot];
     if (seq < 0) continue;
     const int4 r0 = *reinterpret_cast<const int4*>(plan + kPlanRec + 8 * seq);
     const int2 r1 = *reinterpret_cast<const int2*>(plan + kPlanRec + 8 * seq + 4);  // virtual end, expected
@@ -2569,21 +2578,35 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   int cleft = min(__builtin_amdgcn_readfirstlane(tstart[b + 1] - tstart[b]) - __builtin_amdgcn_readfirstlane(wr0.y),
                   count);
   using QOp = typename std::conditional<C16, QOperand16, QOperandF8>::type;
+  // Wide virtual sequences (FP8 tiles, 8 kv heads): a virtual entry has two
+  // blocks of 16 query columns (twice the members per walk of the shared
+  // pages); both read the same K and V of each tile from LDS.
+  constexpr bool kWide = TPR == 1 && !C16;
+  const bool wide_call = kWide && a.vcols > kSCols;
   QOp qop;
-  bool colv;
+  QOperandF8 qop2;  // second column block (wide virtual entries)
+  bool colv, colv2;
+  bool wide = false;  // the compute side's entry is a wide virtual one (wave-uniform)
   auto load_query = [&]() {
     int qrow, qhead;
     stream_column<TPR>(a, plan, V, b, h, c, qrow, qhead, colv);
     if constexpr (C16) stream_load_q16<QDT, QVEC>(a, qrow, qhead, colv, g, qop);
     else stream_load_q8<QDT, QVEC>(a, qrow, qhead, colv, g, qop);
+    wide = wide_call && b < V;
+    if constexpr (kWide) {
+      if (wide) {
+        stream_column<TPR>(a, plan, V, b, h, c + kSCols, qrow, qhead, colv2);
+        stream_load_q8<QDT, QVEC>(a, qrow, qhead, colv2, g, qop2);
+      }
+    }
   };
   load_query();
 
-  floatx4 acc[8];
+  floatx4 acc[8], acc2[8];
 #pragma unroll
-  for (int j = 0; j < 8; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY;  // running max (log2 domain) of query column c
-  float l_run = 0.f;        // this lane's share of the running sum
+  for (int j = 0; j < 8; ++j) acc[j] = acc2[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, m_run2 = -INFINITY;  // running max (log2 domain) of query column c (16 + c)
+  float l_run = 0.f, l_run2 = 0.f;              // this lane's share of the running sum
 
   // Per-lane LDS addresses inside stage 0 (loop invariant).
   const uint32_t k_off0 = stage0 + c * kSRow + stream_slot(h, c) * kHeadDim + (((2 * g) ^ stream_swz(c)) << 4);
@@ -2753,77 +2776,92 @@ paged_decode_stream_kernel(const DecodeArgs a) {
       const i32x8 ka = {static_cast<int>(k0[0]), static_cast<int>(k0[1]), static_cast<int>(k0[2]),
                         static_cast<int>(k0[3]), static_cast<int>(k1[0]), static_cast<int>(k1[1]),
                         static_cast<int>(k1[2]), static_cast<int>(k1[3])};
-      floatx4 sc = {0.f, 0.f, 0.f, 0.f};
-      // (a bf16 query's third term is zero: two terms hold every bf16 value
-      // the fp8 grid can, and the third only refines f16/f32 queries)
-      if constexpr (QDT != PRISM_DTYPE_BF16)
-        sc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, qop.t[2], sc, 0, 0, 0, 0, 0, 0);
-      sc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, qop.t[1], sc, 0, 0, 0, 0, 0, 0);
-      sc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, qop.t[0], sc, 0, 0, 0, 0, 0, 0);
-      // ---- scores in the log2 domain.  Query columns without a query hold
-      // q = 0, so their scores are finite and their rows are never written.
-      float x[4];
-      float vsm[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        x[i] = sc[i] * (ks[i] * qop.colscale);
-        vsm[i] = vs[i];
-      }
       // Only a sequence's last tile can reach past its end (uniform branch).
       // Masked slots get score -inf (weight 0) and v scale 0, and their V
       // bytes are zeroed: rows past the end may hold anything, and the MFMA
       // would turn 0 * NaN into NaN.
-      if (nv < kTTok) {
+      float vsm[4];
+      bool tv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        tv[i] = true;
+        vsm[i] = vs[i];
+      }
+      const bool partial = nv < kTTok;
+      if (partial) {
         uint32_t keep = 0;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const bool tv = tok_lane + TPR * i < nv;
-          x[i] = tv ? x[i] : -INFINITY;
-          vsm[i] = tv ? vsm[i] : 0.f;
-          keep |= tv ? (0xFFu << (8 * i)) : 0u;
+          tv[i] = tok_lane + TPR * i < nv;
+          vsm[i] = tv[i] ? vsm[i] : 0.f;
+          keep |= tv[i] ? (0xFFu << (8 * i)) : 0u;
         }
         const uint64_t keep2 = static_cast<uint64_t>(keep) | (static_cast<uint64_t>(keep) << 32);
 #pragma unroll
         for (int jp = 0; jp < 4; ++jp) vt[jp] &= keep2;
       }
-      // ---- online softmax with lazy rescaling
-      // (IEEE maximum: no canonicalising of masked or swapped values)
-      float tmax = nan_max(nan_max(x[0], x[1]), nan_max(x[2], x[3]));
-      tmax = wave_maximum_across_groups(tmax);
-      const bool raise = tmax > m_run + kSRescaleThreshold;
-      if (__builtin_amdgcn_ballot_w64(raise) != 0) {  // wave-uniform branch
-        const float m_new = raise ? tmax : m_run;
-        const float alpha = raise ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.f;
-        m_run = m_new;
-        l_run *= alpha;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float ai = __shfl(alpha, 4 * g + i);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) acc[j][i] *= ai;
-        }
-      }
-      const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
-      // v_exp_f32 directly: arguments are at most 2^3 above the running max,
-      // and results below 2^-126 (flushed to 0) weigh nothing next to it.
-      float pv[4];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float p = __builtin_amdgcn_exp2f(x[i] - m_use);  // 0 for masked slots
-        l_run += p;
-        pv[i] = p * vsm[i];
-      }
-      // ---- PV: one transposed read feeds N-tiles 2jp and 2jp+1.
-      const shortx4 pa = {__builtin_bit_cast(short, static_cast<__bf16>(pv[0])),
-                          __builtin_bit_cast(short, static_cast<__bf16>(pv[1])),
-                          __builtin_bit_cast(short, static_cast<__bf16>(pv[2])),
-                          __builtin_bit_cast(short, static_cast<__bf16>(pv[3]))};
+      // V's E4M3FN bytes as bf16 (exact): one transposed read feeds N-tiles
+      // 2jp and 2jp+1 of every column block
+      shortx4 vb[8];
 #pragma unroll
       for (int jp = 0; jp < 4; ++jp) {
-        const shortx4 b0 = fp8x4_to_bf16x4_bits(static_cast<uint32_t>(vt[jp]));
-        const shortx4 b1 = fp8x4_to_bf16x4_bits(static_cast<uint32_t>(vt[jp] >> 32));
-        acc[2 * jp] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, b0, acc[2 * jp], 0, 0, 0);
-        acc[2 * jp + 1] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, b1, acc[2 * jp + 1], 0, 0, 0);
+        vb[2 * jp] = fp8x4_to_bf16x4_bits(static_cast<uint32_t>(vt[jp]));
+        vb[2 * jp + 1] = fp8x4_to_bf16x4_bits(static_cast<uint32_t>(vt[jp] >> 32));
+      }
+      // One block of 16 query columns: scores, online softmax with lazy
+      // rescaling, PV.
+      auto column_block = [&](const QOperandF8& qo, floatx4 (&ac)[8], float& mr, float& lr) {
+        floatx4 sc = {0.f, 0.f, 0.f, 0.f};
+        // (a bf16 query's third term is zero: two terms hold every bf16 value
+        // the fp8 grid can, and the third only refines f16/f32 queries)
+        if constexpr (QDT != PRISM_DTYPE_BF16)
+          sc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, qo.t[2], sc, 0, 0, 0, 0, 0, 0);
+        sc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, qo.t[1], sc, 0, 0, 0, 0, 0, 0);
+        sc = __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(ka, qo.t[0], sc, 0, 0, 0, 0, 0, 0);
+        // ---- scores in the log2 domain.  Query columns without a query hold
+        // q = 0, so their scores are finite and their rows are never written.
+        float x[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          x[i] = sc[i] * (ks[i] * qo.colscale);
+          if (partial) x[i] = tv[i] ? x[i] : -INFINITY;
+        }
+        // (IEEE maximum: no canonicalising of masked or swapped values)
+        float tmax = nan_max(nan_max(x[0], x[1]), nan_max(x[2], x[3]));
+        tmax = wave_maximum_across_groups(tmax);
+        const bool raise = tmax > mr + kSRescaleThreshold;
+        if (__builtin_amdgcn_ballot_w64(raise) != 0) {  // wave-uniform branch
+          const float m_new = raise ? tmax : mr;
+          const float alpha = raise ? __builtin_amdgcn_exp2f(mr - m_new) : 1.f;
+          mr = m_new;
+          lr *= alpha;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float ai = __shfl(alpha, 4 * g + i);
+#pragma unroll
+            for (int j = 0; j < 8; ++j) ac[j][i] *= ai;
+          }
+        }
+        const float m_use = (mr == -INFINITY) ? 0.f : mr;
+        // v_exp_f32 directly: arguments are at most 2^3 above the running max,
+        // and results below 2^-126 (flushed to 0) weigh nothing next to it.
+        float pv[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float p = __builtin_amdgcn_exp2f(x[i] - m_use);  // 0 for masked slots
+          lr += p;
+          pv[i] = p * vsm[i];
+        }
+        const shortx4 pa = {__builtin_bit_cast(short, static_cast<__bf16>(pv[0])),
+                            __builtin_bit_cast(short, static_cast<__bf16>(pv[1])),
+                            __builtin_bit_cast(short, static_cast<__bf16>(pv[2])),
+                            __builtin_bit_cast(short, static_cast<__bf16>(pv[3]))};
+#pragma unroll
+        for (int n = 0; n < 8; ++n) ac[n] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, vb[n], ac[n], 0, 0, 0);
+      };
+      column_block(qop, acc, m_run, l_run);
+      if constexpr (kWide) {
+        if (wide) column_block(qop2, acc2, m_run2, l_run2);
       }
     }
     const int cdone = cstage;  // the stage just consumed (refilled only after the next barrier)
@@ -2893,29 +2931,40 @@ paged_decode_stream_kernel(const DecodeArgs a) {
       // at vrow0 + ((wg + v) * 8 + h) * 16 + column (head slots below Hkv only)
       const bool virt = b < V;
       const int ncols = virt ? kSCols : a.groups;
-      const int64_t row0 = virt ? a.vrow0 + ((static_cast<int64_t>(blockIdx.x) + b) * kSKv + h) * kSCols
+      const int64_t row0 = virt ? a.vrow0 + ((static_cast<int64_t>(blockIdx.x) + b) * kSKv + h) * a.vcols
                                 : (static_cast<int64_t>(blockIdx.x) + b) * (kSKv * a.groups) + h * a.groups;
+      // one column block's rows: column qr at row rb + qr
+      auto flush_block = [&](const floatx4 (&ac)[8], float mr, float lt, int64_t rb) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int qr = 4 * g + i;
-        const float li = __shfl(l_tot, qr);
-        const float mi = __shfl(m_run, qr);
-        if (qr < ncols && h < kSKv / TPR) {
-          const int64_t row = row0 + qr;
-          float* dst = a.part_acc + row * kHeadDim + c;
+        for (int i = 0; i < 4; ++i) {
+          const int qr = 4 * g + i;
+          const float li = __shfl(lt, qr);
+          const float mi = __shfl(mr, qr);
+          if (qr < ncols && h < kSKv / TPR) {
+            const int64_t row = rb + qr;
+            float* dst = a.part_acc + row * kHeadDim + c;
 #pragma unroll
-          for (int j = 0; j < 8; ++j) store_coherent(dst + 16 * j, acc[j][i]);
-          if (c == 0) {
-            store_coherent(a.part_ml + row * 2 + 0, mi);
-            store_coherent(a.part_ml + row * 2 + 1, li);
+            for (int j = 0; j < 8; ++j) store_coherent(dst + 16 * j, ac[j][i]);
+            if (c == 0) {
+              store_coherent(a.part_ml + row * 2 + 0, mi);
+              store_coherent(a.part_ml + row * 2 + 1, li);
+            }
           }
+        }
+      };
+      flush_block(acc, m_run, l_tot, row0);
+      if constexpr (kWide) {
+        if (wide) {
+          float l_tot2 = l_run2 + __shfl_xor(l_run2, 16);
+          l_tot2 += __shfl_xor(l_tot2, 32);
+          flush_block(acc2, m_run2, l_tot2, row0 + kSCols);
         }
       }
       if (more) {
 #pragma unroll
-        for (int j = 0; j < 8; ++j) acc[j] = floatx4{0.f, 0.f, 0.f, 0.f};
-        m_run = -INFINITY;
-        l_run = 0.f;
+        for (int j = 0; j < 8; ++j) acc[j] = acc2[j] = floatx4{0.f, 0.f, 0.f, 0.f};
+        m_run = m_run2 = -INFINITY;
+        l_run = l_run2 = 0.f;
         do {
           ++b;
         } while (tstart[b + 1] == tstart[b] && b + 1 < NS);
@@ -2943,6 +2992,10 @@ paged_decode_stream_kernel(const DecodeArgs a) {
     d[2] = static_cast<int>(t_loop & 0x7FFFFFFF);
     d[5] = static_cast<int>(__builtin_amdgcn_s_memrealtime() & 0x7FFFFFFF);
     d[7] = (b - wr0.x + 1) | ((wr0.x < V) ? 0x10000 : 0) | (count << 17);  // entries, virtual first, tiles
+    // where the workgroup ran: XCC id (high half), HW_ID's CU/SH/SE fields (low half)
+    const unsigned hw = __builtin_amdgcn_s_getreg((31 << 11) | 4);
+    const unsigned xcc = __builtin_amdgcn_s_getreg((31 << 11) | 20);
+    a.plan_region[kPlanMergeStamps + 4 * blockIdx.x + 3] = static_cast<int>(((xcc & 0xF) << 16) | ((hw >> 8) & 0xFF));
   }
   if ((PRISM_DBG(a) & 8) && threadIdx.x == 0) {  // measurement aid: start, loop end, end (100 MHz clock)
     const uint64_t t_end = __builtin_amdgcn_s_memrealtime();
@@ -3064,6 +3117,7 @@ struct Geometry {
   // streaming path (canonical layout only; chosen per call from the strides)
   bool stream_shape;
   int stream_nwg;
+  int stream_vcols;  // query columns of a virtual sequence
   int64_t stream_acc_off, stream_ml_off, stream_vrow0;
 };
 
@@ -3184,14 +3238,16 @@ Geometry geometry(int batch, int num_heads, int num_kv_heads, int head_dim, int 
     // workspace: shared-page plan, then partial rows of the real sequences
     // and of the virtual ones
     geo.stream_nwg = device_cu_count() * kSWgPerCu;
-    const int members = kSCols / (num_heads / num_kv_heads);
+    // FP8 tiles of 8 kv heads walk shared pages for two column blocks at once
+    geo.stream_vcols = (cache_dtype == PRISM_DTYPE_FP8_E4M3FN && num_kv_heads == kSKv) ? kVMax : kSCols;
+    const int members = geo.stream_vcols / (num_heads / num_kv_heads);
     const int64_t vmax = (batch <= kSShareMaxBatch && members >= 2) ? std::min(kSMaxVirt, batch / 2) : 0;
     // real rows: (wg + V + b) * 8G (one set of G per head slot); virtual
-    // rows: (wg + v) * 8 * 16
+    // rows: (wg + v) * 8 * vcols
     const int64_t slot_rows = static_cast<int64_t>(kSKv) * (num_heads / num_kv_heads);
     geo.stream_vrow0 = (static_cast<int64_t>(geo.stream_nwg) + vmax + batch) * slot_rows;
     const int64_t rows =
-        geo.stream_vrow0 + (vmax > 0 ? (static_cast<int64_t>(geo.stream_nwg) + vmax) * kSKv * kSCols : 0);
+        geo.stream_vrow0 + (vmax > 0 ? (static_cast<int64_t>(geo.stream_nwg) + vmax) * kSKv * geo.stream_vcols : 0);
     geo.stream_acc_off = plan_bytes;
     geo.stream_ml_off = geo.stream_acc_off + align_up(rows * head_dim * 4, 256);
     const int64_t need = geo.stream_ml_off + align_up(rows * 2 * 4, 256);
@@ -3500,6 +3556,7 @@ extern "C" int prism_paged_decode_stage(
     args.s_ttok = kSTile * args.s_tpr;
     args.share = env_overrides().share.load();
     args.stream_nwg = geo.stream_nwg;
+    args.vcols = geo.stream_vcols;
     args.plan_spin = env_overrides().plan_spin.load();
   }
   hipStream_t stream = static_cast<hipStream_t>(stream_ptr);
