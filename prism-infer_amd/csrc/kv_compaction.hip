@@ -27,8 +27,18 @@ namespace prism {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kMoveWgPerCu = 8;  // move workgroups per CU, over all rows
-constexpr int kMoveUnroll = 4;   // chunks in flight per lane
+#ifndef PRISM_MOVE_WG_PER_CU
+#define PRISM_MOVE_WG_PER_CU 4
+#endif
+#ifndef PRISM_MOVE_UNROLL
+#define PRISM_MOVE_UNROLL 4
+#endif
+// Move grid: workgroups per CU (over all rows) and chunks in flight per lane.
+// Config 5's payload + scale calls, cold, with the pipelined slot indices:
+// 4 / 4 321 us; 8 / 4 346, 4 / 8 331, 2 / 8 334, 1 / 8 344 us (the loop
+// without the pipelining, 8 / 4: 338 us; 1 / 8: 650 us).
+constexpr int kMoveWgPerCu = PRISM_MOVE_WG_PER_CU;
+constexpr int kMoveUnroll = PRISM_MOVE_UNROLL;
 
 // Workspace: tags (one uint32 per slot), the hazard word, the temporary.
 int64_t workspace_layout(int64_t rows, int64_t num_slots, int64_t vec_bytes, int64_t retained, int64_t* flag_off,
@@ -102,7 +112,11 @@ struct Chunk<1> { using T = uint8_t; };
 // canonical shape: token rows of 1024 or 32 bytes, whole blocks), else
 // c / U and c % U (USHIFT < 0).  Each thread moves kMoveUnroll chunks per
 // trip with all loads issued before the stores, and every byte is read and
-// written once, so both go through the non-temporal cache policy.
+// written once, so both go through the non-temporal cache policy.  The
+// entries' slot indices are software-pipelined: a trip's data loads go out
+// with the next trip's index loads behind them, so the only round trip per
+// trip is the data's (the index loads of a trip would otherwise precede its
+// data loads as a second, dependent one).
 template <int BYTES, int MODE>
 __global__ void __launch_bounds__(kThreads)
 compact_move_kernel(uint8_t* __restrict__ cache, int64_t num_slots, int64_t vec_bytes, int ushift,
@@ -116,8 +130,31 @@ compact_move_kernel(uint8_t* __restrict__ cache, int64_t num_slots, int64_t vec_
   const int64_t row = blockIdx.y;
   const int64_t row_base = row * num_slots;
   const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
-  for (int64_t base = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; base < per_row;
-       base += kMoveUnroll * stride) {
+  auto entry_of = [&](int64_t c, int64_t& i, int64_t& part) {
+    if (ushift >= 0) {
+      i = c >> ushift;
+      part = c & (chunks_per_vec - 1);
+    } else {
+      i = c / chunks_per_vec;
+      part = c - i * chunks_per_vec;
+    }
+  };
+  // slot indices of a trip's chunks (-1: past the end)
+  int64_t s[kMoveUnroll], d[kMoveUnroll];
+  auto load_indices = [&](int64_t b) {
+#pragma unroll
+    for (int u = 0; u < kMoveUnroll; ++u) {
+      const int64_t c = b + u * stride;
+      int64_t i, part;
+      entry_of(c, i, part);
+      const bool in = c < per_row;
+      s[u] = in ? src[i] : -1;
+      d[u] = in ? dst[i] : -1;
+    }
+  };
+  int64_t base = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+  if (base < per_row) load_indices(base);
+  for (; base < per_row; base += kMoveUnroll * stride) {
     T val[kMoveUnroll];
     T* to[kMoveUnroll];
     bool ok[kMoveUnroll];
@@ -125,23 +162,16 @@ compact_move_kernel(uint8_t* __restrict__ cache, int64_t num_slots, int64_t vec_
     for (int u = 0; u < kMoveUnroll; ++u) {
       const int64_t c = base + u * stride;
       int64_t i, part;
-      if (ushift >= 0) {
-        i = c >> ushift;
-        part = c & (chunks_per_vec - 1);
-      } else {
-        i = c / chunks_per_vec;
-        part = c - i * chunks_per_vec;
-      }
-      const bool in = c < per_row;
-      const int64_t s = in ? src[i] : -1;
-      const int64_t d = in ? dst[i] : -1;
-      ok[u] = entry_live(s, d, num_slots);
+      entry_of(c, i, part);
+      ok[u] = entry_live(s[u], d[u], num_slots);
       T* tmp = reinterpret_cast<T*>(temp + (row * retained + i) * vec_bytes) + part;
-      T* direct = reinterpret_cast<T*>(cache + (row_base + d) * vec_bytes) + part;
-      const T* from = MODE == 0 ? reinterpret_cast<const T*>(cache + (row_base + s) * vec_bytes) + part : tmp;
+      T* direct = reinterpret_cast<T*>(cache + (row_base + d[u]) * vec_bytes) + part;
+      const T* from = MODE == 0 ? reinterpret_cast<const T*>(cache + (row_base + s[u]) * vec_bytes) + part : tmp;
       to[u] = (MODE == 0 && staged) ? tmp : direct;
       if (ok[u]) val[u] = __builtin_nontemporal_load(from);
     }
+    const int64_t next = base + kMoveUnroll * stride;
+    if (next < per_row) load_indices(next);
 #pragma unroll
     for (int u = 0; u < kMoveUnroll; ++u)
       if (ok[u]) __builtin_nontemporal_store(val[u], to[u]);
