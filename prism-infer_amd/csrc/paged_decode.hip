@@ -1362,7 +1362,8 @@ constexpr int kPlanSlotInts = (kPlanInts + 1023) / 1024 * 1024;
 constexpr int kPlanMeasure = kPlanHdrInts + 2 * kPlanSlotInts;
 constexpr int kPlanBuildStamps = kPlanMeasure + 8 * kSMaxWg + 4 * kSMaxWg * kSKv;  // measurement aid: 16 ints
 constexpr int kPlanMergeStamps = kPlanBuildStamps + 16;  // measurement aid: 4 ints per workgroup
-constexpr int kPlanRegionInts = kPlanMergeStamps + 4 * kSMaxWg;
+constexpr int kPlanPrologueStamps = kPlanMergeStamps + 4 * kSMaxWg;  // measurement aid: 4 ints per workgroup
+constexpr int kPlanRegionInts = kPlanPrologueStamps + 4 * kSMaxWg;
 constexpr int kPlanMagic = 0x504C414E;
 static_assert(kPlanKeyBt % 4 == 0 && kPlanHdrInts % 4 == 0 && kPlanSlotInts % 4 == 0, "16-byte key reads");
 constexpr int kPlanThreads = 1024;
@@ -2421,6 +2422,12 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   const unsigned long long w0 = static_cast<unsigned long long>(hdr.x) | (static_cast<unsigned long long>(hdr.y) << 32);
   const unsigned int give_ups = hdr.z;  // plan header int kPlanGiveUps
   int* plan = plan_slot(a, __builtin_amdgcn_readfirstlane(static_cast<int>(w0 & 1)));
+  auto prologue_stamp = [&](int k, unsigned long long dep) {  // measurement aid (bit 32)
+    if ((PRISM_DBG(a) & 32) && threadIdx.x == 0)
+      a.plan_region[kPlanPrologueStamps + 4 * blockIdx.x + k] =
+          static_cast<int>(__builtin_amdgcn_s_memrealtime() & 0x7FFFFFFF) + (dep == 0x1234567ull ? 1 : 0);
+  };
+  prologue_stamp(0, w0);
   // prefix sums go to registers first and to LDS after the key check, so the
   // check's loads leave in the same round
   constexpr int kTs = (kSMaxBatch + kSMaxVirt + 1 + kSThreads - 1) / kSThreads;
@@ -2450,8 +2457,11 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   const bool same =
       (PRISM_DBG(a) & 128) ? true
                            : (!plan_building_here(w0, a.epoch) && plan_key_check<kSThreads>(a, plan, L) && give_ups == 0);
+  prologue_stamp(1, same ? 1 : 0);
   store_tstart();
-  if (__builtin_expect(!__syncthreads_and(same ? 1 : 0), 0)) {
+  const bool all_same = __syncthreads_and(same ? 1 : 0);
+  prologue_stamp(2, all_same ? 1 : 0);
+  if (__builtin_expect(!all_same, 0)) {
     const bool staged = !(PRISM_DBG(a) & 128) && !plan_building_here(w0, a.epoch);  // the check above staged L
     const int slot =
         __builtin_amdgcn_readfirstlane(plan_select_slow<kSThreads>(a, L, tstart, w0, staged, give_ups));
