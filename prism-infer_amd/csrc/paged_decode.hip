@@ -2120,21 +2120,23 @@ __device__ __forceinline__ void stream_column(const DecodeArgs& a, const int* pl
   qhead = h * G + (valid ? qh : 0);
 }
 
-constexpr int kMergeRedOffset = 4096;  // floats: the merge's LDS scratch starts 16 KiB into the stages
-
 // Outputs of a batch of nb merged sequences from the streaming partials, by
 // the whole workgroup.  A unit is (q head, 8 dims): 16 units per head.  When
 // the heads fill fewer units than threads (fewer q heads than 32, as on a
 // tensor-parallel rank), the threads form ng = threads / units slots of
-// `units` threads; the batch's nb <= ng sequences get ng / nb slots each,
-// slot cg of a sequence merging its candidates cg, cg + ng / nb, ..., and a
-// sequence's slots meet in LDS (`red`, 10 floats per thread), so the batch's
-// loads are in flight together.  Otherwise (nb = 1) one slot covers the heads
-// in passes of 32.  The candidates are the (workgroup, token slot) pairs
-// whose workgroups met b's own tiles or its virtual sequence's tiles (one per
-// workgroup: with fewer kv heads the workgroup merged its token slots before
-// writing); their rows follow the layout the streaming kernel writes (real entry e of workgroup w at (w + e) * 8G + slot * G +
-// column; virtual entry v at vrow0 + ((w + v) * 8 + slot) * 16 + column).  A
+// `units` threads and each of the batch's nb <= ng sequences takes one slot,
+// so the batch's loads are in flight together.  Otherwise (nb = 1) one slot
+// covers the heads in passes of 32.  A sequence's candidates are always
+// summed by one slot in candidate order, so its output does not depend on
+// how many sequences the completing workgroup happens to merge at once
+// (splitting a sequence's candidates over the free slots made the rounding,
+// and so the output bits, depend on that count, which timing decides).  The
+// candidates are the (workgroup, token slot) pairs whose workgroups met b's
+// own tiles or its virtual sequence's tiles (one per workgroup: with fewer kv
+// heads the workgroup merged its token slots before writing); their rows
+// follow the layout the streaming kernel writes (real entry e of workgroup w
+// at (w + e) * 8G + slot * G + column; virtual entry v at
+// vrow0 + ((w + v) * 8 + slot) * vcols + column).  A
 // partial with m = -inf attended nothing and weighs 0.  Eight candidates are
 // loaded per round and slot, (m, l) and 32 accumulator bytes each, with a
 // running maximum across rounds; the usual sequence needs one round.  This
@@ -2144,18 +2146,16 @@ constexpr int kMergeRedOffset = 4096;  // floats: the merge's LDS scratch starts
 // record (first, end, virtual slot, virtual first, virtual end), stride 8.
 template <int QDT, int TPR>
 __device__ __forceinline__ void stream_merge_batch(const DecodeArgs& a, int V, const int* recs, int nb,
-                                                   const StreamSplit& sp, float* red, bool stamp = false) {
+                                                   const StreamSplit& sp, bool stamp = false) {
   constexpr int tl = 0;  // one partial per kv head and workgroup entry: the token slots met at the flush
   constexpr int hkv = kSKv / TPR;
   constexpr int kU = 8;
   const int units = a.num_heads * 16;
   const int ng = units >= kSThreads ? 1 : kSThreads / units;  // slots (nb <= ng)
-  const int gpm = ng / nb;                                     // slots per sequence
   const int slot = ng > 1 ? static_cast<int>(threadIdx.x) / units : 0;
   const int u0 = ng > 1 ? static_cast<int>(threadIdx.x) - slot * units : static_cast<int>(threadIdx.x);
-  const int kseq = min(slot / gpm, nb - 1);                    // this slot's sequence in the batch
-  const int cg = slot - kseq * gpm;                            // candidate group within it
-  const bool active = slot < nb * gpm;  // other threads only take part in the barriers
+  const int kseq = min(slot, nb - 1);  // this slot's sequence in the batch
+  const bool active = slot < nb;
   const int* rec = recs + 8 * kseq;
   const int b = rec[0];
   const int first = rec[1], end = rec[2], vslot = rec[3], vfirst = rec[4], vend = rec[5];
@@ -2195,13 +2195,13 @@ __device__ __forceinline__ void stream_merge_batch(const DecodeArgs& a, int V, c
     float o[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) o[j] = 0.f;
-    const int mine = active ? (cnt - cg + gpm - 1) / gpm : 0;  // candidates cg, cg + gpm, ...
+    const int mine = active ? cnt : 0;
     for (int base = 0; base < mine; base += kU) {
       float mv[kU], lv[kU];
       floatx4 x0[kU], x1[kU];
 #pragma unroll
       for (int k = 0; k < kU; ++k) {
-        const int i = min(base + k, mine - 1) * gpm + cg;
+        const int i = min(base + k, mine - 1);
         const int wi = i >> tl;
         const int sl = i & ((1 << tl) - 1);
         const bool second = wi >= cnt0;
@@ -2252,33 +2252,7 @@ __device__ __forceinline__ void stream_merge_batch(const DecodeArgs& a, int V, c
       if ((PRISM_DBG(a) & 32) && stamp && threadIdx.x == 0 && base == 0 && o[7] != 12345.f)  // measurement aid: accumulated
         a.plan_region[kPlanMergeStamps + 4 * blockIdx.x + 2] = static_cast<int>(__builtin_amdgcn_s_memrealtime() & 0x7FFFFFFF);
     }
-    if (gpm > 1) {  // a sequence's slots meet in LDS; its slot 0 finishes the unit
-      __syncthreads();  // `red` is free (the previous batch may still read it)
-      if (active) {
-        float* r = red + 10 * threadIdx.x;
-        r[0] = m_run;
-        r[1] = l_sum;
-#pragma unroll
-        for (int j = 0; j < 8; ++j) r[2 + j] = o[j];
-      }
-      __syncthreads();
-      if (!active || cg != 0) continue;
-      float mx = -INFINITY;
-      for (int k = 0; k < gpm; ++k) mx = fmaxf(mx, red[10 * ((kseq * gpm + k) * units + u0)]);
-      const float m_use = mx == -INFINITY ? 0.f : mx;
-      l_sum = 0.f;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) o[j] = 0.f;
-      for (int k = 0; k < gpm; ++k) {
-        const float* r = red + 10 * ((kseq * gpm + k) * units + u0);
-        const float wgt = exp2f(r[0] - m_use);  // 0 for a slot that attended nothing
-        l_sum += wgt * r[1];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) o[j] += wgt * r[2 + j];
-      }
-    } else if (!active) {
-      continue;
-    }
+    if (!active) continue;
     const float inv = l_sum > 0.f ? 1.f / l_sum : 0.f;
     const int64_t obase = static_cast<int64_t>(b) * a.o_sb + static_cast<int64_t>(hq) * a.o_sh;
     store_out8<QDT>(a, obase + d0 * a.o_sd, o, inv);
@@ -2298,7 +2272,6 @@ __device__ __forceinline__ void stream_finish(const DecodeArgs& a, int* plan, in
   constexpr int kRec = 5;
   int* n_merge = scratch;
   int* merge_rec = scratch + 4;  // per merged sequence: b, then its 5-int plan record (stride 8)
-  static_assert(kMergeRedOffset * 4 + 10 * 4 * kSThreads <= kSStages * kSStage, "merge scratch fits the stages");
   // this wave's partial stores have completed (device scope): the flushes may be counted
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   if (threadIdx.x == 0) *n_merge = 0;
@@ -2352,8 +2325,7 @@ __device__ __forceinline__ void stream_finish(const DecodeArgs& a, int* plan, in
   for (int k = 0; k < nm; k += slots) {
     if ((PRISM_DBG(a) & 32) && k == 0 && threadIdx.x == 0)  // measurement aid: first batch starts
       a.plan_region[kPlanMergeStamps + 4 * blockIdx.x] = static_cast<int>(__builtin_amdgcn_s_memrealtime() & 0x7FFFFFFF);
-    stream_merge_batch<QDT, TPR>(a, V, merge_rec + 8 * k, min(slots, nm - k), sp,
-                                 reinterpret_cast<float*>(scratch) + kMergeRedOffset, k == 0);
+    stream_merge_batch<QDT, TPR>(a, V, merge_rec + 8 * k, min(slots, nm - k), sp, k == 0);
     if ((PRISM_DBG(a) & 32) && k == 0 && threadIdx.x == 0) {  // measurement aid: first batch done
       int* d = a.plan_region + kPlanMeasure + 8 * blockIdx.x;
       d[6] = static_cast<int>(__builtin_amdgcn_s_memrealtime() & 0x7FFFFFFF);
