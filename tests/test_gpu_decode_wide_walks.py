@@ -5,9 +5,10 @@ leading pages once for 32 / G members (two 16-column MFMA blocks per walk);
 with fewer kv heads a walk keeps one block of 16 columns.  These cases put
 groups of 2, 3, 8, 9, 17 and 33 sharers (more than one walk's worth, a
 remainder of one member, which is not a walk, and partial last pages) next to
-private sequences, for G = 1, 2, 4, 8 and 16, and check the streaming kernel
-against ``decode_kernel_semantics`` within the decode tolerance, and that a
-second call on the same plan gives the same bits.
+private sequences, for G = 1, 2, 3, 4, 6, 8 and 16 (with G = 3 and 6 the 32
+columns hold 10 and 5 members and two columns stay empty), and check the
+streaming kernel against ``decode_kernel_semantics`` within the decode
+tolerance, and that a second call on the same plan gives the same bits.
 """
 
 from __future__ import annotations
@@ -60,7 +61,7 @@ def _batch(hkv: int, groups: int, seed: int):
     return q, k, v, ks, vs, tables, lens
 
 
-@pytest.mark.parametrize("hkv,groups", [(8, 1), (8, 2), (8, 4), (8, 8), (8, 16), (4, 4), (2, 8)])
+@pytest.mark.parametrize("hkv,groups", [(8, 1), (8, 2), (8, 3), (8, 4), (8, 6), (8, 8), (8, 16), (4, 4), (2, 8)])
 def test_shared_prefix_groups_on_the_streaming_kernel(hkv, groups):
     require_gpu()
     from prism_infer.ops.paged_decode import paged_decode_attention
