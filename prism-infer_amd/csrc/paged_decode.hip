@@ -1285,11 +1285,13 @@ __device__ __forceinline__ void stream_load_q8(const DecodeArgs& a, int qrow, in
 // pages (a shared read-only prefix) would each stream those pages.  The plan
 // build finds, on the device, groups of sequences with the same first page
 // and, per member, how many leading whole pages it shares with the group's
-// leader (the lowest-numbered member).  Members are packed M = 16 / G at a
-// time into "virtual sequences": a virtual sequence walks the leader's shared
-// pages once with a query operand whose 16 columns are the G query heads of
-// each of its M members, so every shared page is read once per M members
-// instead of once per member, at the same MFMA cost per tile.  A member then
+// leader (the lowest-numbered member).  Members are packed M = vcols / G at
+// a time into "virtual sequences": a virtual sequence walks the leader's
+// shared pages once with a query operand whose vcols columns are the G query
+// heads of each of its M members, so every shared page is read once per M
+// members instead of once per member.  vcols is 32 (two MFMA column blocks
+// computed from one LDS tile) on FP8 tiles of 8 kv heads and 16 (one block)
+// otherwise.  A member then
 // streams only its private tail (the tokens after the shared pages), and the
 // merge combines the partials of its tail with those of its virtual sequence.
 //
@@ -1299,16 +1301,17 @@ __device__ __forceinline__ void stream_load_q8(const DecodeArgs& a, int qrow, in
 //   tstart[NS + 1]      tile prefix sums over the stream order, NS = V + batch:
 //                       virtual sequences first, then the real ones
 //   skip[batch]         tokens a real sequence leaves to its virtual sequence
-//   vslot[batch]        v * 16 + member slot, or -1
+//   vslot[batch]        v * kVMax + member slot, or -1
 //   vsrc[kSMaxVirt]     block-table row (the leader) of virtual sequence v
-//   vmem[kSMaxVirt][16] members of v (-1 = unused slot)
+//   vmem[kSMaxVirt][kVMax] members of v (-1 = unused slot)
 //   vrot[kSMaxVirt]     tile at which virtual sequence v starts its walk (it
 //                       wraps around): the virtual sequences of one group
 //                       start at different pages, so the workgroups reading
 //                       them at the same time do not all hit the same pages
 //
-// Work split: workgroup w streams tiles [w * total / nwg, (w+1) * total / nwg)
-// of the stream; ranges are contiguous and in stream order, so the pair
+// Work split: workgroup w streams the tiles whose cost positions fall in
+// [w * total / nwg, (w+1) * total / nwg) of the stream (cost model below);
+// ranges are contiguous and in stream order, so the pair
 // (workgroup, stream entry) indexes a partial uniquely as w + entry.
 
 constexpr int kSCols = 16;                 // query columns of the MFMA operand
@@ -1436,7 +1439,7 @@ __device__ __forceinline__ int stream_owner_count(int first, int end, int total,
 // workgroups, about 124 tiles each): entry costs of 0 / 1 / 2 / 3 / 4 / 6 / 8
 // / 12 tiles gave 176.0 / 174.9 / 174.5 / 173.6 / 173.6 / 172.2 / 171.9 /
 // 172.6 us, and virtual tiles at 22/16 of a tile 171.1 us (at 13/16: 188 us;
-// a walk of shared pages is followed by merges over its 4 members' outputs).
+// a walk of shared pages is followed by merges over its members' outputs).
 // Before the weights, a workgroup meeting two entries ended its loop 2.6 us
 // after one meeting one, and the last loops ended 7 us after the mean.
 // With two column blocks per virtual walk (a wide walk computes both blocks
@@ -2099,7 +2102,8 @@ __device__ __forceinline__ void stream_seq(const DecodeArgs& a, const int* plan,
 
 // Query column c of wave h (kv head hk = h % Hkv) for stream entry i: real
 // sequence b -> q head hk*G + c (c < G); virtual sequence -> q head hk*G + qh
-// of member m, c = m*G + qh.
+// of member m, c = m*G + qh (c < vcols: the second column block passes
+// c + 16).
 template <int TPR>
 __device__ __forceinline__ void stream_column(const DecodeArgs& a, const int* plan, int V, int i, int h_slot, int c,
                                               int& qrow,
