@@ -2564,13 +2564,13 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   int cleft = min(__builtin_amdgcn_readfirstlane(tstart[b + 1] - tstart[b]) - __builtin_amdgcn_readfirstlane(wr0.y),
                   count);
   using QOp = typename std::conditional<C16, QOperand16, QOperandF8>::type;
-  // Wide virtual sequences (FP8 tiles, 8 kv heads): a virtual entry has two
-  // blocks of 16 query columns (twice the members per walk of the shared
-  // pages); both read the same K and V of each tile from LDS.
-  constexpr bool kWide = TPR == 1 && !C16;
+  // Wide virtual sequences (8 kv heads: FP8 or 16-bit tiles): a virtual
+  // entry has two blocks of 16 query columns (twice the members per walk of
+  // the shared pages); both read the same K and V of each tile from LDS.
+  constexpr bool kWide = TPR == 1;
   const bool wide_call = kWide && a.vcols > kSCols;
   QOp qop;
-  QOperandF8 qop2;  // second column block (wide virtual entries)
+  QOp qop2;  // second column block (wide virtual entries)
   bool colv, colv2;
   bool wide = false;  // the compute side's entry is a wide virtual one (wave-uniform)
   auto load_query = [&]() {
@@ -2582,7 +2582,8 @@ paged_decode_stream_kernel(const DecodeArgs a) {
     if constexpr (kWide) {
       if (wide) {
         stream_column<TPR>(a, plan, V, b, h, c + kSCols, qrow, qhead, colv2);
-        stream_load_q8<QDT, QVEC>(a, qrow, qhead, colv2, g, qop2);
+        if constexpr (C16) stream_load_q16<QDT, QVEC>(a, qrow, qhead, colv2, g, qop2);
+        else stream_load_q8<QDT, QVEC>(a, qrow, qhead, colv2, g, qop2);
       }
     }
   };
@@ -2644,18 +2645,23 @@ paged_decode_stream_kernel(const DecodeArgs a) {
   for (int done = 0; done < count; ++done) {
     // Wait for this tile's loads (the younger tiles' loads may stay in flight),
     // then one barrier: every wave's loads have landed and every wave has
-    // finished the previous tile, whose stage the refill below reuses.
-    static_assert(kSStages == 4 && kS16Stages == 2, "wait counts below assume three (16-bit: one) tiles in flight");
+    // finished the previous tile, whose stage the refill below reuses.  At
+    // this wait the tiles issued are those before done + kStg - 1 (the
+    // prologue issued kStg - 1, each earlier iteration one more after its
+    // barrier), so min(kStg - 2, count - done - 1) younger tiles may be in
+    // flight: two for FP8 tiles, none for 16-bit tiles.  Vector-memory
+    // operations the compiler issued after this tile's loads (partial
+    // stores, query loads) are younger still, so the count can only
+    // over-wait for them.
+    static_assert(kSStages == 4 && kS16Stages == 2, "wait counts below assume four (16-bit: two) stages");
     if constexpr (C16) {
-      if (done + 1 < count) __builtin_amdgcn_s_waitcnt(0xF70 | kS16LoadsPerStage);  // one younger tile in flight
-      else __builtin_amdgcn_s_waitcnt(0xF70);
-    } else if (done + 3 < count) {  // steady state: three younger tiles in flight
-      __builtin_amdgcn_s_waitcnt(0xF70 | (3 * kSLoadsPerStage));
+      __builtin_amdgcn_s_waitcnt(0xF70);
+    } else if (done + 2 < count) {  // steady state: two younger tiles in flight
+      __builtin_amdgcn_s_waitcnt(0xF70 | (2 * kSLoadsPerStage));
+    } else if (done + 1 < count) {
+      __builtin_amdgcn_s_waitcnt(0xF70 | (1 * kSLoadsPerStage));
     } else {
-      const int younger = count - done - 1;
-      if (younger == 2) __builtin_amdgcn_s_waitcnt(0xF70 | (2 * kSLoadsPerStage));
-      else if (younger == 1) __builtin_amdgcn_s_waitcnt(0xF70 | (1 * kSLoadsPerStage));
-      else __builtin_amdgcn_s_waitcnt(0xF70);
+      __builtin_amdgcn_s_waitcnt(0xF70);
     }
     stream_barrier();
     xs_mark(0);
@@ -2673,73 +2679,82 @@ paged_decode_stream_kernel(const DecodeArgs a) {
         uint64_t vt[8];
         lds_read_tr16_x8(v16_off, slot, vt);
         // ---- QK over 16 tokens: the K rows are the MFMA's A operand as they
-        // are (row = token c, k = dims 32g + 8kb ..), the query the B operand
-        floatx4 sc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kb = 0; kb < 4; ++kb) {
-          if constexpr (QDT == PRISM_DTYPE_BF16)
-            sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kw[kb]),
-                                                         __builtin_bit_cast(bf16x8, qop.t[kb]), sc, 0, 0, 0);
-          else
-            sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, kw[kb]),
-                                                        __builtin_bit_cast(f16x8, qop.t[kb]), sc, 0, 0, 0);
-        }
-        float x[4];
-#pragma unroll
-        for (int i = 0; i < 4; ++i) x[i] = sc[i] * qop.colscale;
-        // only a sequence's last tile can reach past its end: masked tokens
-        // get score -inf and zero V elements (rows past the end may hold NaN)
-        if (nv < kTTok) {
+        // are (row = token c, k = dims 32g + 8kb ..), the query the B operand.
+        // Only a sequence's last tile can reach past its end: masked tokens
+        // get score -inf and zero V elements (rows past the end may hold NaN).
+        const bool partial = nv < kTTok;
+        bool tv[4] = {true, true, true, true};
+        if (partial) {
           uint64_t keep = 0;
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const bool tv = tok_lane + i < nv;
-            x[i] = tv ? x[i] : -INFINITY;
-            keep |= tv ? (uint64_t{0xFFFF} << (16 * i)) : 0;
+            tv[i] = tok_lane + i < nv;
+            keep |= tv[i] ? (uint64_t{0xFFFF} << (16 * i)) : 0;
           }
 #pragma unroll
           for (int nt = 0; nt < 8; ++nt) vt[nt] &= keep;
         }
-        float tmax = nan_max(nan_max(x[0], x[1]), nan_max(x[2], x[3]));
-        tmax = wave_maximum_across_groups(tmax);
-        const bool raise = tmax > m_run + kSRescaleThreshold;
-        if (__builtin_amdgcn_ballot_w64(raise) != 0) {  // wave-uniform branch
-          const float m_new = raise ? tmax : m_run;
-          const float alpha = raise ? __builtin_amdgcn_exp2f(m_run - m_new) : 1.f;
-          m_run = m_new;
-          l_run *= alpha;
+        // one block of 16 query columns: scores, online softmax, PV
+        auto column_block16 = [&](const QOperand16& qo, floatx4 (&ac)[8], float& mr, float& lr) {
+          floatx4 sc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int kb = 0; kb < 4; ++kb) {
+            if constexpr (QDT == PRISM_DTYPE_BF16)
+              sc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, kw[kb]),
+                                                           __builtin_bit_cast(bf16x8, qo.t[kb]), sc, 0, 0, 0);
+            else
+              sc = __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, kw[kb]),
+                                                          __builtin_bit_cast(f16x8, qo.t[kb]), sc, 0, 0, 0);
+          }
+          float x[4];
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            const float ai = __shfl(alpha, 4 * g + i);
-#pragma unroll
-            for (int j = 0; j < 8; ++j) acc[j][i] *= ai;
+            x[i] = sc[i] * qo.colscale;
+            if (partial) x[i] = tv[i] ? x[i] : -INFINITY;
           }
-        }
-        const float m_use = (m_run == -INFINITY) ? 0.f : m_run;
-        float pv[4];
+          float tmax = nan_max(nan_max(x[0], x[1]), nan_max(x[2], x[3]));
+          tmax = wave_maximum_across_groups(tmax);
+          const bool raise = tmax > mr + kSRescaleThreshold;
+          if (__builtin_amdgcn_ballot_w64(raise) != 0) {  // wave-uniform branch
+            const float m_new = raise ? tmax : mr;
+            const float alpha = raise ? __builtin_amdgcn_exp2f(mr - m_new) : 1.f;
+            mr = m_new;
+            lr *= alpha;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          pv[i] = __builtin_amdgcn_exp2f(x[i] - m_use);  // 0 for masked tokens
-          l_run += pv[i];
-        }
-        // ---- PV: P (A operand, k = tokens 4g .. 4g + 3) in the cache's
-        // 16-bit type, V N-tile nt from the transposed read (B operand)
-        if constexpr (QDT == PRISM_DTYPE_BF16) {
-          const shortx4 pa = {__builtin_bit_cast(short, static_cast<__bf16>(pv[0])),
-                              __builtin_bit_cast(short, static_cast<__bf16>(pv[1])),
-                              __builtin_bit_cast(short, static_cast<__bf16>(pv[2])),
-                              __builtin_bit_cast(short, static_cast<__bf16>(pv[3]))};
+            for (int i = 0; i < 4; ++i) {
+              const float ai = __shfl(alpha, 4 * g + i);
 #pragma unroll
-          for (int nt = 0; nt < 8; ++nt)
-            acc[nt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, __builtin_bit_cast(shortx4, vt[nt]), acc[nt], 0,
-                                                                0, 0);
-        } else {
-          const f16x4 pa = {static_cast<_Float16>(pv[0]), static_cast<_Float16>(pv[1]), static_cast<_Float16>(pv[2]),
-                            static_cast<_Float16>(pv[3])};
+              for (int j = 0; j < 8; ++j) ac[j][i] *= ai;
+            }
+          }
+          const float m_use = (mr == -INFINITY) ? 0.f : mr;
+          float pv[4];
 #pragma unroll
-          for (int nt = 0; nt < 8; ++nt)
-            acc[nt] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(f16x4, vt[nt]), acc[nt], 0, 0, 0);
-        }
+          for (int i = 0; i < 4; ++i) {
+            pv[i] = __builtin_amdgcn_exp2f(x[i] - m_use);  // 0 for masked tokens
+            lr += pv[i];
+          }
+          // ---- PV: P (A operand, k = tokens 4g .. 4g + 3) in the cache's
+          // 16-bit type, V N-tile nt from the transposed read (B operand)
+          if constexpr (QDT == PRISM_DTYPE_BF16) {
+            const shortx4 pa = {__builtin_bit_cast(short, static_cast<__bf16>(pv[0])),
+                                __builtin_bit_cast(short, static_cast<__bf16>(pv[1])),
+                                __builtin_bit_cast(short, static_cast<__bf16>(pv[2])),
+                                __builtin_bit_cast(short, static_cast<__bf16>(pv[3]))};
+#pragma unroll
+            for (int nt = 0; nt < 8; ++nt)
+              ac[nt] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pa, __builtin_bit_cast(shortx4, vt[nt]), ac[nt], 0,
+                                                                 0, 0);
+          } else {
+            const f16x4 pa = {static_cast<_Float16>(pv[0]), static_cast<_Float16>(pv[1]),
+                              static_cast<_Float16>(pv[2]), static_cast<_Float16>(pv[3])};
+#pragma unroll
+            for (int nt = 0; nt < 8; ++nt)
+              ac[nt] = __builtin_amdgcn_mfma_f32_16x16x16f16(pa, __builtin_bit_cast(f16x4, vt[nt]), ac[nt], 0, 0, 0);
+          }
+        };
+        column_block16(qop, acc, m_run, l_run);
+        if (wide) column_block16(qop2, acc2, m_run2, l_run2);
       }
     } else if (nv != 0 && !(PRISM_DBG(a) & 1)) {
       const uint32_t slot = static_cast<uint32_t>(cstage) * kSStage;
@@ -3224,8 +3239,8 @@ Geometry geometry(int batch, int num_heads, int num_kv_heads, int head_dim, int 
     // workspace: shared-page plan, then partial rows of the real sequences
     // and of the virtual ones
     geo.stream_nwg = device_cu_count() * kSWgPerCu;
-    // FP8 tiles of 8 kv heads walk shared pages for two column blocks at once
-    geo.stream_vcols = (cache_dtype == PRISM_DTYPE_FP8_E4M3FN && num_kv_heads == kSKv) ? kVMax : kSCols;
+    // tiles of 8 kv heads (FP8 or 16-bit) walk shared pages for two column blocks at once
+    geo.stream_vcols = num_kv_heads == kSKv ? kVMax : kSCols;
     const int members = geo.stream_vcols / (num_heads / num_kv_heads);
     const int64_t vmax = (batch <= kSShareMaxBatch && members >= 2) ? std::min(kSMaxVirt, batch / 2) : 0;
     // real rows: (wg + V + b) * 8G (one set of G per head slot); virtual

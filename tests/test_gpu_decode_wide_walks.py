@@ -1,6 +1,7 @@
 """GPU parity: virtual walks of shared pages with two query-column blocks.
 
-On FP8 tiles of 8 kv heads the streaming kernel walks a group's shared
+On tiles of 8 kv heads (scaled FP8, or a bf16/f16 cache of the query's
+dtype) the streaming kernel walks a group's shared
 leading pages once for 32 / G members (two 16-column MFMA blocks per walk);
 with fewer kv heads a walk keeps one block of 16 columns.  These cases put
 groups of 2, 3, 8, 9, 17 and 33 sharers (more than one walk's worth, a
@@ -37,7 +38,7 @@ def _quantize(src):
     return k, s
 
 
-def _batch(hkv: int, groups: int, seed: int):
+def _batch(hkv: int, groups: int, seed: int, dtype=None):
     g = torch.Generator().manual_seed(20261202 + 97 * hkv + groups + seed)
     page, width, d = 64, 12, 128
     private = 16
@@ -55,7 +56,11 @@ def _batch(hkv: int, groups: int, seed: int):
         # some members end inside the shared prefix, one exactly at its end
         lens[members[1]] = shared * page
         lens[members[-1]] = max(1, shared * page - int(torch.randint(1, page, (1,), generator=g)))
-    q = torch.randn(batch, hkv * groups, d, generator=g).to(torch.bfloat16)
+    q = torch.randn(batch, hkv * groups, d, generator=g).to(dtype or torch.bfloat16)
+    if dtype is not None:  # a 16-bit cache of the query's dtype, no scales
+        k = torch.randn(pool, page, hkv, d, generator=g).to(dtype)
+        v = torch.randn(pool, page, hkv, d, generator=g).to(dtype)
+        return q, k, v, None, None, tables, lens
     k, ks = _quantize(torch.randn(pool, page, hkv, d, generator=g).to(torch.bfloat16))
     v, vs = _quantize(torch.randn(pool, page, hkv, d, generator=g).to(torch.bfloat16))
     return q, k, v, ks, vs, tables, lens
@@ -79,6 +84,29 @@ def test_shared_prefix_groups_on_the_streaming_kernel(hkv, groups):
     set_decode_overrides(path="stream")
     first = paged_decode_attention(*args, **kw)
     again = paged_decode_attention(*args, **kw)
+    torch.cuda.synchronize()
+    assert_decode_close(first, want, label=label)
+    assert torch.equal(first, again), f"{label}: a second call on the same plan differs"
+
+
+@pytest.mark.parametrize("groups,dtype", [(1, torch.bfloat16), (4, torch.bfloat16), (16, torch.bfloat16),
+                                          (3, torch.float16)])
+def test_shared_prefix_groups_on_16bit_tiles(groups, dtype):
+    """The same groups over a 16-bit cache (two-block walks of 16-bit tiles)."""
+
+    require_gpu()
+    from prism_infer.ops.paged_decode import paged_decode_attention
+
+    q, k, v, _, _, tables, lens = _batch(8, groups, 1, dtype)
+    scale = 128 ** -0.5
+    want = oracle.decode_kernel_semantics(q, k, v, tables, lens, scale, compute_dtype=torch.float32)
+    dev = torch.device("cuda")
+    args = (q.to(dev), k.to(dev), v.to(dev), tables.to(dev), lens.to(dev), scale)
+    label = f"B={q.shape[0]} Hq={q.shape[1]} Hkv=8 G={groups} {dtype} groups {GROUP_SIZES}"
+    print(label, flush=True)
+    set_decode_overrides(path="stream")
+    first = paged_decode_attention(*args)
+    again = paged_decode_attention(*args)
     torch.cuda.synchronize()
     assert_decode_close(first, want, label=label)
     assert torch.equal(first, again), f"{label}: a second call on the same plan differs"
