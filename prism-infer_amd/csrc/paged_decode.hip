@@ -2882,46 +2882,62 @@ paged_decode_stream_kernel(const DecodeArgs a) {
         // write one partial per kv head and entry.  LDS-only barriers: the
         // younger tiles' loads stay in flight.
         constexpr int kHk = kSKv / TPR;
-        constexpr int kState = kSCols * kHeadDim + 2 * kSCols;  // floats of one wave's state
+        // One wave's state: its 64 lanes' accumulators as rows of eight
+        // 16-byte chunks (chunk j = acc[j], XOR-swizzled by lane so that eight
+        // consecutive lanes hit distinct banks), then the 16 columns' running
+        // max and sum.  Writer and reader lanes of the same (g, c) meet, so
+        // each side moves its 32 values with eight b128 accesses.
+        constexpr int kAccFloats = 64 * 8 * 4;
+        constexpr int kState = kAccFloats + 2 * kSCols;  // floats of one wave's state
         static_assert(kSKv / 2 * kState * 4 <= kSStage, "half the waves' states fit one stage");
         float* buf = reinterpret_cast<float*>(stages + cdone * kSStage);
         const int sub = h / kHk;
         const int hk = h - sub * kHk;
+        const int swz = lane & 7;
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         stream_barrier();  // every wave is done reading the stage
 #pragma unroll
         for (int span = TPR / 2; span >= 1; span /= 2) {
           if (sub >= span && sub < 2 * span) {
             float* st = buf + ((sub - span) * kHk + hk) * kState;
+            floatx4* rowp = reinterpret_cast<floatx4*>(st) + lane * 8;
 #pragma unroll
-            for (int i = 0; i < 4; ++i)
-#pragma unroll
-              for (int j = 0; j < 8; ++j) st[(4 * g + i) * kHeadDim + c + 16 * j] = acc[j][i];
+            for (int j = 0; j < 8; ++j) rowp[j ^ swz] = acc[j];
             if (g == 0) {
-              st[kSCols * kHeadDim + c] = m_run;
-              st[kSCols * kHeadDim + kSCols + c] = l_tot;
+              st[kAccFloats + c] = m_run;
+              st[kAccFloats + kSCols + c] = l_tot;
             }
           }
           asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
           stream_barrier();
           if (sub < span) {
             const float* st = buf + (sub * kHk + hk) * kState;
-            const float pm = st[kSCols * kHeadDim + c];
-            const float pl = st[kSCols * kHeadDim + kSCols + c];
+            const floatx4* rowp = reinterpret_cast<const floatx4*>(st) + lane * 8;
+            floatx4 other[8];
+#pragma unroll
+            for (int j = 0; j < 8; ++j) other[j] = rowp[j ^ swz];
+            const float pm = st[kAccFloats + c];
+            const float pl = st[kAccFloats + kSCols + c];
+            // (v_exp_f32: one weight of each pair is exp2(0) = 1, and a
+            // weight flushed below 2^-126 is nothing next to it)
             const float mx = fmaxf(m_run, pm);
             const float mu = mx == -INFINITY ? 0.f : mx;
-            l_tot = l_tot * exp2f(m_run - mu) + pl * exp2f(pm - mu);  // exp2(-inf) = 0
+            l_tot = l_tot * __builtin_amdgcn_exp2f(m_run - mu) + pl * __builtin_amdgcn_exp2f(pm - mu);
+            float ao[4], ap[4];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               const int qr = 4 * g + i;
               const float mo = __shfl(m_run, qr);
-              const float mp = st[kSCols * kHeadDim + qr];
+              const float mp = st[kAccFloats + qr];
               const float mxi = fmaxf(mo, mp);
               const float mui = mxi == -INFINITY ? 0.f : mxi;
-              const float ao = exp2f(mo - mui), ap = exp2f(mp - mui);
-#pragma unroll
-              for (int j = 0; j < 8; ++j) acc[j][i] = acc[j][i] * ao + st[qr * kHeadDim + c + 16 * j] * ap;
+              ao[i] = __builtin_amdgcn_exp2f(mo - mui);
+              ap[i] = __builtin_amdgcn_exp2f(mp - mui);
             }
+#pragma unroll
+            for (int j = 0; j < 8; ++j)
+#pragma unroll
+              for (int i = 0; i < 4; ++i) acc[j][i] = acc[j][i] * ao[i] + other[j][i] * ap[i];
             m_run = mx;
           }
           asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
