@@ -2877,10 +2877,15 @@ paged_decode_stream_kernel(const DecodeArgs a) {
       if constexpr (TPR > 1) {
         // With fewer kv heads a row holds TPR tokens per head and the waves
         // h, h + Hkv, ... hold token slots of the same kv head: their states
-        // meet (tree of log2 TPR levels) in the stage just consumed, which no
-        // load refills before the next barrier, so the head slots below Hkv
-        // write one partial per kv head and entry.  LDS-only barriers: the
-        // younger tiles' loads stay in flight.
+        // meet in LDS and one partial per kv head and entry is written.
+        // * The range's last flush: no load is in flight, so every stage is
+        //   free and all eight states fit at once; after one barrier wave
+        //   (sub, hk) combines the TPR slots of kv head hk for its 8 / TPR of
+        //   the accumulator chunks and writes them.
+        // * Earlier flushes (the younger tiles' loads stay in flight): a tree
+        //   of log2 TPR levels in the stage just consumed, which no load
+        //   refills before the next barrier; LDS-only barriers; the head
+        //   slots below Hkv then write the merged state.
         constexpr int kHk = kSKv / TPR;
         // One wave's state: its 64 lanes' accumulators as rows of eight
         // 16-byte chunks (chunk j = acc[j], XOR-swizzled by lane so that eight
@@ -2890,58 +2895,131 @@ paged_decode_stream_kernel(const DecodeArgs a) {
         constexpr int kAccFloats = 64 * 8 * 4;
         constexpr int kState = kAccFloats + 2 * kSCols;  // floats of one wave's state
         static_assert(kSKv / 2 * kState * 4 <= kSStage, "half the waves' states fit one stage");
+        static_assert(kSKv * kState * 4 <= kSStages * kSStage, "all the waves' states fit the stages");
         float* buf = reinterpret_cast<float*>(stages + cdone * kSStage);
         const int sub = h / kHk;
         const int hk = h - sub * kHk;
         const int swz = lane & 7;
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
         stream_barrier();  // every wave is done reading the stage
+        if (!more) {
+          float* mine = reinterpret_cast<float*>(stages) + h * kState;
+          floatx4* rowp = reinterpret_cast<floatx4*>(mine) + lane * 8;
 #pragma unroll
-        for (int span = TPR / 2; span >= 1; span /= 2) {
-          if (sub >= span && sub < 2 * span) {
-            float* st = buf + ((sub - span) * kHk + hk) * kState;
-            floatx4* rowp = reinterpret_cast<floatx4*>(st) + lane * 8;
-#pragma unroll
-            for (int j = 0; j < 8; ++j) rowp[j ^ swz] = acc[j];
-            if (g == 0) {
-              st[kAccFloats + c] = m_run;
-              st[kAccFloats + kSCols + c] = l_tot;
-            }
+          for (int j = 0; j < 8; ++j) rowp[j ^ swz] = acc[j];
+          if (g == 0) {
+            mine[kAccFloats + c] = m_run;
+            mine[kAccFloats + kSCols + c] = l_tot;
           }
           asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
           stream_barrier();
-          if (sub < span) {
-            const float* st = buf + (sub * kHk + hk) * kState;
-            const floatx4* rowp = reinterpret_cast<const floatx4*>(st) + lane * 8;
-            floatx4 other[8];
+          // slot s of kv head hk is wave s * kHk + hk; this lane's columns
+          // are 4g .. 4g + 3, its dims c + 16 j for the chunks j it combines
+          constexpr int kJ = 8 / TPR;
+          floatx4 ms[TPR], ls[TPR];
 #pragma unroll
-            for (int j = 0; j < 8; ++j) other[j] = rowp[j ^ swz];
-            const float pm = st[kAccFloats + c];
-            const float pl = st[kAccFloats + kSCols + c];
-            // (v_exp_f32: one weight of each pair is exp2(0) = 1, and a
-            // weight flushed below 2^-126 is nothing next to it)
-            const float mx = fmaxf(m_run, pm);
-            const float mu = mx == -INFINITY ? 0.f : mx;
-            l_tot = l_tot * __builtin_amdgcn_exp2f(m_run - mu) + pl * __builtin_amdgcn_exp2f(pm - mu);
-            float ao[4], ap[4];
+          for (int sl = 0; sl < TPR; ++sl) {
+            const float* st = reinterpret_cast<const float*>(stages) + (sl * kHk + hk) * kState;
+            ms[sl] = *reinterpret_cast<const floatx4*>(st + kAccFloats + 4 * g);
+            ls[sl] = *reinterpret_cast<const floatx4*>(st + kAccFloats + kSCols + 4 * g);
+          }
+          floatx4 mx = ms[0];
+#pragma unroll
+          for (int sl = 1; sl < TPR; ++sl)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) mx[i] = fmaxf(mx[i], ms[sl][i]);
+          floatx4 wt[TPR];
+          floatx4 lsum = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const float mu = mx[i] == -INFINITY ? 0.f : mx[i];
+#pragma unroll
+            for (int sl = 0; sl < TPR; ++sl) {
+              // (v_exp_f32: the largest slot weighs exp2(0) = 1, and a weight
+              // flushed below 2^-126 is nothing next to it)
+              wt[sl][i] = __builtin_amdgcn_exp2f(ms[sl][i] - mu);
+              lsum[i] += wt[sl][i] * ls[sl][i];
+            }
+          }
+          const bool virt = b < V;
+          const int ncols = virt ? kSCols : a.groups;
+          const int64_t row0 = virt ? a.vrow0 + ((static_cast<int64_t>(blockIdx.x) + b) * kSKv + hk) * a.vcols
+                                    : (static_cast<int64_t>(blockIdx.x) + b) * (kSKv * a.groups) + hk * a.groups;
+#pragma unroll
+          for (int jj = 0; jj < kJ; ++jj) {
+            const int j = sub * kJ + jj;
+            floatx4 o = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int sl = 0; sl < TPR; ++sl) {
+              const floatx4 x = reinterpret_cast<const floatx4*>(stages)[((sl * kHk + hk) * kState) / 4 + lane * 8 +
+                                                                         (j ^ swz)];
+#pragma unroll
+              for (int i = 0; i < 4; ++i) o[i] += wt[sl][i] * x[i];
+            }
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               const int qr = 4 * g + i;
-              const float mo = __shfl(m_run, qr);
-              const float mp = st[kAccFloats + qr];
-              const float mxi = fmaxf(mo, mp);
-              const float mui = mxi == -INFINITY ? 0.f : mxi;
-              ao[i] = __builtin_amdgcn_exp2f(mo - mui);
-              ap[i] = __builtin_amdgcn_exp2f(mp - mui);
+              if (qr < ncols) store_coherent(a.part_acc + (row0 + qr) * kHeadDim + c + 16 * j, o[i]);
             }
-#pragma unroll
-            for (int j = 0; j < 8; ++j)
-#pragma unroll
-              for (int i = 0; i < 4; ++i) acc[j][i] = acc[j][i] * ao[i] + other[j][i] * ap[i];
-            m_run = mx;
           }
-          asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-          stream_barrier();  // the next level reuses the buffer
+          if (sub == 0 && c == 0) {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const int qr = 4 * g + i;
+              if (qr < ncols) {
+                store_coherent(a.part_ml + (row0 + qr) * 2 + 0, mx[i]);
+                store_coherent(a.part_ml + (row0 + qr) * 2 + 1, lsum[i]);
+              }
+            }
+          }
+        } else {
+#pragma unroll
+          for (int span = TPR / 2; span >= 1; span /= 2) {
+            if (sub >= span && sub < 2 * span) {
+              float* st = buf + ((sub - span) * kHk + hk) * kState;
+              floatx4* rowp = reinterpret_cast<floatx4*>(st) + lane * 8;
+#pragma unroll
+              for (int j = 0; j < 8; ++j) rowp[j ^ swz] = acc[j];
+              if (g == 0) {
+                st[kAccFloats + c] = m_run;
+                st[kAccFloats + kSCols + c] = l_tot;
+              }
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            stream_barrier();
+            if (sub < span) {
+              const float* st = buf + (sub * kHk + hk) * kState;
+              const floatx4* rowp = reinterpret_cast<const floatx4*>(st) + lane * 8;
+              floatx4 other[8];
+#pragma unroll
+              for (int j = 0; j < 8; ++j) other[j] = rowp[j ^ swz];
+              const float pm = st[kAccFloats + c];
+              const float pl = st[kAccFloats + kSCols + c];
+              // (v_exp_f32: one weight of each pair is exp2(0) = 1, and a
+              // weight flushed below 2^-126 is nothing next to it)
+              const float mx = fmaxf(m_run, pm);
+              const float mu = mx == -INFINITY ? 0.f : mx;
+              l_tot = l_tot * __builtin_amdgcn_exp2f(m_run - mu) + pl * __builtin_amdgcn_exp2f(pm - mu);
+              float ao[4], ap[4];
+#pragma unroll
+              for (int i = 0; i < 4; ++i) {
+                const int qr = 4 * g + i;
+                const float mo = __shfl(m_run, qr);
+                const float mp = st[kAccFloats + qr];
+                const float mxi = fmaxf(mo, mp);
+                const float mui = mxi == -INFINITY ? 0.f : mxi;
+                ao[i] = __builtin_amdgcn_exp2f(mo - mui);
+                ap[i] = __builtin_amdgcn_exp2f(mp - mui);
+              }
+#pragma unroll
+              for (int j = 0; j < 8; ++j)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) acc[j][i] = acc[j][i] * ao[i] + other[j][i] * ap[i];
+              m_run = mx;
+            }
+            asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+            stream_barrier();  // the next level reuses the buffer
+          }
         }
       }
       // partial rows: real entry b at (wg + b) * 8G + slot * G + column; virtual entry v
@@ -2969,7 +3047,7 @@ paged_decode_stream_kernel(const DecodeArgs a) {
           }
         }
       };
-      flush_block(acc, m_run, l_tot, row0);
+      if (TPR == 1 || more) flush_block(acc, m_run, l_tot, row0);
       if constexpr (kWide) {
         if (wide) {
           float l_tot2 = l_run2 + __shfl_xor(l_run2, 16);
