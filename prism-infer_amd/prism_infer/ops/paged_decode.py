@@ -9,8 +9,10 @@ kernel semantics (:83-180):
   [num_blocks, block_size, num_kv_heads];
 - block_tables: int32 [>= batch, max_blocks]; block ids < 0 are skipped;
 - context_lens: int32 [>= batch]; max_context_len: int32 scalar tensor read on
-  the device (graph replay follows updated values); derived with
-  ``context_lens.max()`` on the device when omitted;
+  the device (graph replay follows updated values).  When it is omitted the
+  reference derives ``context_lens.max()``, a bound no sequence's own length
+  exceeds, so it clips nothing; a cached "no bound" scalar (2^31 - 1) gives
+  the same attended tokens without the reduction launch;
 - a sequence with no attended token returns zeros.
 
 ``block_n`` is validated as in the reference (positive power of two) but the
@@ -230,6 +232,30 @@ def _launch_paged_decode_attention(q, k_cache, v_cache, block_tables, context_le
     return output
 
 
+_NO_BOUND: dict = {}
+
+
+def _no_context_bound(context_lens: torch.Tensor) -> torch.Tensor:
+    """The omitted ``max_context_len``: min(ctx[b], max(context_lens)) is
+    ctx[b] for every sequence, so a scalar that bounds nothing attends the
+    same tokens as the reference's ``context_lens.max()`` (`paged_decode.py:458-461`)
+    and needs no reduction kernel per call.  Cached per device; while a graph
+    is being captured and no scalar is cached yet, the reduction is captured
+    instead (no allocation from the graph's pool is kept)."""
+
+    if context_lens.numel() == 0:
+        return context_lens.max()  # raises torch's error for an empty reduction, as the reference does
+    dev = context_lens.device
+    cached = _NO_BOUND.get(dev)
+    if cached is not None:
+        return cached
+    if dev.type == "cuda" and torch.cuda.is_current_stream_capturing():
+        return context_lens.max()
+    cached = torch.full((1,), 2**31 - 1, dtype=torch.int32, device=dev)
+    _NO_BOUND[dev] = cached
+    return cached
+
+
 def paged_decode_attention(
     q: torch.Tensor,
     k_cache: torch.Tensor,
@@ -246,8 +272,7 @@ def paged_decode_attention(
     """Single-query paged attention over (scaled-)FP8 or 16/32-bit KV pages."""
 
     if max_context_len is None:
-        # Device-side scalar; no host synchronisation.
-        max_context_len = context_lens.max()
+        max_context_len = _no_context_bound(context_lens)
     scaled_kv = _validate_paged_decode_inputs(
         q, k_cache, v_cache, block_tables, context_lens, max_context_len,
         k_scale_cache=k_scale_cache, v_scale_cache=v_scale_cache, block_n=block_n,

@@ -158,6 +158,20 @@ def test_decode_has_no_cpu_fallback():
         paged_decode_attention(q, k, v, tables, lens, 0.3, k_scale_cache=ks, v_scale_cache=vs)
 
 
+def test_omitted_max_context_len_bounds_nothing():
+    """The omitted bound: the reference's context_lens.max() is at least every
+    sequence's length, so it never clips; the cached scalar bounds nothing
+    either, is int32 of one element on the lengths' device, and is reused."""
+
+    lens = torch.tensor([0, 7, 4096, 3], dtype=torch.int32)
+    bound = paged_decode._no_context_bound(lens)
+    assert bound.dtype == torch.int32 and bound.numel() == 1 and bound.device == lens.device
+    assert int(bound) == 2**31 - 1 and int(bound) >= int(lens.max())
+    assert paged_decode._no_context_bound(lens[:2]) is bound
+    with pytest.raises(RuntimeError):  # torch's empty-reduction error, as in the reference
+        paged_decode._no_context_bound(lens[:0])
+
+
 def test_compaction_contract_and_cpu_branch():
     cache = torch.zeros(2, 1, 16, 2, 8, dtype=FP8)
     src = torch.tensor([1, 2])
