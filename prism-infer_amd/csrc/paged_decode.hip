@@ -3326,8 +3326,20 @@ Geometry geometry(int batch, int num_heads, int num_kv_heads, int head_dim, int 
                      batch <= kSMaxBatch && !stream_disabled() &&
                      device_cu_count() * kSWgPerCu <= kSMaxWg;
   if (geo.stream_shape && forced_path() != 2) {
+    // Automatic choice, from the table's capacity in tiles (the lengths live
+    // on the device).  The streaming kernel spreads each sequence over about
+    // nwg / batch workgroups, whose partials one workgroup then merges, so
+    // few sequences favour the per-split kernel even with many tiles.
+    // Measured (8 kv heads, scaled FP8 / bf16, cold, 8 layers back to back;
+    // stream against split, us): B = 2, 16k and 32k tokens 61 / 35 and 70 /
+    // 52; B = 4, 8k / 16k / 32k: 43 / 35, 52 / 52, 72 / 80; B = 8, 2k / 4k
+    // / 8k: 29 / 24, 34 / 35, 43 / 52; B = 16 x 1k, 32 x 512, 64 x 256 (4
+    // tiles per workgroup): 23 / 24, 21 / 26, 20 / 21.
     const int64_t cap_tiles = static_cast<int64_t>(batch) * ceil_div(static_cast<int64_t>(width) * page_size, ttok);
-    if (cap_tiles < 8LL * device_cu_count() * kSWgPerCu) geo.stream_shape = false;
+    const int64_t nwg = static_cast<int64_t>(device_cu_count()) * kSWgPerCu;
+    const bool enough = (batch >= 16 && cap_tiles >= 4 * nwg) || (batch >= 8 && cap_tiles >= 8 * nwg) ||
+                        (batch >= 4 && cap_tiles >= 32 * nwg);
+    if (!enough) geo.stream_shape = false;
   }
   if (geo.stream_shape) {
     // workspace: shared-page plan, then partial rows of the real sequences
