@@ -3217,9 +3217,10 @@ struct Geometry {
 };
 
 // PRISM_DECODE_PATH=split|stream forces a kernel family (tests, A/B runs);
-// unset, the streaming kernel is used when the batch offers enough tiles to
-// keep every workgroup busy and the per-split kernel otherwise (lower latency
-// for one or a few short sequences).
+// unset, the streaming kernel is used when the table's capacity gives enough
+// tiles for the batch size (geometry()) and the per-split kernel otherwise
+// (lower latency for a few sequences, whose streaming partials one workgroup
+// per sequence would merge).
 // Kernel-family overrides: PRISM_DECODE_PATH (split|stream), PRISM_DECODE_SPLIT
 // (tokens per split) and PRISM_DECODE_SHARE=0 (no shared-page analysis) are
 // read from the environment once, on the first decode call of the process;
