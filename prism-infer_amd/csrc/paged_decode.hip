@@ -3271,8 +3271,15 @@ bool fast_geometry(int num_heads, int num_kv_heads, int head_dim, int cache_dtyp
 }
 
 // Tokens per chunk of the split-K path (a multiple of 8 tiles, one per
-// wave): aim for about two workgroups per CU over batch x kv heads x chunks,
-// with at least one tile per wave and at most kSplitMaxChunks chunks.
+// wave): aim for about one workgroup per CU over batch x kv heads x chunks,
+// with at least one tile per wave and at most kSplitMaxChunks chunks.  Fewer,
+// longer chunks than two per CU: each wave keeps its tiles' loads in flight
+// back to back and the merge reads half the partials.  Measured (8 kv heads,
+// cold, 8 layers back to back, scaled FP8 / bf16 us, two per CU -> one): B = 1
+// x 32k 37.8 -> 32.3 / 44.9 -> 40.6, B = 2 x 16k 35.5 -> 31.3, B = 4 x 16k
+// 52.0 -> 46.3, B = 8 x 2k 24.6 -> 23.7 / 31.2 -> 27.1; shapes whose chunk
+// count was already bound by one tile per wave (B = 1 x 1800, B = 4 x 1k)
+// are unchanged.
 int choose_split(int batch, int num_kv_heads, int page_size, int width) {
   constexpr int64_t kChunkTok = static_cast<int64_t>(kSplitWaves) * kTile;
   {
@@ -3281,7 +3288,7 @@ int choose_split(int batch, int num_kv_heads, int page_size, int width) {
   }
   const int64_t cap = static_cast<int64_t>(width) * page_size;
   const int64_t slots = std::max<int64_t>(1, static_cast<int64_t>(batch) * num_kv_heads);
-  const int64_t target = static_cast<int64_t>(device_cu_count()) * 2;
+  const int64_t target = static_cast<int64_t>(device_cu_count());
   int64_t chunks = ceil_div(target, slots);
   chunks = std::min<int64_t>(chunks, std::min<int64_t>(kSplitMaxChunks, std::max<int64_t>(1, ceil_div(cap, kChunkTok))));
   if (chunks < 1) chunks = 1;
@@ -3331,14 +3338,14 @@ Geometry geometry(int batch, int num_heads, int num_kv_heads, int head_dim, int 
     // on the device).  The streaming kernel spreads each sequence over about
     // nwg / batch workgroups, whose partials one workgroup then merges, so
     // few sequences favour the per-split kernel even with many tiles.
-    // Measured (8 kv heads, scaled FP8 / bf16, cold, 8 layers back to back;
-    // stream against split, us): B = 2, 16k and 32k tokens 61 / 35 and 70 /
-    // 52; B = 4, 8k / 16k / 32k: 43 / 35, 52 / 52, 72 / 80; B = 8, 2k / 4k
-    // / 8k: 29 / 24, 34 / 35, 43 / 52; B = 16 x 1k, 32 x 512, 64 x 256 (4
-    // tiles per workgroup): 23 / 24, 21 / 26, 20 / 21.
+    // Measured (8 kv heads, scaled FP8, cold, 8 layers back to back; stream
+    // against split, us): B = 2 x 32k 71 / 46; B = 4 x 8k / 16k / 32k / 64k
+    // 44 / 31, 52 / 46, 74 / 75, 111 / 133; B = 8 x 2k / 4k / 8k / 16k 29 /
+    // 24, 33 / 31, 44 / 46, 62 / 76; B = 16 x 1k / 2k 23 / 23, 29 / 31; B =
+    // 32 x 512 22 / 20, B = 64 x 256 20 / 21, B = 128 x 256 26 / 35.
     const int64_t cap_tiles = static_cast<int64_t>(batch) * ceil_div(static_cast<int64_t>(width) * page_size, ttok);
     const int64_t nwg = static_cast<int64_t>(device_cu_count()) * kSWgPerCu;
-    const bool enough = (batch >= 16 && cap_tiles >= 4 * nwg) || (batch >= 8 && cap_tiles >= 8 * nwg) ||
+    const bool enough = (batch >= 16 && cap_tiles >= 4 * nwg) || (batch >= 8 && cap_tiles >= 16 * nwg) ||
                         (batch >= 4 && cap_tiles >= 32 * nwg);
     if (!enough) geo.stream_shape = false;
   }

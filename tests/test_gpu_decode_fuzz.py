@@ -189,13 +189,13 @@ def test_fewer_kv_heads_streaming(hkv, hq, monkeypatch):
 
 
 @pytest.mark.parametrize("batch,ctx,family", [(1, 1800, 1), (2, 16384, 1), (2, 32768, 1), (4, 8192, 1),
-                                              (4, 16384, 1), (4, 32768, 2), (8, 2048, 1), (8, 4096, 2),
-                                              (16, 512, 1), (16, 1024, 2), (32, 512, 2), (64, 256, 2),
-                                              (64, 16384, 2)])
+                                              (4, 16384, 1), (4, 32768, 2), (8, 2048, 1), (8, 4096, 1),
+                                              (8, 8192, 2), (16, 512, 1), (16, 1024, 2), (32, 512, 2),
+                                              (64, 256, 2), (64, 16384, 2)])
 def test_family_choice_by_batch_and_capacity(batch, ctx, family):
     """The automatic family on a 256-CU MI355X (8 kv heads, 256-token pages,
     scaled FP8): the streaming kernel needs enough tiles for the batch (4 per
-    workgroup from 16 sequences, 8 from 8, 32 from 4), the per-split kernel
+    workgroup from 16 sequences, 16 from 8, 32 from 4), the per-split kernel
     takes the rest; both give the decode semantics, so this pins speed only."""
 
     require_gpu()
